@@ -1,0 +1,306 @@
+"""Benchmark of zentorch's quantized-linear hot path on one MI355X.
+
+Prints ONE JSON line.  The headline workload is BASELINE config 0: a single
+zentorch_woq_linear, bf16 activations [M=4, K=4096], int4 symmetric weights
+[N=4096, K=4096] packed 8 per int32, bf16 group-128 scales, bf16 output.
+A "step" is one call of the op.  ``value`` is algorithmic HBM bytes per call
+(N*K/2 + G*N*2 + M*K*2 + M*N*2) divided by the time per call, with the calls
+replayed back to back from a HIP graph over 64 rotating weight copies
+(> 512 MB, so the 256 MB Infinity Cache cannot hold them).  Inputs are
+resident in HBM before timing starts.
+
+Secondary workloads in the same line (``workloads``): the Llama-3-8B decode
+layer at M in {1, 8, 16, 64} (config 2), dynamic int8 qlinear at M=128
+(config 1) and the M=2048 prefill layer through both paths (config 3).
+
+``roofline`` is for the dominant kernel of the headline workload (the decode
+GEMV): average kernel duration from HIP events around each launch on the
+stream the op launches on.  ``cpu_baseline`` times the CPU oracle (a port of
+the reference's semantics; zentorch itself cannot be built offline) on a
+bounded sample of the same workload on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "zendnn-pytorch-plugin_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5033.0   # dense, 256 CU x 2.4 GHz x 8192 ops/clk/CU
+BF16_PEAK_TFLOPS = 2517.0
+ROTATE_BYTES = 600 << 20  # weight bytes rotated through per timed pass
+
+
+def woq_bytes(M, N, K, G, n_bin=0, bias=False):
+    return N * K // 2 + G * N * 2 + M * K * 2 + M * N * 2 + n_bin * M * N * 2 + (N * 2 if bias else 0)
+
+
+def dyn_bytes(M, N, K):
+    return N * K + N * 4 + N * 2 + M * K * 2 + M * N * 2
+
+
+class WoqLinear:
+    """One int4 WOQ linear with its weight, scales and fused epilogue."""
+
+    def __init__(self, M, N, K, gs=128, post=None, copies=1, gen=None, dev="cuda"):
+        G = K // gs
+        self.M, self.N, self.K, self.G, self.post = M, N, K, G, post
+        g = gen
+        self.x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+        self.w, self.s = [], []
+        for _ in range(copies):
+            q = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int8).to(dev)
+            wp = torch.ops.zentorch.zentorch_woq_repack_weight(q)  # [N, K/8]
+            self.w.append(wp.t())  # the op's [K/8, N] view
+            self.s.append((torch.rand(G, N, generator=g) * 0.015 + 0.005).bfloat16().to(dev))
+        self.extra = None
+        if post in ("silu_mul", "add"):
+            self.extra = torch.randn(M, N, generator=g).bfloat16().to(dev)
+
+    def bytes(self):
+        return woq_bytes(self.M, self.N, self.K, self.G, n_bin=1 if self.extra is not None else 0)
+
+    def __call__(self, i=0):
+        ops = torch.ops.zentorch
+        w, s = self.w[i % len(self.w)], self.s[i % len(self.s)]
+        if self.post == "silu_mul":
+            return ops.zentorch_woq_linear_silu_mul(self.x, w, s, None, self.extra)
+        if self.post == "add":
+            return ops.zentorch_woq_linear_add(self.x, w, s, None, self.extra)
+        return ops.zentorch_woq_linear(self.x, w, s, None)
+
+
+class DynLinear:
+    def __init__(self, M, N, K, copies=1, gen=None, dev="cuda"):
+        g = gen
+        self.M, self.N, self.K = M, N, K
+        self.x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+        self.w, self.sw = [], []
+        for _ in range(copies):
+            self.w.append(torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev))
+            self.sw.append((torch.rand(N, generator=g) * 0.009 + 0.001).to(dev))
+        self.b = (torch.randn(N, generator=g) * 0.1).bfloat16().to(dev)
+
+    def bytes(self):
+        return dyn_bytes(self.M, self.N, self.K)
+
+    def __call__(self, i=0):
+        j = i % len(self.w)
+        return torch.ops.zentorch.zentorch_dynamic_qlinear(self.x, self.w[j], self.sw[j], self.b)
+
+
+def graph_time(calls, reps, warmup):
+    """Seconds per pass over `calls`, replayed from a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(max(warmup, 1)):
+            for c in calls:
+                c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    for _ in range(max(warmup, 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3 / reps
+
+
+def kernel_time(call, n, warmup=3):
+    """Average seconds of one op call measured by HIP events placed directly
+    around each launch on the launching stream (no other work in between)."""
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record()
+        call(i)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in ev)
+    return sum(ts) / len(ts) / 1e3, ts[len(ts) // 2] / 1e3
+
+
+def copies_for(bytes_per_copy):
+    return max(1, min(64, -(-ROTATE_BYTES // bytes_per_copy)))
+
+
+def bench_config0(args, gen):
+    M, N, K = 4, 4096, 4096
+    per = N * K // 2 + (K // 128) * N * 2
+    lin = WoqLinear(M, N, K, copies=copies_for(per), gen=gen)
+    calls = [lambda i=i: lin(i) for i in range(len(lin.w))]
+    reps = max(1, args.steps // len(calls))
+    t_step = graph_time(calls, reps, args.warmup) / len(calls)
+    k_avg, k_med = kernel_time(lin, max(64, len(calls)))
+    b = lin.bytes()
+    return {"M": M, "N": N, "K": K, "G": K // 128, "bytes_per_call": b,
+            "s_per_call": t_step, "GBps": b / t_step / 1e9,
+            "kernel_avg_s": k_avg, "kernel_med_s": k_med, "kernel_GBps": b / k_avg / 1e9,
+            "copies": len(lin.w), "calls_timed": reps * len(calls)}
+
+
+LLAMA = [("qkv", 6144, 4096, None), ("o", 4096, 4096, None),
+         ("gate_up", 14336, 4096, "silu_mul"), ("down", 4096, 14336, "add")]
+
+
+def bench_decode_layer(M, args, gen):
+    # gate_up is modelled as its gate half [14336 x 4096] with the up half's
+    # product as the silu_mul multiplier, so the weight bytes per layer equal
+    # the fused [28672 x 4096] gate_up's half; both halves are timed by running
+    # the gate_up linear twice (once per half), as a merged-weight kernel would
+    # stream both halves.
+    layer = []
+    for name, N, K, post in LLAMA:
+        reps = 2 if name == "gate_up" else 1
+        for _ in range(reps):
+            layer.append(WoqLinear(M, N, K, post=post, copies=1, gen=gen))
+    per_layer = sum(l.N * l.K // 2 + l.G * l.N * 2 for l in layer)
+    ncopy = max(1, -(-ROTATE_BYTES // per_layer))
+    layers = [layer] + [[WoqLinear(M, l.N, l.K, post=l.post, copies=1, gen=gen) for l in layer]
+                        for _ in range(ncopy - 1)]
+    calls = [lambda l=l: l() for lay in layers for l in lay]
+    reps = max(1, args.steps // len(calls) + 1)
+    t_pass = graph_time(calls, reps, args.warmup)
+    b = sum(l.bytes() for lay in layers for l in lay)
+    t_layer = t_pass / len(layers)
+    return {"M": M, "layer_bytes": b // len(layers), "s_per_layer": t_layer,
+            "GBps": b / t_pass / 1e9, "layer_copies": len(layers)}
+
+
+def bench_dyn(M, shapes, args, gen):
+    lins = []
+    for N, K in shapes:
+        per = N * K
+        lins.append(DynLinear(M, N, K, copies=1 if M >= 1024 else copies_for(per) // len(shapes) or 1,
+                              gen=gen))
+    calls = [lambda l=l, i=i: l(i) for l in lins for i in range(len(l.w))]
+    reps = max(1, args.steps // len(calls) + 1)
+    t = graph_time(calls, reps, args.warmup)
+    ops = sum(2 * l.M * l.N * l.K * len(l.w) for l in lins)
+    b = sum(l.bytes() * len(l.w) for l in lins)
+    return {"M": M, "shapes": shapes, "s_per_pass": t, "TOPS": ops / t / 1e12,
+            "frac_int8_peak": ops / t / 1e12 / INT8_PEAK_TOPS, "GBps": b / t / 1e9,
+            "frac_hbm": b / t / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_woq_prefill(args, gen):
+    M = 2048
+    lins = []
+    for name, N, K, post in LLAMA:
+        lins.append(WoqLinear(M, N if name != "gate_up" else 2 * N, K, post=None, gen=gen))
+    calls = [lambda l=l: l() for l in lins]
+    reps = max(1, args.steps // len(calls) + 1)
+    t = graph_time(calls, reps, args.warmup)
+    flops = sum(2 * l.M * l.N * l.K for l in lins)
+    return {"M": M, "s_per_layer": t, "TFLOPS": flops / t / 1e12,
+            "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS}
+
+
+def cpu_baseline(budget_s=12.0):
+    """CPU oracle (port of the reference semantics) on config 0's shape."""
+    from oracle import oracle as O
+    g = torch.Generator().manual_seed(0)
+    M, N, K = 4, 4096, 4096
+    x = torch.randn(M, K, generator=g).bfloat16()
+    q = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int8)
+    wp = O.woq_repack_weight(q)
+    s = (torch.rand(K // 128, N, generator=g) * 0.015 + 0.005).bfloat16()
+    threads = O.max_threads()
+    for _ in range(3):
+        O.woq_linear(x, wp, s)
+    n, t0 = 0, time.perf_counter()
+    times = []
+    while time.perf_counter() - t0 < budget_s and n < 200:
+        a = time.perf_counter_ns()
+        O.woq_linear(x, wp, s)
+        times.append((time.perf_counter_ns() - a) / 1e9)
+        n += 1
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": woq_bytes(M, N, K, K // 128) / med / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle/zt_oracle.c zto_woq_linear on config 0 (M=4,N=K=4096,G=32), "
+                      f"median of {n} calls after 3 warm-up, {threads} OpenMP threads, "
+                      f"same algorithmic-bytes formula"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=640)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default=None,
+                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+    import zentorch  # noqa: F401  (loads the HIP ops; fails loudly if not built)
+
+    torch.manual_seed(0)
+    gen = torch.Generator().manual_seed(0)
+    with torch.inference_mode():
+        only = args.only
+        res = {}
+        if only in (None, "config0"):
+            res["config0"] = bench_config0(args, gen)
+        if only in (None, "decode"):
+            res["decode_layer"] = [bench_decode_layer(M, args, gen) for M in (1, 8, 16, 64)]
+        if only in (None, "dyn128"):
+            res["dyn_qlinear_m128"] = bench_dyn(128, [(11008, 4096)], args, gen)
+        if only in (None, "prefill_int8"):
+            res["prefill_int8_m2048"] = bench_dyn(
+                2048, [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)], args, gen)
+        if only in (None, "prefill_int4"):
+            res["prefill_int4_m2048"] = bench_woq_prefill(args, gen)
+
+    c0 = res.get("config0")
+    line = {
+        "metric": "int4 WOQ linear HBM GB/s (%peak) at M<=16; int8 qlinear TOPS (%MFMA peak)",
+        "value": round(c0["GBps"], 2) if c0 else None,
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": c0["calls_timed"] if c0 else args.steps, "warmup": args.warmup,
+        "ms_per_step": round(c0["s_per_call"] * 1e3, 6) if c0 else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 x int4 (bf16 MFMA, fp32 accumulate)", "data": "synthetic",
+        "config": {"workload": "BASELINE config 0: zentorch_woq_linear M=4 N=K=4096 int4 "
+                               "group-128 bf16 scales, 64 rotating weight copies, HIP graph",
+                   "global_batch": 4, "seq_len": 1, "parallelism": "single GPU"},
+    }
+    if c0:
+        line["roofline"] = {"bound": "hbm", "achieved": round(c0["kernel_GBps"], 2),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(c0["kernel_GBps"] / HBM_PEAK_GBS, 4),
+                            "traffic": None,
+                            "kernel": "woq_decode_kernel", "kernel_avg_us": round(c0["kernel_avg_s"] * 1e6, 3),
+                            "algorithmic_bytes": c0["bytes_per_call"]}
+    if not args.no_cpu_baseline and only in (None, "config0"):
+        line["cpu_baseline"] = cpu_baseline()
+    line["workloads"] = res
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,170 @@
+/*
+ * zentorch_hip.h -- C-ABI of libzentorch_hip.so, the gfx950 kernels behind
+ * zentorch's quantized-linear ops.
+ *
+ * Plain pointers, sizes and a HIP stream; no torch types.  Every pointer is a
+ * device pointer unless stated otherwise.  All entry points are asynchronous
+ * on `stream`, allocate nothing, are thread-safe, and return 0 on success or
+ * a ZT_E* code; zt_last_error_string() gives the message of the calling
+ * thread's last failure.
+ *
+ * The reference calls ZenDNNL's C++ matmul_direct from its ATen ops; each
+ * entry point below names the reference code it stands in for (paths are
+ * relative to the amd/ZenDNN-pytorch-plugin checkout).
+ */
+#ifndef ZENTORCH_HIP_H
+#define ZENTORCH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A hipStream_t (0 = the null stream). */
+typedef struct ihipStream_t *zt_stream_t;
+
+/* Element types (src/cpu/cpp/Memory.hpp:20-44 maps the same torch dtypes). */
+enum zt_dtype {
+  ZT_DT_NONE = -1,
+  ZT_DT_F32 = 0,
+  ZT_DT_BF16 = 1,
+  ZT_DT_F16 = 2,
+  ZT_DT_S8 = 3,
+  ZT_DT_U8 = 4,
+  ZT_DT_S32 = 5
+};
+
+/* Post-op ids with the reference's numbering (src/cpu/cpp/Utils.hpp:56-71):
+ * unary ops act on the running value, MUL/ADD combine it with the next
+ * buffer, applied in list order (src/cpu/cpp/MatmulUtils.hpp:36-77). */
+enum zt_post_op {
+  ZT_PO_NONE = 0,
+  ZT_PO_RELU = 1,
+  ZT_PO_GELU_TANH = 2,
+  ZT_PO_GELU_ERF = 3,
+  ZT_PO_SILU = 4,
+  ZT_PO_SIGMOID = 5,
+  ZT_PO_TANH = 6,
+  ZT_PO_MUL = 7,
+  ZT_PO_ADD = 8
+};
+
+enum zt_status {
+  ZT_OK = 0,
+  ZT_EINVAL = 1,     /* bad argument (shape, dtype, null pointer) */
+  ZT_EUNSUPPORTED = 2, /* valid request this build does not implement */
+  ZT_EHIP = 3        /* a HIP runtime call failed */
+};
+
+#define ZT_MAX_POST_OPS 4
+
+/* Fused epilogue: up to ZT_MAX_POST_OPS ops.  Binary buffers are [M, ld]
+ * (row m at buf + m*ld elements) in bf16 or fp32. */
+typedef struct zt_post_ops {
+  int32_t count;
+  int32_t ids[ZT_MAX_POST_OPS];
+  const void *bufs[ZT_MAX_POST_OPS]; /* i-th binary op uses bufs[i-th binary] */
+  int32_t buf_dtypes[ZT_MAX_POST_OPS];
+  int64_t buf_ld[ZT_MAX_POST_OPS];
+} zt_post_ops;
+
+/*
+ * int4 weight-only linear: y = post(x . dequant(W)^T + bias).
+ *
+ * Replaces zentorch_woq_linear_impl's matmul_direct call
+ * (src/cpu/cpp/WOQ_Linear.cpp:14-112, call at :103-108) and, through the
+ * post-op list, the _relu/_sigmoid/_gelu_tanh/_gelu_erf/_add/_mul_add/_add_add
+ * wrappers (:178-292, registered :435-512).
+ *
+ *  x        [M, ldx] bf16 or fp32 activations (K used columns)
+ *  w_packed [N, K/8] int32, row-major: the storage of the op's [K/8, N]
+ *           transposed weight view; nibble i of word (n, c) is element
+ *           (n, 8c+i), LSB first (WOQ_Linear.cpp:345-350)
+ *  scales   [G, N] bf16 or fp32 (G = 1: per channel; K % G == 0)
+ *  zp       [G, N] or NULL.  NULL: signed int4 (s4).  Otherwise unsigned
+ *           int4 (u4, WOQ_Linear.cpp:47-49): a bf16/fp32 zp is the tinygemm
+ *           float zero point, w = (u-8)*s + z; an s8/s32 zp gives w = (u-zp)*s
+ *  bias     [N] bf16/fp32 or NULL
+ *  y        [M, ldy] in y_dtype (bf16 or fp32)
+ */
+int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                  int64_t ldx, const int32_t *w_packed, int64_t N,
+                  const void *scales, int32_t scales_dtype, int64_t G,
+                  const void *zp, int32_t zp_dtype, const void *bias,
+                  int32_t bias_dtype, const zt_post_ops *post, void *y,
+                  int32_t y_dtype, int64_t ldy, void *workspace,
+                  size_t workspace_bytes, zt_stream_t stream);
+
+/* Bytes of device workspace zt_woq_linear needs for these sizes (0 when the
+ * chosen kernel needs none).  The first 4096 bytes hold tile counters that
+ * must be zero before the first call; every completed call leaves them zero
+ * again, so a workspace is zeroed once and then reused.  Calls that overlap
+ * in time must not share a workspace. */
+size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
+                                    int64_t G);
+
+/*
+ * Dynamic int8 linear: per-token symmetric s8 quantisation of x inside the
+ * op, int8 x int8 -> int32 GEMM, y = acc * sx[m] * sw[n] + bias[n].
+ *
+ * Replaces zentorch_dynamic_qlinear_impl's matmul_direct(dynamic_quant)
+ * (src/cpu/cpp/DynamicQLinear.cpp:74-135, call at :124-129).
+ *
+ *  x        [M, K] bf16 or fp32, contiguous (DynamicQLinear.cpp:160-162)
+ *  w        [N, K] int8 row-major (transB=true, ldb=K, :124-126)
+ *  w_scales [N] fp32 or bf16 per output channel
+ *  bias     [N] fp32/bf16 or NULL
+ *  post     NULL for the reference op (it has no post-ops,
+ *           docs/zentorch_dynamic_qlinear.md:99); non-NULL is an extension
+ *  y        [M, N] in y_dtype
+ *  workspace: zt_dynamic_qlinear_workspace_size(M, K) bytes
+ */
+int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                       const int8_t *w, int64_t N, const void *w_scales,
+                       int32_t w_scales_dtype, const void *bias,
+                       int32_t bias_dtype, const zt_post_ops *post, void *y,
+                       int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                       zt_stream_t stream);
+
+size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K);
+
+/*
+ * The quantisation stage of zt_dynamic_qlinear on its own (same kernel):
+ * qx[M, K] int8 and sx[M] fp32, sx = max(amax_k|x|, 1e-12)/127,
+ * qx = clamp(round_half_even(x/sx), -128, 127).  Exposes what ZenDNNL
+ * computes inside matmul_direct (DynamicQLinear.cpp:100-110) so it can be
+ * checked bit for bit.
+ */
+int zt_dynamic_quantize(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                        int8_t *qx, float *sx, zt_stream_t stream);
+
+/*
+ * The GEMM stage of zt_dynamic_qlinear on its own (same kernels, int32
+ * epilogue): acc[M, N] = qa[M, K] . w[N, K]^T exactly in int32.
+ */
+int zt_s8s8s32_gemm(const int8_t *qa, const int8_t *w, int64_t M, int64_t N,
+                    int64_t K, int32_t *acc, zt_stream_t stream);
+
+/* Repack int8 [N, K] int4 values into int32 [N, K/8] on the GPU.
+ * Replaces zentorch_woq_repack_weight (src/cpu/cpp/WOQ_Linear.cpp:294-357). */
+int zt_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out,
+                         zt_stream_t stream);
+
+/* torch CPU int4pack uint8 [N, K/2] -> int32 [N, K/8] on the GPU.
+ * Replaces zentorch_woq_repack_from_int4pack (WOQ_Linear.cpp:361-433). */
+int zt_woq_repack_from_int4pack(const uint8_t *packed, int64_t N, int64_t K,
+                                int32_t *out, zt_stream_t stream);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char *zt_last_error_string(void);
+
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int32_t zt_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZENTORCH_HIP_H */

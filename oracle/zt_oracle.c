@@ -1,0 +1,351 @@
+/*
+ * zt_oracle.c -- CPU restatement of zentorch's quantized-linear semantics.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP kernels in
+ * zendnn-pytorch-plugin_amd/csrc.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it; the product path never calls it
+ * (the torch ops have no CPU kernel and fail loudly without the HIP library).
+ *
+ * What each function restates (paths relative to the reference checkout):
+ *   zto_woq_repack_weight   src/cpu/cpp/WOQ_Linear.cpp:294-357 (LSB-first, 8
+ *                           nibbles per int32, order_map is the identity :326)
+ *   zto_unpack_int4pack     src/cpu/cpp/WOQ_Linear.cpp:361-428 (torch CPU
+ *                           int4pack, BLOCK_N=64, 16x4 interleave)
+ *   zto_woq_linear          src/cpu/cpp/WOQ_Linear.cpp:14-176 (matmul_direct
+ *                           with s4/u4 weights, [G,N] scales, optional zp),
+ *                           post-ops in list order MatmulUtils.hpp:36-77,
+ *                           post-op ids Utils.hpp:56-71.  Numerics follow the
+ *                           reference's own test reference
+ *                           test/unittests/op_tests/test_woq_linear.py:118-128:
+ *                           dequantised weight rounded to the input dtype,
+ *                           fp32 accumulation, one rounding of the output.
+ *   zto_dynamic_quantize    test/unittests/op_tests/test_dynamic_qlinear.py:32-36
+ *                           and DynamicQLinear.cpp:94-110: per-token symmetric
+ *                           s8, scale = max(amax,1e-12)/127 (fp32 IEEE divide),
+ *                           q = clamp(round_half_even(x/scale), -128, 127).
+ *   zto_s8s8s32_gemm        exact int32 accumulation of DynamicQLinear.cpp:124-129
+ *                           (compute=s8, transB=true, ldb=K).
+ *   zto_dynamic_qlinear     DynamicQLinear.cpp:74-181: y = acc*sx[m]*sw[n] + b[n]
+ *                           in fp32, rounded once to the output dtype.
+ *
+ * Where the reference leaves numerics to ZenDNNL (accumulation order, the
+ * rounding of the dequantised weight, the u4 zero-point convention) the
+ * choice made here is stated at the function.  Compiled with
+ * -ffp-contract=off so a*b+c is always two roundings.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* dtype codes shared with include/zentorch_hip.h */
+enum { ZT_DT_NONE = -1, ZT_DT_F32 = 0, ZT_DT_BF16 = 1, ZT_DT_F16 = 2,
+       ZT_DT_S8 = 3, ZT_DT_U8 = 4, ZT_DT_S32 = 5 };
+/* post-op ids: same numbering as the reference's UNARY_POST_OP/BINARY_POST_OP
+ * (src/cpu/cpp/Utils.hpp:56-71) */
+enum { PO_NONE = 0, PO_RELU = 1, PO_GELU_TANH = 2, PO_GELU_ERF = 3,
+       PO_SILU = 4, PO_SIGMOID = 5, PO_TANH = 6, PO_MUL = 7, PO_ADD = 8 };
+
+#define ZTO_OK 0
+#define ZTO_EINVAL 1
+
+static inline float bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* IEEE round-to-nearest-even fp32 -> bf16; NaN stays NaN (quiet). */
+static inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline float round_to_dtype(float v, int dt) {
+  if (dt == ZT_DT_BF16) return bf16_to_f32(f32_to_bf16(v));
+  return v;
+}
+
+static inline float load_f(const void *p, int dt, int64_t i) {
+  switch (dt) {
+  case ZT_DT_F32: return ((const float *)p)[i];
+  case ZT_DT_BF16: return bf16_to_f32(((const uint16_t *)p)[i]);
+  case ZT_DT_S8: return (float)((const int8_t *)p)[i];
+  case ZT_DT_U8: return (float)((const uint8_t *)p)[i];
+  case ZT_DT_S32: return (float)((const int32_t *)p)[i];
+  default: return 0.f;
+  }
+}
+
+static inline void store_f(void *p, int dt, int64_t i, float v) {
+  if (dt == ZT_DT_F32) ((float *)p)[i] = v;
+  else ((uint16_t *)p)[i] = f32_to_bf16(v);
+}
+
+static inline float unary(int id, float v) {
+  switch (id) {
+  case PO_RELU: return v > 0.f ? v : 0.f;
+  case PO_GELU_TANH: {
+    const float k0 = 0.7978845608028654f; /* sqrt(2/pi) */
+    return 0.5f * v * (1.f + tanhf(k0 * (v + 0.044715f * v * v * v)));
+  }
+  case PO_GELU_ERF: return 0.5f * v * (1.f + erff(v * 0.7071067811865476f));
+  case PO_SILU: return v / (1.f + expf(-v));
+  case PO_SIGMOID: return 1.f / (1.f + expf(-v));
+  case PO_TANH: return tanhf(v);
+  default: return v;
+  }
+}
+
+/* Post-ops are applied in list order; a binary op consumes the next buffer
+ * (MatmulUtils.hpp:62-76).  Buffers are [M, ld] in their own dtype. */
+static inline float apply_post_ops(float v, int n_post, const int *ids,
+                                   const void *const *bufs, const int *dts,
+                                   const int64_t *lds, int64_t m, int64_t n) {
+  int b = 0;
+  for (int i = 0; i < n_post; ++i) {
+    int id = ids[i];
+    if (id == PO_ADD || id == PO_MUL) {
+      float o = load_f(bufs[b], dts[b], m * lds[b] + n);
+      ++b;
+      v = (id == PO_ADD) ? v + o : v * o;
+    } else {
+      v = unary(id, v);
+    }
+  }
+  return v;
+}
+
+static void set_threads(int nthreads) {
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+}
+
+int zto_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------ A1 */
+/* WOQ_Linear.cpp:294-357: word[n][c] = sum_i (w[n][8c+i] & 0xF) << 4i. */
+int zto_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out) {
+  if (K < 8 || K % 8 != 0 || N < 0) return ZTO_EINVAL;
+  const int64_t KW = K / 8;
+  for (int64_t n = 0; n < N; ++n) {
+    const int8_t *src = w + n * K;
+    for (int64_t c = 0; c < KW; ++c) {
+      uint32_t word = 0;
+      for (int i = 0; i < 8; ++i)
+        word |= ((uint32_t)(uint8_t)src[8 * c + i] & 0xFu) << (4 * i);
+      out[n * KW + c] = (int32_t)word;
+    }
+  }
+  return ZTO_OK;
+}
+
+/* ------------------------------------------------------------------ A2 */
+/* WOQ_Linear.cpp:361-428.  packed: uint8 [N, K/2] in torch's CPU int4pack
+ * layout; out: int8 [N, K] holding the unsigned nibble (0..15). */
+int zto_unpack_int4pack(const uint8_t *packed, int64_t N, int64_t K,
+                        int8_t *out) {
+  const int BLOCK_N = 64;
+  if (N % BLOCK_N != 0 || K % 2 != 0) return ZTO_EINVAL;
+  for (int64_t nb = 0; nb < N / BLOCK_N; ++nb) {
+    const uint8_t *src = packed + nb * K * BLOCK_N / 2;
+    int8_t *dst = out + nb * BLOCK_N * K;
+    for (int64_t k = 0; k < K; ++k) {
+      for (int d = 0; d < 16; ++d) {
+        uint8_t p02 = src[k * 32 + d];
+        uint8_t p13 = src[k * 32 + 16 + d];
+        dst[(d + 0) * K + k] = (int8_t)(p02 & 0xF);
+        dst[(d + 16) * K + k] = (int8_t)(p13 & 0xF);
+        dst[(d + 32) * K + k] = (int8_t)((p02 >> 4) & 0xF);
+        dst[(d + 48) * K + k] = (int8_t)((p13 >> 4) & 0xF);
+      }
+    }
+  }
+  return ZTO_OK;
+}
+
+/* ------------------------------------------------------------- A3-A5 */
+/* Dequantised weight element (n, k):
+ *   no zero points (s4, WOQ_Linear.cpp:47-49): q = signed nibble, w = q*s
+ *   floating zero points (u4): tinygemm convention w = (u-8)*s + z, the
+ *     convention of aten._weight_int4pack_mm_for_cpu that the reference's
+ *     asymmetric test compares against (test_woq_linear_asymmetric.py:28-42)
+ *   integer zero points (u4): w = (u - zp)*s
+ * then rounded to the compute (= input) dtype, as the reference test does
+ * with dq_weight.to(bfloat16) (test_woq_linear.py:121,127). */
+static inline float woq_dequant(uint32_t nib, float s, const void *zp,
+                                int zp_dt, int64_t zidx, int compute_dt) {
+  float w;
+  if (!zp) {
+    int q = (int)(nib ^ 8u) - 8; /* sign-extend 4 bits */
+    w = (float)q * s;
+  } else if (zp_dt == ZT_DT_F32 || zp_dt == ZT_DT_BF16) {
+    float z = load_f(zp, zp_dt, zidx);
+    w = (float)((int)nib - 8) * s;
+    w = w + z;
+  } else {
+    float z = load_f(zp, zp_dt, zidx);
+    w = ((float)nib - z) * s;
+  }
+  return round_to_dtype(w, compute_dt);
+}
+
+/* x: [M, ldx] in x_dt (bf16/fp32); wpk: [N, K/8] int32 (the storage of the
+ * [K/8, N] transposed view the op receives); scales/zp: [G, N]; bias: [N];
+ * y: [M, ldy] in y_dt.  Accumulates each output in fp32, k ascending. */
+int zto_woq_linear(const void *x, int x_dt, int64_t M, int64_t K, int64_t ldx,
+                   const int32_t *wpk, int64_t N, const void *scales, int s_dt,
+                   int64_t G, const void *zp, int zp_dt, const void *bias,
+                   int b_dt, int n_post, const int *post_ids,
+                   const void *const *post_bufs, const int *post_dts,
+                   const int64_t *post_lds, void *y, int y_dt, int64_t ldy,
+                   int nthreads) {
+  if (K % 8 != 0 || G <= 0 || K % G != 0) return ZTO_EINVAL;
+  const int64_t KW = K / 8, gs = K / G;
+  set_threads(nthreads);
+  int err = 0;
+#pragma omp parallel
+  {
+    const int NB = 16;
+    float *wdq = (float *)malloc(sizeof(float) * (size_t)K * NB);
+    float *xr = (float *)malloc(sizeof(float) * (size_t)K);
+    if (!wdq || !xr) {
+#pragma omp atomic write
+      err = 1;
+    } else {
+#pragma omp for schedule(static)
+      for (int64_t n0 = 0; n0 < N; n0 += NB) {
+        const int nb = (int)((N - n0) < NB ? (N - n0) : NB);
+        /* dequantise a [K, nb] block, k-major so the inner loop runs over n */
+        for (int j = 0; j < nb; ++j) {
+          const int64_t n = n0 + j;
+          for (int64_t c = 0; c < KW; ++c) {
+            uint32_t word = (uint32_t)wpk[n * KW + c];
+            for (int i = 0; i < 8; ++i) {
+              int64_t k = 8 * c + i;
+              int64_t sidx = (k / gs) * N + n;
+              float s = load_f(scales, s_dt, sidx);
+              wdq[k * NB + j] = woq_dequant((word >> (4 * i)) & 0xFu, s, zp,
+                                            zp_dt, sidx, x_dt);
+            }
+          }
+        }
+        for (int64_t m = 0; m < M; ++m) {
+          float acc[16];
+          for (int j = 0; j < NB; ++j) acc[j] = 0.f;
+          for (int64_t k = 0; k < K; ++k) xr[k] = load_f(x, x_dt, m * ldx + k);
+          for (int64_t k = 0; k < K; ++k) {
+            const float xv = xr[k];
+            const float *wr = wdq + k * NB;
+            for (int j = 0; j < NB; ++j) acc[j] += xv * wr[j];
+          }
+          for (int j = 0; j < nb; ++j) {
+            const int64_t n = n0 + j;
+            float v = acc[j];
+            if (bias) v = v + load_f(bias, b_dt, n);
+            v = apply_post_ops(v, n_post, post_ids, post_bufs, post_dts,
+                               post_lds, m, n);
+            store_f(y, y_dt, m * ldy + n, v);
+          }
+        }
+      }
+    }
+    free(wdq);
+    free(xr);
+  }
+  return err ? ZTO_EINVAL : ZTO_OK;
+}
+
+/* ------------------------------------------------------------------ A6 */
+/* Per-token symmetric s8 quantisation.  All arithmetic in fp32 after the
+ * exact bf16->fp32 widening:
+ *   amax = max_k |x[m,k]|; sx = max(amax, 1e-12f) / 127.0f  (IEEE divide)
+ *   q = clamp(rint(x / sx), -128, 127)   (rint: round half to even) */
+int zto_dynamic_quantize(const void *x, int x_dt, int64_t M, int64_t K,
+                         int8_t *qx, float *sx, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    float amax = 0.f;
+    for (int64_t k = 0; k < K; ++k) {
+      float v = fabsf(load_f(x, x_dt, m * K + k));
+      amax = v > amax ? v : amax;
+    }
+    if (!(amax >= 1e-12f)) amax = 1e-12f;
+    const float s = amax / 127.0f;
+    sx[m] = s;
+    for (int64_t k = 0; k < K; ++k) {
+      float r = rintf(load_f(x, x_dt, m * K + k) / s);
+      r = r < -128.f ? -128.f : (r > 127.f ? 127.f : r);
+      qx[m * K + k] = (int8_t)r;
+    }
+  }
+  return ZTO_OK;
+}
+
+/* acc[m,n] = sum_k qa[m,k] * w[n,k], exact in int32 (w is [N,K] row-major,
+ * the transB=true / ldb=K layout of DynamicQLinear.cpp:124-126). */
+int zto_s8s8s32_gemm(const int8_t *qa, const int8_t *w, int64_t M, int64_t N,
+                     int64_t K, int32_t *acc, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const int8_t *wr = w + n * K;
+    for (int64_t m = 0; m < M; ++m) {
+      const int8_t *ar = qa + m * K;
+      int32_t s = 0;
+      for (int64_t k = 0; k < K; ++k) s += (int32_t)ar[k] * (int32_t)wr[k];
+      acc[m * N + n] = s;
+    }
+  }
+  return ZTO_OK;
+}
+
+/* Full op: quantise, exact int32 GEMM, then y = ((float)acc*sx[m])*sw[n] + b[n]
+ * with the post-ops (an extension; the reference op has none) and one
+ * rounding to y_dt.  Returns qx/sx/acc through the optional out pointers. */
+int zto_dynamic_qlinear(const void *x, int x_dt, int64_t M, int64_t K,
+                        const int8_t *w, int64_t N, const void *sw, int sw_dt,
+                        const void *bias, int b_dt, int n_post,
+                        const int *post_ids, const void *const *post_bufs,
+                        const int *post_dts, const int64_t *post_lds, void *y,
+                        int y_dt, int8_t *qx_out, float *sx_out,
+                        int32_t *acc_out, int nthreads) {
+  int8_t *qx = qx_out ? qx_out : (int8_t *)malloc((size_t)(M * K > 0 ? M * K : 1));
+  float *sx = sx_out ? sx_out : (float *)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1));
+  int32_t *acc = acc_out ? acc_out
+                         : (int32_t *)malloc(sizeof(int32_t) * (size_t)(M * N > 0 ? M * N : 1));
+  if (!qx || !sx || !acc) return ZTO_EINVAL;
+  zto_dynamic_quantize(x, x_dt, M, K, qx, sx, nthreads);
+  zto_s8s8s32_gemm(qx, w, M, N, K, acc, nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float v = (float)acc[m * N + n] * sx[m];
+      v = v * load_f(sw, sw_dt, n);
+      if (bias) v = v + load_f(bias, b_dt, n);
+      v = apply_post_ops(v, n_post, post_ids, post_bufs, post_dts, post_lds, m, n);
+      store_f(y, y_dt, m * N + n, v);
+    }
+  }
+  if (!qx_out) free(qx);
+  if (!sx_out) free(sx);
+  if (!acc_out) free(acc);
+  return ZTO_OK;
+}

@@ -1,0 +1,133 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads and exports
+every symbol include/*.h declares, the torch ops carry the reference's exact
+schemas, Meta kernels give the reference's output shapes, and a CPU tensor
+is an error (no CPU fallback).  No GPU compute is called here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+PKG = os.path.join(ROOT, "zendnn-pytorch-plugin_amd", "zentorch")
+
+
+def declared(header):
+    text = open(os.path.join(INCLUDE, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:zt|aoti_torch_cuda_zentorch)_\w+)\s*\(", text)))
+
+
+def exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib], capture_output=True, text=True,
+                         check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if l.strip()}
+
+
+def test_c_abi_exports_every_declared_symbol():
+    names = declared("zentorch_hip.h")
+    assert "zt_woq_linear" in names and "zt_dynamic_qlinear" in names
+    lib = os.path.join(PKG, "libzentorch_hip.so")
+    syms = exported(lib)
+    missing = [n for n in names if n not in syms]
+    assert not missing, missing
+    L = ctypes.CDLL(lib)
+    for n in names:
+        getattr(L, n)
+    L.zt_version.restype = ctypes.c_int32
+    assert L.zt_version() >= 100
+
+
+def test_c_abi_needs_no_torch():
+    out = subprocess.run(["readelf", "-d", os.path.join(PKG, "libzentorch_hip.so")],
+                         capture_output=True, text=True, check=True).stdout
+    assert "torch" not in out and "c10" not in out
+
+
+def test_aoti_shims_exported():
+    names = declared("shim_cuda_zentorch.h")
+    assert len(names) == 10
+    syms = exported(os.path.join(PKG, "_C.so"))
+    assert not [n for n in names if n not in syms]
+
+
+def test_c_abi_validates_without_gpu():
+    import zt_capi as C
+    L = C.lib()
+    # K not a multiple of 8 is rejected before any device work
+    rc = L.zt_woq_linear(None, 1, 4, 12, 12, None, 16, None, 1, 1, None, -1, None, -1,
+                         None, None, 1, 16, None, 0, None)
+    assert rc == 1 and b"K" in L.zt_last_error_string()
+    rc = L.zt_woq_repack_from_int4pack(None, 10, 64, None, None)
+    assert rc == 1 and b"multiple of 64" in L.zt_last_error_string()
+    assert L.zt_dynamic_qlinear_workspace_size(128, 4096) >= 128 * 4096 + 128 * 4
+    # the split-K workspace is needed for the long-K decode shapes
+    assert L.zt_woq_linear_workspace_size(16, 14336, 4096, 112) > 4096
+    assert L.zt_woq_linear_workspace_size(2048, 4096, 4096, 32) == 0
+
+
+# Schemas as the reference registers them (src/cpu/cpp/WOQ_Linear.cpp:435-480,
+# DynamicQLinear.cpp:184-189), in torch's canonical printing.
+REFERENCE_SCHEMAS = {
+    "zentorch_woq_linear": "zentorch::zentorch_woq_linear(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear\") -> Tensor",
+    "zentorch_woq_linear_relu": "zentorch::zentorch_woq_linear_relu(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_relu\") -> Tensor",
+    "zentorch_woq_linear_sigmoid": "zentorch::zentorch_woq_linear_sigmoid(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_sigmoid\") -> Tensor",
+    "zentorch_woq_linear_gelu_tanh": "zentorch::zentorch_woq_linear_gelu_tanh(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_gelu_tanh\") -> Tensor",
+    "zentorch_woq_linear_gelu_erf": "zentorch::zentorch_woq_linear_gelu_erf(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_gelu_erf\") -> Tensor",
+    "zentorch_woq_linear_add": "zentorch::zentorch_woq_linear_add(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor add_input, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_add\") -> Tensor",
+    "zentorch_woq_linear_mul_add": "zentorch::zentorch_woq_linear_mul_add(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor mul_input, Tensor add_input, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_mul_add\") -> Tensor",
+    "zentorch_woq_linear_add_add": "zentorch::zentorch_woq_linear_add_add(Tensor input, Tensor weight, Tensor weight_scales, Tensor? weight_zero_points, Tensor add_input, Tensor add_input_2, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_woq_linear_add_add\") -> Tensor",
+    "zentorch_woq_repack_weight": "zentorch::zentorch_woq_repack_weight(Tensor unpacked_weight) -> Tensor",
+    "zentorch_woq_repack_from_int4pack": "zentorch::zentorch_woq_repack_from_int4pack(Tensor packed_weight) -> Tensor",
+    "zentorch_dynamic_qlinear": "zentorch::zentorch_dynamic_qlinear(Tensor input, Tensor weight, Tensor weight_scales, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_dynamic_qlinear\") -> Tensor",
+}
+
+
+@pytest.mark.parametrize("op", sorted(REFERENCE_SCHEMAS))
+def test_op_schema_matches_reference(op):
+    import zentorch  # noqa: F401
+    assert str(getattr(torch.ops.zentorch, op).default._schema) == REFERENCE_SCHEMAS[op]
+
+
+def test_reference_tags_kept():
+    import zentorch  # noqa: F401
+    ops = torch.ops.zentorch
+    assert torch.Tag.needs_contiguous_strides in ops.zentorch_woq_linear_add.default.tags
+    assert torch.Tag.needs_fixed_stride_order in ops.zentorch_woq_linear_mul_add.default.tags
+    assert torch.Tag.needs_fixed_stride_order in ops.zentorch_woq_linear_add_add.default.tags
+
+
+def test_meta_shapes():
+    import zentorch  # noqa: F401
+    ops = torch.ops.zentorch
+    m = dict(device="meta")
+    x = torch.empty(2, 3, 4096, dtype=torch.bfloat16, **m)
+    w = torch.empty(512, 6144, dtype=torch.int32, **m)
+    s = torch.empty(32, 6144, dtype=torch.bfloat16, **m)
+    y = ops.zentorch_woq_linear(x, w, s, None)
+    assert y.shape == (2, 3, 6144) and y.dtype == torch.bfloat16
+    buf = torch.empty(2, 3, 6144, dtype=torch.bfloat16, **m)
+    assert ops.zentorch_woq_linear_mul_add(x, w, s, None, buf, buf).shape == (2, 3, 6144)
+    assert ops.zentorch_woq_linear_silu_mul(x, w, s, None, buf).shape == (2, 3, 6144)
+    xw = torch.empty(128, 4096, dtype=torch.float32, **m)
+    wq = torch.empty(11008, 4096, dtype=torch.int8, **m)
+    y = ops.zentorch_dynamic_qlinear(xw, wq, torch.empty(11008, **m))
+    assert y.shape == (128, 11008) and y.dtype == torch.float32
+    r = ops.zentorch_woq_repack_weight(torch.empty(64, 256, dtype=torch.int8, **m))
+    assert r.shape == (64, 32) and r.dtype == torch.int32
+    r = ops.zentorch_woq_repack_from_int4pack(torch.empty(64, 128, dtype=torch.uint8, **m))
+    assert r.shape == (64, 32) and r.dtype == torch.int32
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    import zentorch  # noqa: F401
+    x = torch.randn(4, 64).bfloat16()
+    with pytest.raises(NotImplementedError):
+        torch.ops.zentorch.zentorch_woq_linear(x, torch.zeros(8, 16, dtype=torch.int32),
+                                               torch.ones(1, 16).bfloat16(), None)
+    with pytest.raises(NotImplementedError):
+        torch.ops.zentorch.zentorch_dynamic_qlinear(x, torch.zeros(16, 64, dtype=torch.int8),
+                                                    torch.ones(16))

@@ -1,0 +1,98 @@
+"""GPU parity of the dynamic int8 path against the CPU oracle, through the
+C-ABI.  Quantised activations (qx, sx) and int32 accumulators are integer /
+exact-closed-form results and must be bit-exact; bf16/fp32 outputs are held
+to rtol = atol = 1e-2 (test/unittests/op_tests/test_dynamic_qlinear.py:103).
+"""
+import os
+
+import pytest
+import torch
+from safetensors.torch import load_file
+
+import zt_capi as C
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[case] {request.node.name}", flush=True)
+
+
+def make(M, K, N, seed, x_dtype=torch.bfloat16, sw_dtype=torch.float32, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(x_dtype)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = (torch.rand(N, generator=g) * 0.009 + 0.001).to(sw_dtype)
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16() if bias else None
+    return x, w, sw, b
+
+
+@pytest.mark.parametrize("M,K", [(1, 4), (3, 12), (16, 16), (128, 4096), (7, 11008),
+                                 (2048, 4096), (5, 1)])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_quantize_bit_exact(M, K, x_dtype):
+    g = torch.Generator().manual_seed(M * 31 + K)
+    x = (torch.randn(M, K, generator=g) * 2).to(x_dtype)
+    if M > 2:
+        x[1] = 0  # all-zero row -> scale 1e-12/127
+    qx, sx = C.dynamic_quantize(x.to(DEV))
+    qr, sr = O.dynamic_quantize(x)
+    assert torch.equal(sx.cpu(), sr)
+    assert torch.equal(qx.cpu(), qr)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 16), (5, 33, 48), (64, 96, 256), (128, 11008, 4096),
+                                   (300, 130, 512), (2048, 256, 1024), (4, 17, 12)])
+def test_s8_gemm_accumulators_bit_exact(M, N, K):
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    acc = C.s8s8s32_gemm(a.to(DEV), w.to(DEV)).cpu()
+    ref = O.s8s8s32_gemm(a, w) if M * N * K <= 2 ** 28 else torch._int_mm(a, w.t().contiguous())
+    assert torch.equal(acc, ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4, 8), (4, 12, 16), (16, 16, 32), (24, 128, 48),
+                                   (128, 4096, 11008), (33, 4096, 4096), (256, 1024, 640)])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_dynamic_qlinear_vs_oracle(M, K, N, x_dtype):
+    x, w, sw, b = make(M, K, N, seed=M + K + N, x_dtype=x_dtype)
+    y_ref = O.dynamic_qlinear(x, w, sw, b)
+    y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV)).cpu()
+    assert y.dtype == x_dtype
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_dynamic_qlinear_bf16_scales_no_bias():
+    x, w, sw, _ = make(8, 256, 64, seed=9, sw_dtype=torch.bfloat16, bias=False)
+    y_ref = O.dynamic_qlinear(x, w, sw, None)
+    y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), None).cpu()
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_golden_dynamic_fixture():
+    c = load_file(os.path.join(GOLDEN, "dynamic_qlinear.safetensors"))
+    qx, sx = C.dynamic_quantize(c["x"].to(DEV))
+    assert torch.equal(qx.cpu(), c["qx"]) and torch.equal(sx.cpu(), c["sx"])
+    acc = C.s8s8s32_gemm(c["qx"].to(DEV), c["w"].to(DEV)).cpu()
+    assert torch.equal(acc, c["acc"])
+    y = C.dynamic_qlinear(c["x"].to(DEV), c["w"].to(DEV), c["w_scales"].to(DEV),
+                          c["bias"].to(DEV)).cpu()
+    torch.testing.assert_close(y, c["y"], rtol=1e-2, atol=1e-2)
+    qb, sb = C.dynamic_quantize(c["x_bf16"].to(DEV))
+    assert torch.equal(qb.cpu(), c["qx_bf16"]) and torch.equal(sb.cpu(), c["sx_bf16"])
+
+
+def test_prefill_shape_accumulator_checksum():
+    # M = 2048 prefill (int8 path, one linear): exact
+    # accumulators against torch._int_mm on the CPU
+    g = torch.Generator().manual_seed(2048)
+    M, K, N = 2048, 4096, 6144
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    acc = C.s8s8s32_gemm(a.to(DEV), w.to(DEV)).cpu()
+    assert torch.equal(acc, torch._int_mm(a, w.t().contiguous()))

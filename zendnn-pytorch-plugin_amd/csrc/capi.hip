@@ -1,0 +1,237 @@
+// extern "C" entry points of libzentorch_hip.so (declared in
+// include/zentorch_hip.h): argument validation, kernel choice, launch.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "zt_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return ZT_OK;
+  return fail(ZT_EHIP, "%s: HIP error %d (%s)", what, (int)e,
+              hipGetErrorString(e));
+}
+
+bool is_float_dt(int dt) { return dt == ZT_DT_F32 || dt == ZT_DT_BF16; }
+
+int convert_post_ops(const zt_post_ops *in, zt::PostOps *out, const char *op) {
+  std::memset(out, 0, sizeof(*out));
+  if (!in) return ZT_OK;
+  if (in->count < 0 || in->count > ZT_MAX_POST_OPS)
+    return fail(ZT_EINVAL, "%s: post-op count %d outside [0, %d]", op,
+                (int)in->count, ZT_MAX_POST_OPS);
+  int nbuf = 0;
+  out->count = in->count;
+  for (int i = 0; i < in->count; ++i) {
+    const int id = in->ids[i];
+    if (id < ZT_PO_NONE || id > ZT_PO_ADD)
+      return fail(ZT_EINVAL, "%s: unknown post-op id %d", op, id);
+    out->ids[i] = id;
+    if (id == ZT_PO_ADD || id == ZT_PO_MUL) {
+      if (!in->bufs[nbuf])
+        return fail(ZT_EINVAL, "%s: binary post-op %d has no buffer", op, i);
+      if (!is_float_dt(in->buf_dtypes[nbuf]))
+        return fail(ZT_EINVAL, "%s: post-op buffer %d must be bf16 or fp32", op,
+                    nbuf);
+      out->bufs[nbuf] = in->bufs[nbuf];
+      out->dts[nbuf] = in->buf_dtypes[nbuf];
+      out->ld[nbuf] = in->buf_ld[nbuf];
+      ++nbuf;
+    }
+  }
+  return ZT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *zt_last_error_string(void) { return g_last_error.c_str(); }
+
+int32_t zt_version(void) { return 100; }
+
+size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
+                                    int64_t G) {
+  if (M <= 0 || N <= 0 || K <= 0 || G <= 0 || K % G) return 0;
+  zt::WoqArgs a{};
+  a.x_dt = ZT_DT_BF16;
+  a.M = M, a.K = K, a.N = N, a.G = G, a.ldx = K;
+  // Assume aligned pointers: the workspace a call needs is never larger.
+  a.x = reinterpret_cast<const void *>(256);
+  a.w = reinterpret_cast<const uint32_t *>(256);
+  if (zt::woq_select_kernel(a) != zt::kWoqDecode) return 0;
+  zt::DecodePlan p;
+  if (!zt::woq_decode_plan(M, N, K, &p)) return 0;
+  return zt::woq_decode_workspace(p, M, N);
+}
+
+int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                  int64_t ldx, const int32_t *w_packed, int64_t N,
+                  const void *scales, int32_t scales_dtype, int64_t G,
+                  const void *zp, int32_t zp_dtype, const void *bias,
+                  int32_t bias_dtype, const zt_post_ops *post, void *y,
+                  int32_t y_dtype, int64_t ldy, void *workspace,
+                  size_t workspace_bytes, zt_stream_t stream) {
+  static const char *op = "zt_woq_linear";
+  if (M < 0 || N < 0 || K < 8 || K % 8)
+    return fail(ZT_EINVAL, "%s: need M,N >= 0 and K >= 8 with K %% 8 == 0 "
+                "(M=%lld N=%lld K=%lld)", op, (long long)M, (long long)N,
+                (long long)K);
+  if (G < 1 || K % G)
+    return fail(ZT_EINVAL, "%s: scale groups G=%lld must divide K=%lld", op,
+                (long long)G, (long long)K);
+  if (!is_float_dt(x_dtype) || !is_float_dt(y_dtype) || !is_float_dt(scales_dtype))
+    return fail(ZT_EINVAL, "%s: input, output and scales must be bf16 or fp32", op);
+  if (zp && !(is_float_dt(zp_dtype) || zp_dtype == ZT_DT_S8 ||
+              zp_dtype == ZT_DT_U8 || zp_dtype == ZT_DT_S32))
+    return fail(ZT_EINVAL, "%s: zero points must be bf16, fp32, int8, uint8 or int32", op);
+  if (bias && !is_float_dt(bias_dtype))
+    return fail(ZT_EINVAL, "%s: bias must be bf16 or fp32", op);
+  if (ldx < K || ldy < N)
+    return fail(ZT_EINVAL, "%s: leading dimensions too small", op);
+  if (M == 0 || N == 0) return ZT_OK;
+  if (!x || !w_packed || !scales || !y)
+    return fail(ZT_EINVAL, "%s: null tensor pointer", op);
+
+  zt::WoqArgs a{};
+  a.x = x, a.x_dt = x_dtype, a.M = M, a.K = K, a.ldx = ldx;
+  a.w = reinterpret_cast<const uint32_t *>(w_packed), a.N = N;
+  a.scales = scales, a.s_dt = scales_dtype, a.G = G;
+  a.zp = zp, a.zp_dt = zp ? zp_dtype : ZT_DT_NONE;
+  a.bias = bias, a.b_dt = bias ? bias_dtype : ZT_DT_NONE;
+  a.y = y, a.y_dt = y_dtype, a.ldy = ldy;
+  int rc = convert_post_ops(post, &a.post, op);
+  if (rc) return rc;
+
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (zt::woq_select_kernel(a)) {
+  case zt::kWoqDecode: {
+    zt::DecodePlan p;
+    if (!zt::woq_decode_plan(M, N, K, &p))
+      return hip_status(zt::launch_woq_generic(a, s), op);
+    const size_t need = zt::woq_decode_workspace(p, M, N);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+      return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op,
+                  need, workspace ? workspace_bytes : (size_t)0);
+    return hip_status(zt::launch_woq_decode(a, p, workspace, s), op);
+  }
+  case zt::kWoqGemm:
+    return hip_status(zt::launch_woq_gemm(a, s), op);
+  default:
+    return hip_status(zt::launch_woq_generic(a, s), op);
+  }
+}
+
+size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  const size_t q = ((size_t)M * K + 255) & ~(size_t)255;
+  return q + (size_t)M * sizeof(float);
+}
+
+int zt_dynamic_quantize(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                        int8_t *qx, float *sx, zt_stream_t stream) {
+  static const char *op = "zt_dynamic_quantize";
+  if (!is_float_dt(x_dtype))
+    return fail(ZT_EINVAL, "%s: input must be bf16 or fp32", op);
+  if (M < 0 || K < 1) return fail(ZT_EINVAL, "%s: need M >= 0, K >= 1", op);
+  if (M == 0) return ZT_OK;
+  if (!x || !qx || !sx) return fail(ZT_EINVAL, "%s: null pointer", op);
+  return hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                    op);
+}
+
+int zt_s8s8s32_gemm(const int8_t *qa, const int8_t *w, int64_t M, int64_t N,
+                    int64_t K, int32_t *acc, zt_stream_t stream) {
+  static const char *op = "zt_s8s8s32_gemm";
+  if (M < 0 || N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
+  if (M == 0 || N == 0) return ZT_OK;
+  if (!qa || !w || !acc) return fail(ZT_EINVAL, "%s: null pointer", op);
+  zt::DynArgs a{};
+  a.M = M, a.N = N, a.K = K, a.w = w, a.qx = qa;
+  a.y = acc, a.y_dt = ZT_DT_S32;
+  return hip_status(zt::launch_s8_gemm(a, reinterpret_cast<hipStream_t>(stream)), op);
+}
+
+int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                       const int8_t *w, int64_t N, const void *w_scales,
+                       int32_t w_scales_dtype, const void *bias,
+                       int32_t bias_dtype, const zt_post_ops *post, void *y,
+                       int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                       zt_stream_t stream) {
+  static const char *op = "zt_dynamic_qlinear";
+  if (!is_float_dt(x_dtype) || !is_float_dt(y_dtype))
+    return fail(ZT_EINVAL, "%s: input and output must be bf16 or fp32", op);
+  if (!is_float_dt(w_scales_dtype))
+    return fail(ZT_EINVAL, "%s: weight_scales must be float32 or bfloat16", op);
+  if (bias && !is_float_dt(bias_dtype))
+    return fail(ZT_EINVAL, "%s: bias must be float32 or bfloat16", op);
+  if (M < 0 || N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
+  if (M == 0 || N == 0) return ZT_OK;
+  if (!x || !w || !w_scales || !y) return fail(ZT_EINVAL, "%s: null pointer", op);
+  const size_t need = zt_dynamic_qlinear_workspace_size(M, K);
+  if (!workspace || workspace_bytes < need)
+    return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op,
+                need, workspace ? workspace_bytes : (size_t)0);
+  zt::DynArgs a{};
+  a.x = x, a.x_dt = x_dtype, a.M = M, a.K = K, a.w = w, a.N = N;
+  a.sw = w_scales, a.sw_dt = w_scales_dtype;
+  a.bias = bias, a.b_dt = bias ? bias_dtype : ZT_DT_NONE;
+  a.y = y, a.y_dt = y_dtype;
+  int rc = convert_post_ops(post, &a.post, op);
+  if (rc) return rc;
+  int8_t *qx = reinterpret_cast<int8_t *>(workspace);
+  float *sx = reinterpret_cast<float *>(
+      reinterpret_cast<char *>(workspace) + (((size_t)M * K + 255) & ~(size_t)255));
+  a.qx = qx, a.sx = sx;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, s), op);
+  if (rc) return rc;
+  return hip_status(zt::launch_s8_gemm(a, s), op);
+}
+
+int zt_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out,
+                         zt_stream_t stream) {
+  static const char *op = "zt_woq_repack_weight";
+  if (K < 8 || K % 8)
+    return fail(ZT_EINVAL, "%s: K must be at least 8 and divisible by 8, got %lld",
+                op, (long long)K);
+  if (N < 0) return fail(ZT_EINVAL, "%s: N must be >= 0", op);
+  if (N == 0) return ZT_OK;
+  if (!w || !out) return fail(ZT_EINVAL, "%s: null pointer", op);
+  return hip_status(zt::launch_repack(w, N, K, out, reinterpret_cast<hipStream_t>(stream)), op);
+}
+
+int zt_woq_repack_from_int4pack(const uint8_t *packed, int64_t N, int64_t K,
+                                int32_t *out, zt_stream_t stream) {
+  static const char *op = "zt_woq_repack_from_int4pack";
+  if (N % 64)
+    return fail(ZT_EINVAL, "%s: packed_weight row count (%lld) must be a multiple "
+                "of 64", op, (long long)N);
+  if (K < 8 || K % 8)
+    return fail(ZT_EINVAL, "%s: K must be at least 8 and divisible by 8, got %lld",
+                op, (long long)K);
+  if (N == 0) return ZT_OK;
+  if (!packed || !out) return fail(ZT_EINVAL, "%s: null pointer", op);
+  return hip_status(zt::launch_repack_from_int4pack(
+                        packed, N, K, out, reinterpret_cast<hipStream_t>(stream)),
+                    op);
+}
+
+}  // extern "C"

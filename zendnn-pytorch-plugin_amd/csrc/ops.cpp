@@ -1,0 +1,455 @@
+// TORCH_LIBRARY(zentorch) for PyTorch-ROCm: the reference's quantized-linear
+// operator schemas, implemented for the CUDA (= HIP) dispatch key on top of
+// the C-ABI in include/zentorch_hip.h, plus the AOTInductor C shims
+// (include/shim_cuda_zentorch.h).
+//
+// Schemas are kept character-for-character with the reference
+// (src/cpu/cpp/WOQ_Linear.cpp:435-480, DynamicQLinear.cpp:184-189) so graphs,
+// the compile pass and callers such as vLLM's torchao patch bind unchanged.
+// zentorch_woq_linear_silu_mul is an extension (no reference op; the
+// reference's closest is zentorch_mm_silu_mul, Matmul.cpp:440-441).
+//
+// There is no CPU kernel: a CPU tensor reaching these ops is an error, not a
+// fallback.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+#include <vector>
+
+#include "ops.hpp"
+#include "zentorch_hip.h"
+
+namespace zentorch_hip {
+
+namespace {
+
+int32_t zt_dtype_of(const at::Tensor &t) {
+  switch (t.scalar_type()) {
+  case at::kFloat: return ZT_DT_F32;
+  case at::kBFloat16: return ZT_DT_BF16;
+  case at::kHalf: return ZT_DT_F16;
+  case at::kChar: return ZT_DT_S8;
+  case at::kByte: return ZT_DT_U8;
+  case at::kInt: return ZT_DT_S32;
+  default: return ZT_DT_NONE;
+  }
+}
+
+void check_device(const at::Tensor &t, const at::Tensor &ref, const char *op,
+                  const char *name) {
+  TORCH_CHECK(t.is_cuda(), op, ": ", name,
+              " must be a GPU tensor (zentorch-mi355x has no CPU kernels), got ",
+              t.device());
+  TORCH_CHECK(t.device() == ref.device(), op, ": ", name, " is on ", t.device(),
+              " but input is on ", ref.device());
+}
+
+hipStream_t current_stream() {
+  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+}
+
+// Per-(device, stream) workspace.  Its first bytes hold split-K tile
+// counters that every completed call leaves at zero, so a buffer is zeroed
+// once when it is created and then reused by calls on the same stream.
+struct WorkspaceCache {
+  std::mutex mu;
+  std::map<std::pair<int, hipStream_t>, at::Tensor> bufs;
+};
+
+WorkspaceCache &woq_cache() {
+  static WorkspaceCache c;
+  return c;
+}
+
+void *woq_workspace(const at::Tensor &like, size_t bytes) {
+  if (bytes == 0) return nullptr;
+  auto &c = woq_cache();
+  std::lock_guard<std::mutex> g(c.mu);
+  const auto key = std::make_pair((int)like.get_device(), current_stream());
+  auto it = c.bufs.find(key);
+  if (it == c.bufs.end() || (size_t)it->second.numel() < bytes) {
+    at::Tensor t = at::zeros({(int64_t)bytes},
+                             like.options().dtype(at::kByte));
+    c.bufs[key] = t;
+    return t.data_ptr();
+  }
+  return it->second.data_ptr();
+}
+
+std::vector<int64_t> out_sizes(const at::Tensor &input, int64_t N) {
+  auto s = input.sizes().vec();
+  s.back() = N;
+  return s;
+}
+
+at::Tensor as_2d(const at::Tensor &t) {
+  const int64_t last = t.size(-1);
+  return t.contiguous().view({t.numel() / std::max<int64_t>(last, 1), last});
+}
+
+// Shared body of every zentorch_woq_linear* op.  post_ids follow the
+// reference's post-op numbering; binary ops take binary_inputs in order.
+at::Tensor woq_linear_impl(const at::Tensor &input, const at::Tensor &weight,
+                           const at::Tensor &weight_scales,
+                           const c10::optional<at::Tensor> &weight_zero_points,
+                           const c10::optional<at::Tensor> &bias,
+                           const std::vector<int32_t> &post_ids,
+                           const std::vector<at::Tensor> &binary_inputs,
+                           const std::string &op_name) {
+  const char *op = op_name.c_str();
+  check_device(input, input, op, "input");
+  check_device(weight, input, op, "weight");
+  check_device(weight_scales, input, op, "weight_scales");
+  // Same checks and messages as WOQ_Linear.cpp:35-42.
+  TORCH_CHECK(weight.dtype() == at::kInt, "weight must have dtype int32, got ",
+              weight.dtype());
+  TORCH_CHECK(weight.dim() == 2, "weight must be 2D, got ", weight.dim(), "D");
+  TORCH_CHECK(weight_scales.dim() == 2, "weight_scales must be 2D [G, N], got ",
+              weight_scales.dim(), "D");
+  TORCH_CHECK(weight_scales.size(1) == weight.size(1), "weight_scales dim 1 (",
+              weight_scales.size(1), ") must match weight dim 1 (",
+              weight.size(1), ")");
+  const int64_t K = weight.size(0) * 8;
+  const int64_t N = weight.size(1);
+  TORCH_CHECK(input.dim() >= 2, op, ": input must be at least 2D");
+  TORCH_CHECK(input.size(-1) == K, op, ": input last dim (", input.size(-1),
+              ") must equal 8 * weight.size(0) (", K, ")");
+  TORCH_CHECK(input.scalar_type() == at::kBFloat16 ||
+                  input.scalar_type() == at::kFloat,
+              op, ": input must be bfloat16 or float32, got ",
+              input.scalar_type());
+  const int64_t G = weight_scales.size(0);
+  TORCH_CHECK(G >= 1 && K % G == 0, op, ": weight_scales groups (", G,
+              ") must divide K (", K, ")");
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
+  at::Tensor x2 = as_2d(input);
+  const int64_t M = x2.size(0);
+  // The op's weight is the [K/8, N] view of [N, K/8] storage
+  // (_op_replacements_new.py:376-379); any other strides are materialised.
+  at::Tensor w_nk = weight.t();
+  if (!w_nk.is_contiguous()) w_nk = w_nk.contiguous();
+  at::Tensor s = weight_scales.contiguous();
+  at::Tensor zp, b;
+  if (weight_zero_points.has_value() && weight_zero_points->defined()) {
+    check_device(*weight_zero_points, input, op, "weight_zero_points");
+    TORCH_CHECK(weight_zero_points->sizes() == weight_scales.sizes(), op,
+                ": weight_zero_points must have the shape of weight_scales");
+    zp = weight_zero_points->contiguous();
+  }
+  if (bias.has_value() && bias->defined()) {
+    check_device(*bias, input, op, "bias");
+    TORCH_CHECK(bias->numel() == N, op, ": bias must have N = ", N,
+                " elements, got ", bias->numel());
+    b = bias->contiguous();
+  }
+  at::Tensor result = at::empty(out_sizes(input, N), input.options());
+  if (result.numel() == 0) return result;
+
+  zt_post_ops post{};
+  post.count = (int32_t)post_ids.size();
+  TORCH_CHECK(post.count <= ZT_MAX_POST_OPS, op, ": too many post-ops");
+  std::vector<at::Tensor> keep;
+  size_t nb = 0;
+  for (size_t i = 0; i < post_ids.size(); ++i) {
+    post.ids[i] = post_ids[i];
+    if (post_ids[i] == ZT_PO_ADD || post_ids[i] == ZT_PO_MUL) {
+      TORCH_CHECK(nb < binary_inputs.size(), op, ": missing binary input");
+      const at::Tensor &bi = binary_inputs[nb];
+      check_device(bi, input, op, "binary post-op input");
+      TORCH_CHECK(bi.numel() == M * N, op, ": binary post-op input has ",
+                  bi.numel(), " elements, expected ", M * N);
+      at::Tensor bc = bi.contiguous();
+      if (bc.scalar_type() != at::kBFloat16 && bc.scalar_type() != at::kFloat)
+        bc = bc.to(input.scalar_type());
+      keep.push_back(bc);
+      post.bufs[nb] = bc.data_ptr();
+      post.buf_dtypes[nb] = zt_dtype_of(bc);
+      post.buf_ld[nb] = N;
+      ++nb;
+    }
+  }
+  const size_t ws = zt_woq_linear_workspace_size(M, K, N, G);
+  void *wsp = woq_workspace(input, ws);
+  const int rc = zt_woq_linear(
+      x2.data_ptr(), zt_dtype_of(x2), M, K, K,
+      reinterpret_cast<const int32_t *>(w_nk.data_ptr()), N, s.data_ptr(),
+      zt_dtype_of(s), G, zp.defined() ? zp.data_ptr() : nullptr,
+      zp.defined() ? zt_dtype_of(zp) : ZT_DT_NONE,
+      b.defined() ? b.data_ptr() : nullptr,
+      b.defined() ? zt_dtype_of(b) : ZT_DT_NONE, &post, result.data_ptr(),
+      zt_dtype_of(result), N, wsp, ws,
+      reinterpret_cast<zt_stream_t>(current_stream()));
+  TORCH_CHECK(rc == ZT_OK, op, ": ", zt_last_error_string());
+  return result;
+}
+
+}  // namespace
+
+template <int32_t UNARY>
+at::Tensor woq_linear_unary(const at::Tensor &input, const at::Tensor &weight,
+                            const at::Tensor &weight_scales,
+                            const c10::optional<at::Tensor> &weight_zero_points,
+                            const c10::optional<at::Tensor> &bias,
+                            c10::string_view zentorch_op_name) {
+  std::vector<int32_t> ids;
+  if (UNARY != ZT_PO_NONE) ids.push_back(UNARY);
+  return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias,
+                         ids, {}, std::string(zentorch_op_name));
+}
+
+template at::Tensor woq_linear_unary<ZT_PO_NONE>(
+    const at::Tensor &, const at::Tensor &, const at::Tensor &,
+    const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,
+    c10::string_view);
+template at::Tensor woq_linear_unary<ZT_PO_RELU>(
+    const at::Tensor &, const at::Tensor &, const at::Tensor &,
+    const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,
+    c10::string_view);
+template at::Tensor woq_linear_unary<ZT_PO_SIGMOID>(
+    const at::Tensor &, const at::Tensor &, const at::Tensor &,
+    const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,
+    c10::string_view);
+template at::Tensor woq_linear_unary<ZT_PO_GELU_TANH>(
+    const at::Tensor &, const at::Tensor &, const at::Tensor &,
+    const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,
+    c10::string_view);
+template at::Tensor woq_linear_unary<ZT_PO_GELU_ERF>(
+    const at::Tensor &, const at::Tensor &, const at::Tensor &,
+    const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,
+    c10::string_view);
+
+at::Tensor woq_linear_add(const at::Tensor &input, const at::Tensor &weight,
+                          const at::Tensor &weight_scales,
+                          const c10::optional<at::Tensor> &weight_zero_points,
+                          const at::Tensor &add_input,
+                          const c10::optional<at::Tensor> &bias,
+                          c10::string_view zentorch_op_name) {
+  return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias,
+                         {ZT_PO_ADD}, {add_input}, std::string(zentorch_op_name));
+}
+
+at::Tensor woq_linear_mul_add(const at::Tensor &input, const at::Tensor &weight,
+                              const at::Tensor &weight_scales,
+                              const c10::optional<at::Tensor> &weight_zero_points,
+                              const at::Tensor &mul_input,
+                              const at::Tensor &add_input,
+                              const c10::optional<at::Tensor> &bias,
+                              c10::string_view zentorch_op_name) {
+  return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias,
+                         {ZT_PO_MUL, ZT_PO_ADD}, {mul_input, add_input},
+                         std::string(zentorch_op_name));
+}
+
+at::Tensor woq_linear_add_add(const at::Tensor &input, const at::Tensor &weight,
+                              const at::Tensor &weight_scales,
+                              const c10::optional<at::Tensor> &weight_zero_points,
+                              const at::Tensor &add_input,
+                              const at::Tensor &add_input_2,
+                              const c10::optional<at::Tensor> &bias,
+                              c10::string_view zentorch_op_name) {
+  return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias,
+                         {ZT_PO_ADD, ZT_PO_ADD}, {add_input, add_input_2},
+                         std::string(zentorch_op_name));
+}
+
+at::Tensor woq_linear_silu_mul(const at::Tensor &input, const at::Tensor &weight,
+                               const at::Tensor &weight_scales,
+                               const c10::optional<at::Tensor> &weight_zero_points,
+                               const at::Tensor &mul_input,
+                               const c10::optional<at::Tensor> &bias,
+                               c10::string_view zentorch_op_name) {
+  return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias,
+                         {ZT_PO_SILU, ZT_PO_MUL}, {mul_input},
+                         std::string(zentorch_op_name));
+}
+
+at::Tensor woq_repack_weight(const at::Tensor &unpacked_weight) {
+  // Checks and messages of WOQ_Linear.cpp:295-310.
+  TORCH_CHECK(unpacked_weight.dtype() == at::kChar,
+              "unpacked_weight must have dtype int8, got ",
+              unpacked_weight.dtype());
+  TORCH_CHECK(unpacked_weight.dim() == 2, "unpacked_weight must be 2D, got ",
+              unpacked_weight.dim(), "D");
+  TORCH_CHECK(unpacked_weight.is_cuda(),
+              "zentorch_woq_repack_weight: unpacked_weight must be a GPU tensor, "
+              "got ", unpacked_weight.device());
+  const int64_t N = unpacked_weight.size(0), K = unpacked_weight.size(1);
+  TORCH_CHECK(K >= 8, "K must be at least ", 8, ", got ", K);
+  TORCH_CHECK(K % 8 == 0, "K must be divisible by ", 8, ", got ", K);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(unpacked_weight.device());
+  at::Tensor w = unpacked_weight.contiguous();
+  at::Tensor out = at::empty({N, K / 8}, w.options().dtype(at::kInt));
+  const int rc = zt_woq_repack_weight(
+      reinterpret_cast<const int8_t *>(w.data_ptr()), N, K,
+      reinterpret_cast<int32_t *>(out.data_ptr()),
+      reinterpret_cast<zt_stream_t>(current_stream()));
+  TORCH_CHECK(rc == ZT_OK, "zentorch_woq_repack_weight: ", zt_last_error_string());
+  return out;
+}
+
+at::Tensor woq_repack_from_int4pack(const at::Tensor &packed_weight) {
+  TORCH_CHECK(packed_weight.dtype() == at::kByte,
+              "packed_weight must have dtype uint8, got ", packed_weight.dtype());
+  TORCH_CHECK(packed_weight.dim() == 2, "packed_weight must be 2D, got ",
+              packed_weight.dim(), "D");
+  TORCH_CHECK(packed_weight.is_cuda(),
+              "zentorch_woq_repack_from_int4pack: packed_weight must be a GPU "
+              "tensor, got ", packed_weight.device());
+  const int64_t N = packed_weight.size(0), K = packed_weight.size(1) * 2;
+  TORCH_CHECK(N % 64 == 0, "packed_weight row count (", N,
+              ") must be a multiple of ", 64,
+              ". The int4pack format from PyTorch pads N to BLOCK_N; "
+              "receiving an unpadded tensor indicates a packing mismatch.");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(packed_weight.device());
+  at::Tensor p = packed_weight.contiguous();
+  at::Tensor out = at::empty({N, K / 8}, p.options().dtype(at::kInt));
+  const int rc = zt_woq_repack_from_int4pack(
+      reinterpret_cast<const uint8_t *>(p.data_ptr()), N, K,
+      reinterpret_cast<int32_t *>(out.data_ptr()),
+      reinterpret_cast<zt_stream_t>(current_stream()));
+  TORCH_CHECK(rc == ZT_OK, "zentorch_woq_repack_from_int4pack: ",
+              zt_last_error_string());
+  return out;
+}
+
+at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
+                           const at::Tensor &weight_scales,
+                           const c10::optional<at::Tensor> &bias,
+                           c10::string_view zentorch_op_name) {
+  const std::string name(zentorch_op_name);
+  // dtype / size checks with the messages of DynamicQLinear.cpp:15-70.
+  TORCH_CHECK(input.scalar_type() == at::kBFloat16 ||
+                  input.scalar_type() == at::kFloat,
+              "zentorch_dynamic_qlinear: input must be bfloat16 or float32, got ",
+              input.scalar_type());
+  TORCH_CHECK(weight_scales.scalar_type() == at::kFloat ||
+                  weight_scales.scalar_type() == at::kBFloat16,
+              "zentorch_dynamic_qlinear: weight_scales must be float32, "
+              "bfloat16, got ", weight_scales.scalar_type());
+  TORCH_CHECK(weight.scalar_type() == at::kChar,
+              "zentorch_dynamic_qlinear: weight must be int8 (c10::kChar), got ",
+              weight.scalar_type());
+  at::Tensor b;
+  if (bias.has_value() && bias->defined()) {
+    TORCH_CHECK(bias->scalar_type() == at::kFloat ||
+                    bias->scalar_type() == at::kBFloat16,
+                "zentorch_dynamic_qlinear: bias must be float32 or bfloat16, got ",
+                bias->scalar_type());
+    b = *bias;
+  }
+  TORCH_CHECK(input.dim() >= 2,
+              "zentorch_dynamic_qlinear: input must be at least 2D");
+  TORCH_CHECK(weight.dim() == 2,
+              "zentorch_dynamic_qlinear: weight must be 2D [N, K], got ",
+              weight.dim(), "D");
+  const int64_t N = weight.size(0), K = weight.size(1);
+  TORCH_CHECK(input.size(input.dim() - 1) == K,
+              "zentorch_dynamic_qlinear: input last dim (", input.size(-1),
+              ") must match weight dim 1 (", K, ")");
+  if (b.defined())
+    TORCH_CHECK(b.dim() == 1 && b.size(0) == N,
+                "zentorch_dynamic_qlinear: bias must be 1D with size N (", N, ")");
+  TORCH_CHECK(weight_scales.numel() == N,
+              "zentorch_dynamic_qlinear: weight_scales must hold one scale per "
+              "output channel (", N, "), got ", weight_scales.numel());
+  const char *op = "zentorch_dynamic_qlinear";
+  check_device(input, input, op, "input");
+  check_device(weight, input, op, "weight");
+  check_device(weight_scales, input, op, "weight_scales");
+  if (b.defined()) check_device(b, input, op, "bias");
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
+  at::Tensor result = at::empty(out_sizes(input, N), input.options());
+  if (result.numel() == 0) return result;
+  at::Tensor x2 = as_2d(input);
+  const int64_t M = x2.size(0);
+  at::Tensor wc = weight.contiguous();
+  at::Tensor sc = weight_scales.contiguous();
+  at::Tensor bc = b.defined() ? b.contiguous() : b;
+  const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K);
+  at::Tensor ws = at::empty({(int64_t)ws_bytes}, input.options().dtype(at::kByte));
+  const int rc = zt_dynamic_qlinear(
+      x2.data_ptr(), zt_dtype_of(x2), M, K,
+      reinterpret_cast<const int8_t *>(wc.data_ptr()), N, sc.data_ptr(),
+      zt_dtype_of(sc), bc.defined() ? bc.data_ptr() : nullptr,
+      bc.defined() ? zt_dtype_of(bc) : ZT_DT_NONE, nullptr, result.data_ptr(),
+      zt_dtype_of(result), ws.data_ptr(), ws_bytes,
+      reinterpret_cast<zt_stream_t>(current_stream()));
+  TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
+  return result;
+}
+
+}  // namespace zentorch_hip
+
+TORCH_LIBRARY(zentorch, m) {
+  m.def("zentorch_woq_linear(Tensor input, Tensor weight, "
+        "Tensor weight_scales, Tensor? weight_zero_points, "
+        "Tensor? bias=None, "
+        "*, str zentorch_op_name='zentorch::zentorch_woq_linear') -> Tensor");
+  m.def("zentorch_woq_linear_relu(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, "
+        "*, str zentorch_op_name="
+        "'zentorch::zentorch_woq_linear_relu') -> Tensor");
+  m.def("zentorch_woq_linear_sigmoid(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, "
+        "Tensor? bias=None, *, str "
+        "zentorch_op_name='zentorch::zentorch_woq_linear_sigmoid') -> Tensor");
+  m.def("zentorch_woq_linear_gelu_tanh(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, "
+        "*, str zentorch_op_name="
+        "'zentorch::zentorch_woq_linear_gelu_tanh') -> Tensor");
+  m.def("zentorch_woq_linear_gelu_erf(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, "
+        "*, str zentorch_op_name="
+        "'zentorch::zentorch_woq_linear_gelu_erf') -> Tensor");
+  m.def("zentorch_woq_linear_add(Tensor input, Tensor weight, "
+        "Tensor weight_scales, Tensor? weight_zero_points, "
+        "Tensor add_input, Tensor? bias=None, *, str zentorch_op_name="
+        "'zentorch::zentorch_woq_linear_add') -> Tensor",
+        {at::Tag::needs_contiguous_strides});
+  m.def("zentorch_woq_linear_mul_add(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, "
+        "Tensor mul_input, Tensor add_input, Tensor? bias=None, *, str "
+        "zentorch_op_name= 'zentorch::zentorch_woq_linear_mul_add') -> Tensor",
+        {at::Tag::needs_fixed_stride_order});
+  m.def("zentorch_woq_linear_add_add(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, "
+        "Tensor add_input, Tensor add_input_2, Tensor? bias=None, *, str "
+        "zentorch_op_name='zentorch::zentorch_woq_linear_add_add') -> Tensor",
+        {at::Tag::needs_fixed_stride_order});
+  // Extension: silu(linear) * mul_input, the gate of a gated MLP.
+  m.def("zentorch_woq_linear_silu_mul(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, "
+        "Tensor mul_input, Tensor? bias=None, *, str "
+        "zentorch_op_name='zentorch::zentorch_woq_linear_silu_mul') -> Tensor",
+        {at::Tag::needs_fixed_stride_order});
+  m.def("zentorch_woq_repack_weight(Tensor unpacked_weight) -> Tensor");
+  m.def("zentorch_woq_repack_from_int4pack(Tensor "
+        "packed_weight) -> Tensor");
+  m.def("zentorch_dynamic_qlinear(Tensor input, Tensor weight, "
+        "Tensor weight_scales, Tensor? bias=None, *, "
+        "str zentorch_op_name="
+        "'zentorch::zentorch_dynamic_qlinear') -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
+  using namespace zentorch_hip;
+  m.impl("zentorch_woq_linear", woq_linear_unary<ZT_PO_NONE>);
+  m.impl("zentorch_woq_linear_relu", woq_linear_unary<ZT_PO_RELU>);
+  m.impl("zentorch_woq_linear_sigmoid", woq_linear_unary<ZT_PO_SIGMOID>);
+  m.impl("zentorch_woq_linear_gelu_tanh", woq_linear_unary<ZT_PO_GELU_TANH>);
+  m.impl("zentorch_woq_linear_gelu_erf", woq_linear_unary<ZT_PO_GELU_ERF>);
+  m.impl("zentorch_woq_linear_add", woq_linear_add);
+  m.impl("zentorch_woq_linear_mul_add", woq_linear_mul_add);
+  m.impl("zentorch_woq_linear_add_add", woq_linear_add_add);
+  m.impl("zentorch_woq_linear_silu_mul", woq_linear_silu_mul);
+  m.impl("zentorch_woq_repack_weight", woq_repack_weight);
+  m.impl("zentorch_woq_repack_from_int4pack", woq_repack_from_int4pack);
+  m.impl("zentorch_dynamic_qlinear", dynamic_qlinear);
+}

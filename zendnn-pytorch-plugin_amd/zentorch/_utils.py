@@ -1,0 +1,24 @@
+"""Replacement counters shared by the graph passes and the tests.
+
+``counters["zentorch"][op]`` is incremented once per replaced node, as in the
+reference (src/cpu/python/zentorch/_utils.py:23; incremented e.g. at
+_op_replacements_new.py:381).  ZENTORCH_DUMP_COUNTERS=1 writes them to a JSON
+file at exit (_utils.py:114-134).
+"""
+import atexit
+import json
+import os
+from collections import Counter, defaultdict
+
+counters = defaultdict(Counter)
+
+
+def _dump_counters():
+    if os.environ.get("ZENTORCH_DUMP_COUNTERS", "0") != "1":
+        return
+    path = os.environ.get("ZENTORCH_COUNTERS_FILE", f"zentorch_counters_{os.getpid()}.json")
+    with open(path, "w") as f:
+        json.dump({k: dict(v) for k, v in counters.items()}, f, indent=2)
+
+
+atexit.register(_dump_counters)
