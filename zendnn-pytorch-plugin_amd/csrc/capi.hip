@@ -123,8 +123,11 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   switch (zt::woq_select_kernel(a)) {
   case zt::kWoqDecode: {
     zt::DecodePlan p;
-    if (!zt::woq_decode_plan(M, N, K, &p))
+    if (!zt::woq_decode_plan(M, N, K, &p)) {
+      const int64_t gs = K / G;
+      if (K % 64 == 0 && gs % 32 == 0) return hip_status(zt::launch_woq_gemm(a, s), op);
       return hip_status(zt::launch_woq_generic(a, s), op);
+    }
     const size_t need = zt::woq_decode_workspace(p, M, N);
     if (need > 0 && (!workspace || workspace_bytes < need))
       return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op,

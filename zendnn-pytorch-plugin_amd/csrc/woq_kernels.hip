@@ -25,6 +25,9 @@
 // (n, 8c+i) -- the storage of the [K/8, N] view zentorch_woq_linear takes
 // (src/cpu/cpp/WOQ_Linear.cpp:31-42, repack :345-350).
 #include <algorithm>
+#include <type_traits>
+#include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 
@@ -97,176 +100,264 @@ __global__ __launch_bounds__(256) void woq_generic_kernel(WoqArgs a) {
 // ------------------------------------------------------------- decode
 constexpr unsigned kCounterSlots = 1024;  // 4096-byte counter region
 
-// Per-(row, group) dequantisation constants for one lane's weight row.
-struct RowDq {
-  float s, s16, c0, c1;
-  DqGeneral g;
-};
+// Dequantisation modes of the decode kernel: signed int4 with bf16 scales
+// (the fast path), or the general path with bf16 / fp32 scales.
+enum DecodeMode { kDecFast = 0, kDecGenBf16 = 1, kDecGenF32 = 2 };
 
-template <bool FAST>
-__device__ __forceinline__ RowDq row_dq(const WoqArgs &a, int zmode, int64_t sidx) {
-  RowDq r;
-  const float s = load_elem(a.scales, a.s_dt, sidx);
-  if (FAST) {
-    r.s = s, r.s16 = s * 0.0625f, r.c0 = -1032.f * s, r.c1 = -72.f * s;
-  } else {
-    const float z = zmode ? load_elem(a.zp, a.zp_dt, sidx) : 0.f;
-    r.g = dq_general_params(zmode, s, z);
-  }
-  return r;
+template <int MODE>
+__device__ __forceinline__ float scale_at(const WoqArgs &a, int64_t i) {
+  if (MODE == kDecGenF32) return reinterpret_cast<const float *>(a.scales)[i];
+  return bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(a.scales)[i]);
 }
 
-template <bool FAST>
-__device__ __forceinline__ bf16x8_t dq_word(uint32_t w, const RowDq &r) {
-  const u32x4_t v = FAST ? dq8_s4_bf16scale(w, r.s, r.s16, r.c0, r.c1) : dq8_general(w, r.g);
+template <int MODE>
+__device__ __forceinline__ bf16x8_t dq_word(uint32_t w, float s, float z, int zmode) {
+  u32x4_t v;
+  if (MODE == kDecFast)
+    v = dq8_s4_bf16scale(w, s, s * 0.0625f, -1032.f * s, -72.f * s);
+  else
+    v = dq8_general(w, dq_general_params(zmode, s, z));
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// Decode GEMV / skinny GEMM (M <= 32).  Grid (row blocks, K splits); a
-// workgroup of NW waves covers TPW 16-row tiles over its K split, wave w
-// taking CPW 128-wide chunks of it.  Lane (r = lane%16, g = lane/16) loads
-// the 16 bytes of row r holding elements [32g, 32g+32) of a chunk, which are
-// exactly its A operands for the chunk's four 16x16x32 MFMAs; the matching
-// activations (B operands) are loaded once per wave and reused for every
-// tile.  Partial sums meet in LDS; with more than one K split the last
-// workgroup of a row block adds the splits' fp32 partials.
-template <int MT, int CPW, bool FAST>
-__global__ __launch_bounds__(512, 2) void woq_decode_kernel(
-    WoqArgs a, int S, int TPW, float *part, unsigned *counters) {
-  extern __shared__ float red[];  // [TPW*16 rows][RS]
+// Decode GEMV / skinny GEMM (M <= 32).
+//
+// Grid (row blocks, K splits).  A workgroup has NT x NK waves: wave (ti, ki)
+// takes TPW consecutive 16-row tiles of the row block over K-slice ki of the
+// workgroup's split (CPW 128-wide chunks).  Lane (r = lane%16, g = lane/16)
+// loads the 16 bytes of row r holding elements [32g, 32g+32) of a chunk --
+// exactly its A operands for the chunk's four 16x16x32 MFMAs -- so weights go
+// from HBM to registers without touching LDS.  The activations of the wave's
+// chunks are loaded once into registers as B operands (L2-resident: every
+// workgroup reads the same few KB).  Each wave stores its fp32
+// tile partials to its own LDS slab; after one barrier the slabs are added in
+// ki order (deterministic), and with more than one split the last workgroup
+// of a row block adds the splits' partials from global memory in split order.
+template <int CPW>
+constexpr int decode_max_threads() {
+  return CPW <= 2 ? 1024 : (CPW == 4 ? 512 : 256);
+}
+
+// Bytes of the per-wave partial slabs at the start of the dynamic LDS.
+__host__ __device__ inline size_t decode_slab_bytes(int NK, int NT, int TPW, int mt) {
+  return (size_t)NK * NT * TPW * 16 * (16 * mt + 1) * sizeof(float);
+}
+
+// gfx9 raw buffer resource: 32-bit offsets from one SGPR base, hardware
+// range check (reads past num_records return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+
+// Decode GEMV / skinny GEMM (M <= 32).
+//
+// Grid: one workgroup per row block of NT*TPW 16-row tiles, covering all of
+// K.  Wave (ti, ki) of the NT x NK waves owns the K slice
+// [c_wave, c_wave + CW) of 128-wide chunks and walks NI items, fully
+// unrolled so every wait on memory is exact:
+//  * XR (one phase): item = one of the wave's TPW tiles over the whole
+//    slice; the slice's activations are loaded once into registers and
+//    reused for every tile.
+//  * XG (phased, TPW = 1): item = CPW chunks of the slice; the item's
+//    activations are prefetched with its weights.
+// Lane (r = lane%16, g = lane/16) loads the 16 bytes of row r holding
+// elements [32g, 32g+32) of a chunk -- exactly its A operands for the
+// chunk's four 16x16x32 MFMAs -- so weights go from HBM to registers
+// without touching LDS, two items ahead.  Each wave stores its fp32 tile
+// partials to its own LDS slab; after one barrier the NK slabs of an output
+// are added by a fixed shuffle tree (deterministic).  Scale group of chunk
+// kc: (kc >> cpg_shift) & gmask (gmask = 0: per channel).
+template <int MT, int CPW, int NI, int MODE, bool XR, bool XS>
+__global__ __launch_bounds__(decode_max_threads<CPW>()) void woq_decode_kernel(
+    WoqArgs a, int NK, int NT, int cpg_shift, int gmask) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int RS = 16 * MT + 1;
-  __shared__ int is_last;
+  constexpr int PF = NI < 2 ? NI : 2;  // items in flight while one is computed
+  constexpr int TPW = XR ? NI : 1;
 
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
+  const int ki = wv % NK, ti = wv / NK;
   const int lr = lane & 15, lg = lane >> 4;
-  const int rb = blockIdx.x, sp = blockIdx.y;
   const int M = (int)a.M, N = (int)a.N;
-  const int64_t KW = a.K / 8;
+  const int KW = (int)(a.K / 8);
   const int C = (int)(a.K / 128);
-  const int Cs = (C + S - 1) / S;
-  const int c_lo = sp * Cs + wv * CPW;
-  const int c_hi = min(C, (sp + 1) * Cs);
-  const int64_t gs = a.K / a.G;
+  const int CW = (C + NK - 1) / NK;
+  const int c_wave = ki * CW;
+  const int c_hi = min(C, c_wave + CW);
   const int zmode = zp_mode_of(a.zp, a.zp_dt);
-
-  for (int i = threadIdx.x; i < TPW * 16 * RS; i += blockDim.x) red[i] = 0.f;
-
-  // Activations of this wave's chunks as MFMA B operands: lane (m, g) holds
-  // x[m, 128c + 32g + 8i .. +8) for MFMA i of chunk c.
-  bf16x8_t xb[CPW][MT][4];
+  const int tiles = (N + 15) / 16;
+  const int t_blk = blockIdx.x * NT * TPW;
+  const int t0 = t_blk + ti * TPW;
+  // Items that carry work: tiles that exist (XR) or phases (XG).
+  const int n_items = XR ? min(NI, max(0, tiles - t0)) : (t0 < tiles ? NI : 0);
+  float *slab = reinterpret_cast<float *>(smem);
   const uint16_t *xp = reinterpret_cast<const uint16_t *>(a.x);
+  const int s_bytes = MODE == kDecGenF32 ? 4 : 2;
+  const auto w_rsrc = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rsrc = make_rsrc(a.scales, (uint32_t)(a.G * N * s_bytes));
+
+  // Raw words and scale bits only: converting at load time would make the
+  // compiler wait for the load right there.
+  struct ItemRegs {
+    u32x4_t w[CPW];
+    uint32_t s[CPW];
+    float z[CPW];
+    u32x4_t x[XR ? 1 : CPW][MT][4];
+  };
+  auto x_at = [&](int kc, int mt, int i) -> u32x4_t {
+    const int m = min(mt * 16 + lr, M - 1);
+    return *reinterpret_cast<const u32x4_t *>(xp + (int64_t)m * a.ldx + (int64_t)kc * 128 +
+                                              32 * lg + 8 * i);
+  };
+  // Item it: tile t0 + it over the slice (XR) or chunks it*CPW.. of tile t0
+  // (XG).  Indices are clamped, so every item is in bounds.
+  auto load_item = [&](ItemRegs &dst, int it) {
+    const int tj = XR ? it : 0, ph = XR ? 0 : it;
+    const int n = min((t0 + tj) * 16 + lr, N - 1);
+    const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) {
-    const int kc = c_lo + c;
+    for (int c = 0; c < CPW; ++c) {
+      const int kc = min(c_wave + ph * CPW + c, C - 1);
+      const uint32_t sidx = (uint32_t)((kc >> cpg_shift) & gmask) * (uint32_t)N + (uint32_t)n;
+      dst.w[c] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, row_off + (uint32_t)kc * 64u, 0, 0));
+      if (MODE == kDecGenF32)
+        dst.s[c] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, sidx * 4u, 0, 0);
+      else
+        dst.s[c] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, sidx * 2u, 0, 0);
+      dst.z[c] = (MODE != kDecFast && zmode) ? load_elem(a.zp, a.zp_dt, sidx) : 0.f;
+      if (!XR) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + lr;
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst.x[XR ? 0 : c][mt][i] = x_at(kc, mt, i);
+      }
+    }
+  };
+
+  // XS (M <= 8): the wave's activation slice, M rows x CW*128, with
+  // full-width coalesced loads issued before the weights, bounced through a
+  // wave-private LDS region into the B-operand layout.  A B-operand load
+  // straight from global would keep only M of 16 row lanes busy.
+  constexpr int XSU = XS ? 8 * CPW * 16 / 64 : 1;  // 16-byte units per lane
+  const int xs_upr = CW * 16;                       // units per row
+  const int xs_ld = CW * 128 + 8;                   // bf16 per LDS row
+  uint16_t *xs_lds = reinterpret_cast<uint16_t *>(
+      smem + decode_slab_bytes(NK, NT, TPW, MT) + (size_t)wv * 8 * xs_ld * 2);
+  u32x4_t xs_v[XSU];
+  if (XS) {
+#pragma unroll
+    for (int u = 0; u < XSU; ++u) {
+      const int idx = lane + 64 * u;
+      const int m = min(idx / xs_upr, M - 1), k16 = idx % xs_upr;
+      const int kc = min(c_wave + k16 / 16, C - 1);
+      xs_v[u] = *reinterpret_cast<const u32x4_t *>(xp + (int64_t)m * a.ldx + (int64_t)kc * 128 +
+                                                   (k16 % 16) * 8);
+    }
+  }
+
+  ItemRegs buf[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load_item(buf[p], p);
+  // XR: the slice's activations, once (CPW covers the whole slice).
+  u32x4_t xr[XR ? CPW : 1][MT][4];
+  if (XR && XS) {
+#pragma unroll
+    for (int u = 0; u < XSU; ++u) {
+      const int idx = lane + 64 * u;
+      const int m = idx / xs_upr, k16 = idx % xs_upr;
+      if (m < M) *reinterpret_cast<u32x4_t *>(xs_lds + m * xs_ld + k16 * 8) = xs_v[u];
+    }
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         u32x4_t v = {0u, 0u, 0u, 0u};
-        if (kc < c_hi && m < M)
-          v = *reinterpret_cast<const u32x4_t *>(
-              xp + (int64_t)m * a.ldx + (int64_t)kc * 128 + 32 * lg + 8 * i);
-        xb[c][mt][i] = __builtin_bit_cast(bf16x8_t, v);
+        if (lr < M && c < CW)
+          v = *reinterpret_cast<const u32x4_t *>(xs_lds + lr * xs_ld + c * 128 + 32 * lg + 8 * i);
+        xr[XR ? c : 0][0][i] = v;
       }
-    }
+  } else if (XR) {
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[XR ? c : 0][mt][i] = x_at(min(c_wave + c, C - 1), mt, i);
   }
-  __syncthreads();
 
-  const int tiles = (N + 15) / 16;
-  const int t_lo = rb * TPW;
-  const int t_hi = min(tiles, t_lo + TPW);
-
-  u32x4_t wcur[CPW], wnxt[CPW];
-  auto load_tile = [&](u32x4_t *dst, int t) {
-    const int n = min(t * 16 + lr, N - 1);
-    const uint32_t *row = a.w + (int64_t)n * KW;
+  f32x4_t acc[MT];
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int kc = c_lo + c;
-      if (kc < c_hi)
-        dst[c] = *reinterpret_cast<const u32x4_t *>(row + (int64_t)kc * 16 + 4 * lg);
-      else
-        dst[c] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  if (t_lo < t_hi) load_tile(wcur, t_lo);
-
-  for (int t = t_lo; t < t_hi; ++t) {
-    if (t + 1 < t_hi) load_tile(wnxt, t + 1);
-    const int n_row = min(t * 16 + lr, N - 1);
-    f32x4_t acc[MT];
+  for (int it = 0; it < NI; ++it) {
+    ItemRegs &cur = buf[it % PF];
+    if (it < n_items) {
+      const int ph = XR ? 0 : it;
+      if (XR || it == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int kc = c_lo + c;
-      if (kc >= c_hi) break;
-      const RowDq rd = row_dq<FAST>(a, zmode, (((int64_t)kc * 128) / gs) * N + n_row);
+      for (int c = 0; c < CPW; ++c) {
+        const int kc = c_wave + ph * CPW + c;
+        if (kc < c_hi) {
+          const uint32_t sb = cur.s[c];
+          const float sc = MODE == kDecGenF32 ? __uint_as_float(sb) : __uint_as_float(sb << 16);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bf16x8_t A = dq_word<FAST>(wcur[c][i], rd);
+          for (int i = 0; i < 4; ++i) {
+            const bf16x8_t A = dq_word<MODE>(cur.w[c][i], sc, cur.z[c], zmode);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              u32x4_t v = XR ? xr[XR ? c : 0][mt][i] : cur.x[XR ? 0 : c][mt][i];
+              if (mt * 16 + lr >= M) v = u32x4_t{0u, 0u, 0u, 0u};
+              acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  A, __builtin_bit_cast(bf16x8_t, v), acc[mt], 0, 0, 0);
+            }
+          }
+        }
+      }
+      if (XR || it == n_items - 1) {
+        // D[row = 4g + r][token = lane % 16] into this wave's slab
+        float *sl = slab + ((size_t)(ki * NT + ti) * TPW + (XR ? it : 0)) * 16 * RS;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, xb[c][mt][i], acc[mt], 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sl[(4 * lg + r) * RS + mt * 16 + lr] = acc[mt][r];
       }
     }
-    // D[row = 4g + r][token = lane % 16]
-    float *rt = red + (t - t_lo) * 16 * RS;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        atomicAdd(rt + (4 * lg + r) * RS + mt * 16 + lr, acc[mt][r]);
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) wcur[c] = wnxt[c];
+    if (it + PF < NI) load_item(cur, it + PF);
   }
   __syncthreads();
 
-  const int rows = (t_hi - t_lo) * 16;
-  const int n0 = t_lo * 16;
+  // Add the NK slabs of each output with a fixed shuffle tree: NKP (NK
+  // rounded up to a power of two) consecutive lanes hold one output's
+  // partials, so the result does not depend on wave timing.
+  const int rows = (min(tiles, t_blk + NT * TPW) - t_blk) * 16;
+  const int n0 = t_blk * 16;
   const int total = rows * M;
-  if (S == 1) {
-    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-      const int m = idx / rows, nr = idx - m * rows, n = n0 + nr;
-      if (n >= N) continue;
-      float v = red[nr * RS + m];
+  const int NKP = NK <= 1 ? 1 : (NK <= 2 ? 2 : (NK <= 4 ? 4 : (NK <= 8 ? 8 : 16)));
+  const int per_pass = blockDim.x / NKP;
+  const int kk = threadIdx.x % NKP;
+  for (int pass = 0; pass < total; pass += per_pass) {
+    const int idx = pass + threadIdx.x / NKP;
+    float v = 0.f;
+    int m = 0, nr = 0;
+    if (idx < total) {
+      m = idx / rows, nr = idx - m * rows;
+      if (kk < NK) {
+        const int tb = nr >> 4, r16 = nr & 15;
+        const int tti = tb / TPW, tj = tb - tti * TPW;
+        v = slab[((size_t)(kk * NT + tti) * TPW + tj) * 16 * RS + r16 * RS + m];
+      }
+    }
+    for (int off = 1; off < NKP; off <<= 1) v += __shfl_xor(v, off, kWave);
+    const int n = n0 + nr;
+    if (kk == 0 && idx < total && n < N) {
       if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
       v = apply_post_ops(v, a.post, m, n);
       store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
     }
-    return;
   }
-
-  // K split across workgroups: publish this split's partial, then the last
-  // workgroup of the row block adds all splits and runs the epilogue.
-  float *mine = part + (int64_t)sp * M * N;
-  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-    const int m = idx / rows, nr = idx - m * rows, n = n0 + nr;
-    if (n < N) mine[(int64_t)m * N + n] = red[nr * RS + m];
-  }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old = atomicAdd(counters + rb, 1u);
-    is_last = (old == (unsigned)(S - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-    const int m = idx / rows, nr = idx - m * rows, n = n0 + nr;
-    if (n >= N) continue;
-    float v = 0.f;
-    for (int s2 = 0; s2 < S; ++s2)
-      v += __hip_atomic_load(part + ((int64_t)s2 * M + m) * N + n, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
-    v = apply_post_ops(v, a.post, m, n);
-    store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
-  }
-  if (threadIdx.x == 0) counters[rb] = 0u;
 }
 
 // --------------------------------------------------------------- GEMM
@@ -420,7 +511,10 @@ WoqKernelKind woq_select_kernel(const WoqArgs &a) {
   if (!bf16_ok || a.N < 1) return kWoqGeneric;
   const int64_t gs = a.K / a.G;
   const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");
-  const bool decode_ok = a.K % 128 == 0 && (a.G == 1 || gs % 128 == 0) &&
+  const int64_t cpg = gs / 128;
+  const bool decode_ok = a.K % 128 == 0 &&
+                         (a.G == 1 || (gs % 128 == 0 && (cpg & (cpg - 1)) == 0)) &&
+                         a.N * (a.K / 2) < ((int64_t)1 << 31) &&  // 32-bit buffer offsets
                          a.M <= 32 && a.N < (int64_t)1 << 30;
   const bool gemm_ok = a.K % kGemmBK == 0 && gs % 32 == 0;
   if (f && !std::strcmp(f, "gemm")) return gemm_ok ? kWoqGemm : kWoqGeneric;
@@ -436,55 +530,89 @@ static int env_plan(int *v) {
   return std::sscanf(p, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) == 4;
 }
 
+static int max_waves_for(int cpw) { return (cpw <= 2 ? 1024 : (cpw == 4 ? 512 : 256)) / 64; }
+
+// Instantiated (MT, CPW, NI, XR) shapes; the launcher has one case each.
+static bool decode_shape_ok(int mt, int cpw, int ni, bool xr) {
+  if (cpw != 2) return false;
+  if (xr) return ni == 1 || ni == 2 || ni == 3 || ni == 4 || ni == 6 || ni == 8;
+  return mt == 1 && (ni == 2 || ni == 4 || ni == 8);
+}
+
+static size_t decode_lds(int64_t M, int C, const DecodePlan &p) {
+  size_t b = decode_slab_bytes(p.NK, p.NT, p.TPW, p.mt);
+  if (p.xs) {
+    const int CW = (C + p.NK - 1) / p.NK;
+    b += (size_t)p.NK * p.NT * 8 * (CW * 128 + 8) * 2;
+  }
+  (void)M;
+  return b;
+}
+
+// Shape of a decode launch (measured on MI355X, graph-replayed):
+//  * K slices of 2 chunks per wave (CPW = 2) with up to 16 waves per
+//    workgroup splitting K; for longer K the slice is walked in phases and
+//    the wave count is the one that leaves no idle chunk (K = 14336:
+//    14 waves x 8 chunks);
+//  * one row block per workgroup, TPW = ceil(tiles / 256) tiles per wave, so
+//    the grid is one round over the 256 CUs and each wave reuses its
+//    activations over TPW tiles.
 bool woq_decode_plan(int64_t M, int64_t N, int64_t K, DecodePlan *plan) {
   const int C = (int)(K / 128);
   const int tiles = (int)((N + 15) / 16);
-  const int mt = M <= 16 ? 1 : 2;
-  const int cpw_max = mt == 1 ? 4 : 2;
-  int v[4];
   DecodePlan p{};
-  p.mt = mt;
+  p.mt = M <= 16 ? 1 : 2;
+  p.S = 1;
+  p.CPW = 2;
+  p.NT = 1;
+  auto finish = [&](DecodePlan &q) {
+    const int CW = (C + q.NK - 1) / q.NK;
+    const int nphase = (CW + q.CPW - 1) / q.CPW;
+    q.xl = nphase == 1;  // XR
+    q.xs = q.xl && M <= 8;
+    q.ni = q.xl ? q.TPW : nphase;
+    if (!q.xl && q.TPW != 1) return false;
+    if (!decode_shape_ok(q.mt, q.CPW, q.ni, q.xl)) return false;
+    if (q.NK < 1 || q.NT < 1 || q.NK * q.NT > max_waves_for(q.CPW)) return false;
+    if (decode_lds(M, C, q) > 160 * 1024) return false;
+    q.nrb = (tiles + q.NT * q.TPW - 1) / (q.NT * q.TPW);
+    return true;
+  };
+  int v[4];
   if (env_plan(v)) {
-    p.S = v[0], p.NW = v[1], p.CPW = v[2], p.TPW = v[3];
-  } else {
-    // Smallest K split whose chunks fit 8 waves of cpw_max chunks; then as
-    // many row tiles per workgroup as keep >= 256 workgroups (one per CU)
-    // so the activations held in registers are reused across tiles.
-    auto split = [&](int S, int *NW, int *CPW) {
-      const int Cs = (C + S - 1) / S;
-      *NW = std::min(8, Cs);
-      *CPW = (Cs + *NW - 1) / *NW;
-      *NW = (Cs + *CPW - 1) / *CPW;
-    };
-    int S = 1, NW = 1, CPW = 1;
-    for (;; ++S) {
-      split(S, &NW, &CPW);
-      if (CPW <= cpw_max) break;
-    }
-    // Row-poor problems with more than a few tokens: split K once more so
-    // each workgroup covers several row tiles and reuses its activations.
-    if (M > 4 && tiles * S < 2 * 256 && 2 * S <= C && S < 4) {
-      S *= 2;
-      split(S, &NW, &CPW);
-    }
-    int TPW = std::max(1, (tiles * S) / 256);
-    TPW = std::min(TPW, 1024 / (16 * mt + 1));  // reduction buffer <= 64 KB of LDS
-    p.S = S, p.NW = NW, p.CPW = CPW, p.TPW = TPW;
+    p.NK = v[0], p.NT = v[1], p.CPW = v[2], p.TPW = v[3];
+    if (!finish(p)) return false;
+    *plan = p;
+    return true;
   }
-  if (p.S < 1 || p.NW < 1 || p.NW > 8 || p.CPW < 1 || p.CPW > (mt == 1 ? 8 : 4) ||
-      p.TPW < 1 || p.TPW * 16 * (16 * mt + 1) > 16384)
-    return false;
-  if ((long)p.S * p.NW * p.CPW < C) return false;  // must cover K
-  p.nrb = (tiles + p.TPW - 1) / p.TPW;
-  if (p.S > 1 && p.nrb > (int)kCounterSlots) return false;
+  if (C <= 32) {
+    p.NK = (C + 1) / 2;
+    int tpw = std::max(1, (tiles + 255) / 256);
+    for (int t : {1, 2, 3, 4, 6, 8})
+      if (t >= tpw) { tpw = t; break; }
+    p.TPW = std::min(tpw, 8);
+    // Keep the slabs of wide row blocks inside LDS.
+    while (p.TPW > 1 && !finish(p)) p.TPW = p.TPW == 8 ? 6 : (p.TPW == 6 ? 4 : p.TPW - 1);
+  } else {
+    // Phased: the largest wave count <= 16 whose slice is a whole number of
+    // 2-chunk phases with the fewest idle chunks.
+    int best_nk = 16, best_waste = 1 << 30;
+    for (int nk = 16; nk >= 1; --nk) {
+      int cw = (C + nk - 1) / nk;
+      cw = (cw + 1) / 2 * 2;
+      const int waste = cw * nk - C;
+      if ((cw / 2 == 2 || cw / 2 == 4 || cw / 2 == 8) && waste < best_waste)
+        best_nk = nk, best_waste = waste;
+    }
+    p.NK = best_nk;
+    p.TPW = 1;
+  }
+  if (!finish(p)) return false;
   *plan = p;
   return true;
 }
 
-size_t woq_decode_workspace(const DecodePlan &p, int64_t M, int64_t N) {
-  if (p.S <= 1) return 0;
-  return kCounterSlots * sizeof(unsigned) + (size_t)p.S * M * N * sizeof(float);
-}
+size_t woq_decode_workspace(const DecodePlan &, int64_t, int64_t) { return 0; }
 
 hipError_t launch_woq_generic(const WoqArgs &a, hipStream_t s) {
   const int64_t waves = a.M * a.N;
@@ -494,38 +622,51 @@ hipError_t launch_woq_generic(const WoqArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int MT, int CPW>
-static hipError_t launch_decode_t(const WoqArgs &a, const DecodePlan &p,
-                                  float *part, unsigned *counters,
-                                  hipStream_t s) {
-  const size_t lds = (size_t)p.TPW * 16 * (16 * MT + 1) * sizeof(float);
-  dim3 grid((unsigned)p.nrb, (unsigned)p.S);
-  const bool fast = a.zp == nullptr && a.s_dt == ZT_DT_BF16;
-  if (fast)
-    hipLaunchKernelGGL((woq_decode_kernel<MT, CPW, true>), grid, dim3(64 * p.NW), lds, s,
-                       a, p.S, p.TPW, part, counters);
+template <int MT, int CPW, int NI, bool XR, bool XS>
+static hipError_t launch_decode_t(const WoqArgs &a, const DecodePlan &p, hipStream_t s) {
+  const size_t lds = decode_lds(a.M, (int)(a.K / 128), p);
+  dim3 grid((unsigned)p.nrb), block(64 * p.NK * p.NT);
+  const int64_t cpg = a.G == 1 ? 0 : (a.K / a.G) / 128;
+  int shift = 0;
+  while (cpg > 1 && (1 << shift) < cpg) ++shift;
+  const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  const int mode = a.s_dt == ZT_DT_F32 ? kDecGenF32 : (a.zp ? kDecGenBf16 : kDecFast);
+  if (mode == kDecFast)
+    hipLaunchKernelGGL((woq_decode_kernel<MT, CPW, NI, kDecFast, XR, XS>), grid, block, lds, s, a,
+                       p.NK, p.NT, shift, gmask);
+  else if (mode == kDecGenBf16)
+    hipLaunchKernelGGL((woq_decode_kernel<MT, CPW, NI, kDecGenBf16, XR, XS>), grid, block, lds, s,
+                       a, p.NK, p.NT, shift, gmask);
   else
-    hipLaunchKernelGGL((woq_decode_kernel<MT, CPW, false>), grid, dim3(64 * p.NW), lds, s,
-                       a, p.S, p.TPW, part, counters);
+    hipLaunchKernelGGL((woq_decode_kernel<MT, CPW, NI, kDecGenF32, XR, XS>), grid, block, lds, s,
+                       a, p.NK, p.NT, shift, gmask);
   return hipGetLastError();
 }
 
-hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p,
-                             void *workspace, hipStream_t s) {
+hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *workspace,
+                             hipStream_t s) {
+  (void)workspace;
   if (a.M == 0 || a.N == 0) return hipSuccess;
-  unsigned *counters = reinterpret_cast<unsigned *>(workspace);
-  float *part = workspace ? reinterpret_cast<float *>(
-                                reinterpret_cast<char *>(workspace) +
-                                kCounterSlots * sizeof(unsigned))
-                          : nullptr;
-#define ZT_DECODE_CASE(MT_, CPW_)                                   \
-  if (p.mt == MT_ && p.CPW == CPW_)                                 \
-    return launch_decode_t<MT_, CPW_>(a, p, part, counters, s);
-  ZT_DECODE_CASE(1, 1) ZT_DECODE_CASE(1, 2) ZT_DECODE_CASE(1, 3)
-  ZT_DECODE_CASE(1, 4) ZT_DECODE_CASE(1, 5) ZT_DECODE_CASE(1, 6)
-  ZT_DECODE_CASE(1, 7) ZT_DECODE_CASE(1, 8)
-  ZT_DECODE_CASE(2, 1) ZT_DECODE_CASE(2, 2) ZT_DECODE_CASE(2, 3)
-  ZT_DECODE_CASE(2, 4)
+  if (std::getenv("ZT_WOQ_DEBUG"))
+    std::fprintf(stderr,
+                 "[zt] woq decode M=%lld N=%lld K=%lld: NK=%d NT=%d CPW=%d TPW=%d NI=%d xr=%d "
+                 "xs=%d grid=%d lds=%zu\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, p.NK, p.NT, p.CPW, p.TPW, p.ni,
+                 p.xl, p.xs, p.nrb, decode_lds(a.M, (int)(a.K / 128), p));
+#define ZT_DECODE_CASE(MT_, NI_, XR_, XS_)                                   \
+  if (p.mt == MT_ && p.ni == NI_ && (bool)p.xl == XR_ && (bool)p.xs == XS_) \
+    return launch_decode_t<MT_, 2, NI_, XR_, XS_>(a, p, s);
+  ZT_DECODE_CASE(1, 1, true, true) ZT_DECODE_CASE(1, 2, true, true)
+  ZT_DECODE_CASE(1, 3, true, true) ZT_DECODE_CASE(1, 4, true, true)
+  ZT_DECODE_CASE(1, 6, true, true) ZT_DECODE_CASE(1, 8, true, true)
+  ZT_DECODE_CASE(1, 1, true, false) ZT_DECODE_CASE(1, 2, true, false)
+  ZT_DECODE_CASE(1, 3, true, false) ZT_DECODE_CASE(1, 4, true, false)
+  ZT_DECODE_CASE(1, 6, true, false) ZT_DECODE_CASE(1, 8, true, false)
+  ZT_DECODE_CASE(2, 1, true, false) ZT_DECODE_CASE(2, 2, true, false)
+  ZT_DECODE_CASE(2, 3, true, false) ZT_DECODE_CASE(2, 4, true, false)
+  ZT_DECODE_CASE(2, 6, true, false) ZT_DECODE_CASE(2, 8, true, false)
+  ZT_DECODE_CASE(1, 2, false, false) ZT_DECODE_CASE(1, 4, false, false)
+  ZT_DECODE_CASE(1, 8, false, false)
 #undef ZT_DECODE_CASE
   return hipErrorInvalidValue;
 }

@@ -28,12 +28,17 @@ struct WoqArgs {
   int64_t ldy;
 };
 
-// Split of the decode (M <= 32) kernel: S K-splits, NW waves per workgroup,
-// CPW 128-wide K chunks per wave, TPW 16-row tiles per workgroup.
+// Shape of a decode (M <= 32) launch: S K splits (grid.y); NT x NK waves
+// per workgroup, wave (ti, ki) covering TPW 16-row tiles over CPW 128-wide
+// K chunks; nrb row blocks of NT*TPW tiles (grid.x).
 struct DecodePlan {
-  int mt;   // 16-token tiles (1 or 2)
-  int S, NW, CPW, TPW;
-  int nrb;  // row blocks (grid.x)
+  int mt;  // 16-token tiles (1 or 2)
+  int S, NK, NT, CPW, TPW;
+  int nrb;
+  int xl;  // activations held in registers for the whole slice (1) or
+           // prefetched per item (0)
+  int ni;  // items per wave
+  int xs;  // activation slice staged through wave-private LDS (M <= 8)
 };
 
 enum WoqKernelKind { kWoqGeneric = 0, kWoqDecode = 1, kWoqGemm = 2 };
