@@ -13,13 +13,21 @@ Secondary workloads in the same line (``workloads``): the Llama-3-8B decode
 layer at M in {1, 8, 16, 64} (config 2), dynamic int8 qlinear at M=128
 (config 1) and the M=2048 prefill layer through both paths (config 3).
 
-``roofline`` is for the dominant kernel of the headline workload (the decode
-GEMV): average kernel duration from HIP events around each launch on the
-stream the op launches on.  ``cpu_baseline`` times the CPU oracle (a port of
-the reference's semantics; zentorch itself cannot be built offline) on a
+``roofline`` is for the dominant kernel of the headline workload (the
+decode GEMV, one launch per call): ``achieved`` = algorithmic bytes per
+launch / average launch duration, the duration from HIP events recorded on
+the stream the graph replays on, around the timed replays (one kernel per
+call, so launch duration = time per call).  ``traffic`` is the HBM bytes one
+launch moves according to rocprofv3's FETCH_SIZE and WRITE_SIZE counters,
+each scaled by the factor the same counter shows for a copy kernel of known
+size; it is read from the committed summary profiles/woq_decode_config0_traffic.txt
+(written from two ``--only traffic`` runs under ``rocprofv3 --pmc``) and is
+null when that file is absent.  ``cpu_baseline`` times the CPU oracle (a port
+of the reference's semantics; zentorch itself cannot be built offline) on a
 bounded sample of the same workload on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME]
+       python bench.py --only traffic   (eager launches for rocprofv3 --pmc)
 """
 import argparse
 import json
@@ -124,23 +132,6 @@ def graph_time(calls, reps, warmup):
     return t0.elapsed_time(t1) / 1e3 / reps
 
 
-def kernel_time(call, n, warmup=3):
-    """Average seconds of one op call measured by HIP events placed directly
-    around each launch on the launching stream (no other work in between)."""
-    for i in range(warmup):
-        call(i)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(n)]
-    for i in range(n):
-        ev[i][0].record()
-        call(i)
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    ts = sorted(a.elapsed_time(b) for a, b in ev)
-    return sum(ts) / len(ts) / 1e3, ts[len(ts) // 2] / 1e3
-
-
 def copies_for(bytes_per_copy):
     return max(1, min(64, -(-ROTATE_BYTES // bytes_per_copy)))
 
@@ -152,12 +143,45 @@ def bench_config0(args, gen):
     calls = [lambda i=i: lin(i) for i in range(len(lin.w))]
     reps = max(1, args.steps // len(calls))
     t_step = graph_time(calls, reps, args.warmup) / len(calls)
-    k_avg, k_med = kernel_time(lin, max(64, len(calls)))
     b = lin.bytes()
     return {"M": M, "N": N, "K": K, "G": K // 128, "bytes_per_call": b,
             "s_per_call": t_step, "GBps": b / t_step / 1e9,
-            "kernel_avg_s": k_avg, "kernel_med_s": k_med, "kernel_GBps": b / k_avg / 1e9,
             "copies": len(lin.w), "calls_timed": reps * len(calls)}
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "woq_decode_config0_traffic.txt")
+CAL_BYTES = 8 << 20
+
+
+def traffic_pass(gen):
+    """Eager launches for the two PMC runs: 64 config-0 calls over rotating
+    weight copies, then 16 copies of a CAL_BYTES fp32 buffer (torch.neg, one
+    read and one write of CAL_BYTES each) that calibrate the counters."""
+    M, N, K = 4, 4096, 4096
+    lin = WoqLinear(M, N, K, copies=64, gen=gen)
+    for i in range(64):
+        lin(i)
+    torch.cuda.synchronize()
+    src = [torch.randn(CAL_BYTES // 4, device="cuda") for _ in range(4)]
+    dst = [torch.empty_like(src[0]) for _ in range(4)]
+    for i in range(16):
+        torch.neg(src[i % 4], out=dst[i % 4])
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_pass": "done", "woq_calls": 64, "copy_calls": 16,
+                      "copy_bytes_each_way": CAL_BYTES}))
+
+
+def read_traffic():
+    """HBM bytes per launch of the config-0 decode kernel from the committed
+    PMC summary (line 'traffic_bytes_per_launch: <int>'), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 LLAMA = [("qkv", 6144, 4096, None), ("o", 4096, 4096, None),
@@ -238,11 +262,20 @@ def cpu_baseline(budget_s=12.0):
         n += 1
     times.sort()
     med = times[len(times) // 2]
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {"value": woq_bytes(M, N, K, K // 128) / med / 1e9, "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle/zt_oracle.c zto_woq_linear on config 0 (M=4,N=K=4096,G=32), "
                       f"median of {n} calls after 3 warm-up, {threads} OpenMP threads, "
-                      f"same algorithmic-bytes formula"}
+                      f"same algorithmic-bytes formula, host CPU: {model}"}
 
 
 def main():
@@ -251,7 +284,7 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default=None,
-                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4")
+                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | traffic")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -263,6 +296,9 @@ def main():
     gen = torch.Generator().manual_seed(0)
     with torch.inference_mode():
         only = args.only
+        if only == "traffic":
+            traffic_pass(gen)
+            return
         res = {}
         if only in (None, "config0"):
             res["config0"] = bench_config0(args, gen)
@@ -290,11 +326,13 @@ def main():
                    "global_batch": 4, "seq_len": 1, "parallelism": "single GPU"},
     }
     if c0:
-        line["roofline"] = {"bound": "hbm", "achieved": round(c0["kernel_GBps"], 2),
+        # one decode-kernel launch per call: launch duration = time per call
+        line["roofline"] = {"bound": "hbm", "achieved": round(c0["GBps"], 2),
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(c0["kernel_GBps"] / HBM_PEAK_GBS, 4),
-                            "traffic": None,
-                            "kernel": "woq_decode_kernel", "kernel_avg_us": round(c0["kernel_avg_s"] * 1e6, 3),
+                            "frac": round(c0["GBps"] / HBM_PEAK_GBS, 4),
+                            "traffic": read_traffic(),
+                            "kernel": "woq_decode_kernel",
+                            "kernel_avg_us": round(c0["s_per_call"] * 1e6, 3),
                             "algorithmic_bytes": c0["bytes_per_call"]}
     if not args.no_cpu_baseline and only in (None, "config0"):
         line["cpu_baseline"] = cpu_baseline()
