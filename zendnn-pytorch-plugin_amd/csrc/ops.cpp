@@ -53,9 +53,10 @@ hipStream_t current_stream() {
   return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
 }
 
-// Per-(device, stream) workspace.  Its first bytes hold split-K tile
-// counters that every completed call leaves at zero, so a buffer is zeroed
-// once when it is created and then reused by calls on the same stream.
+// Per-(device, stream) workspace (the dynamic path's quantised activations
+// and row scales).  Calls on one stream are ordered, so they can share it;
+// a larger request replaces the buffer (the old one is freed through the
+// caching allocator, stream-ordered).
 struct WorkspaceCache {
   std::mutex mu;
   std::map<std::pair<int, hipStream_t>, at::Tensor> bufs;
