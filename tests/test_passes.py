@@ -1,0 +1,310 @@
+"""Graph-pass tests on the CPU: the WOQ op replacement and the post-op
+fusions rewrite the subgraphs the reference's passes rewrite
+(src/cpu/python/zentorch/_op_replacements_new.py:316-799,
+_woq_linear_unary_fusion.py, _woq_linear_binary_binary_fusion.py) and leave
+everything else alone.
+
+Graphs are traced with make_fx over Inductor's decomposition table on fake
+tensors, which is the form the post-grad passes see; the zentorch ops only
+run their Meta kernels here.  The passes rewrite GPU subgraphs only, so the
+tests add "cpu" to the pass devices; one test checks that a CPU graph is
+left alone by default.  Numerics of compiled models are GPU tests
+(test_compile_gpu.py).
+"""
+import pytest
+import torch
+from torch._inductor.decomposition import select_decomp_table
+from torch.fx.experimental.proxy_tensor import make_fx
+
+import zentorch
+from zentorch import _utils
+from zentorch._optimize import optimize
+from zentorch._utils import counters
+
+aten = torch.ops.aten
+zt = torch.ops.zentorch
+
+
+@pytest.fixture
+def cpu_passes(monkeypatch):
+    monkeypatch.setattr(_utils, "PASS_DEVICE_TYPES", ("cuda", "cpu"))
+    counters.clear()
+    yield
+    counters.clear()
+
+
+def trace(fn, *args):
+    gm = make_fx(fn, decomposition_table=select_decomp_table(), tracing_mode="fake")(*args)
+    # Inductor removes dead nodes before its passes; the decompositions leave
+    # some (unused dtype casts) that would add users to pattern nodes.
+    gm.graph.eliminate_dead_code()
+    gm.recompile()
+    return gm
+
+
+def targets(gm):
+    return [n.target for n in gm.graph.nodes if n.op == "call_function"]
+
+
+def run_passes(gm):
+    optimize(gm.graph)
+    gm.recompile()
+    return targets(gm)
+
+
+def quantized(N, K, gs=None, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    if gs is None:
+        w = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int8)
+        zp = torch.zeros(N, 1, dtype=torch.int8)
+        s = (torch.rand(N, 1, generator=g) * 0.01 + 0.005).bfloat16()
+    else:
+        w = torch.randint(-8, 8, (N, K // gs, gs), generator=g, dtype=torch.int8)
+        zp = torch.zeros(N, K // gs, 1, dtype=torch.int8)
+        s = (torch.rand(N, K // gs, 1, generator=g) * 0.01 + 0.005).bfloat16()
+    return w, zp, s
+
+
+def dequant_t(w, zp, s, view=None):
+    # woq_test_utils.py:62-74 of the reference: (bf16(w) - bf16(zp)) * s [-> view] -> permute
+    dq = (w.to(torch.bfloat16) - zp.to(torch.bfloat16)) * s
+    if view is not None:
+        dq = dq.view(view)
+    return dq.permute(1, 0)
+
+
+# ---------------------------------------------------------------- replacement
+@pytest.mark.parametrize("gs", [None, 128])
+@pytest.mark.parametrize("bias", [False, True])
+def test_dequant_matmul_replaced(cpu_passes, gs, bias):
+    N, K = 64, 256
+    w, zp, s = quantized(N, K, gs)
+    x = torch.randn(4, K).bfloat16()
+    b = torch.randn(N).bfloat16()
+    view = (N, K) if gs else None
+
+    def f(x, w, zp, s, b):
+        d = dequant_t(w, zp, s, view)
+        return torch.addmm(b, x, d) if bias else torch.mm(x, d)
+
+    gm = trace(f, x, w, zp, s, b)
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
+    assert zt.zentorch_woq_linear.default in t and zt.zentorch_woq_repack_weight.default in t
+    assert aten.mm.default not in t and aten.addmm.default not in t
+    node = next(n for n in gm.graph.nodes if n.target == zt.zentorch_woq_linear.default)
+    # operands: x, [K/8, N] packed view, [G, N] scales, zp dropped, bias
+    assert tuple(node.args[1].meta["val"].shape) == (K // 8, N)
+    assert tuple(node.args[2].meta["val"].shape) == ((K // gs) if gs else 1, N)
+    assert node.args[3] is None
+    assert (len(node.args) > 4 and node.args[4] is not None) == bias
+
+
+def test_per_group_reshape_form_replaced(cpu_passes):
+    # Inductor can turn the per-group view into reshape before the pass runs
+    N, K = 64, 256
+    w, zp, s = quantized(N, K, 128)
+    x = torch.randn(2, K).bfloat16()
+    gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s, (N, K))), x, w, zp, s)
+    for n in gm.graph.nodes:
+        if n.target == aten.view.default:
+            n.target = aten.reshape.default
+    gm.recompile()
+    run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
+
+
+def test_cpu_graph_left_alone_by_default():
+    counters.clear()
+    w, zp, s = quantized(64, 256)
+    x = torch.randn(4, 256).bfloat16()
+    gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)), x, w, zp, s)
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 0
+    assert aten.mm.default in t
+
+
+def test_not_a_transpose_or_bad_shapes_left_alone(cpu_passes):
+    N, K = 64, 256
+    w, zp, s = quantized(N, K)
+    x = torch.randn(4, K).bfloat16()
+    # scales per input column instead of per output row
+    s_bad = (torch.rand(1, K) * 0.01).bfloat16()
+    gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)), x, w, zp, s_bad)
+    run_passes(gm)
+    # K not a multiple of 8
+    w2, zp2, s2 = quantized(16, 12)
+    gm2 = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)),
+                torch.randn(3, 12).bfloat16(), w2, zp2, s2)
+    run_passes(gm2)
+    # int32 "weights" are not the int8 pattern
+    gm3 = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)), torch.randn(4, K).bfloat16(),
+                w.int(), zp, s)
+    run_passes(gm3)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 0
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_int4pack_mm_replaced(cpu_passes, bias):
+    N, K, gs = 64, 256, 128
+    q = torch.randint(0, 16, (N, K), dtype=torch.int32)
+    packed = torch.ops.aten._convert_weight_to_int4pack_for_cpu(q, 1)
+    sz = torch.rand(K // gs, N, 2).bfloat16()
+    x = torch.randn(4, K).bfloat16()
+    b = torch.randn(N).bfloat16()
+
+    def f(x, packed, sz, b):
+        y = torch.ops.aten._weight_int4pack_mm_for_cpu(x, packed, gs, sz)
+        return y + b if bias else y
+
+    gm = trace(f, x, packed, sz, b)
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
+    assert zt.zentorch_woq_repack_from_int4pack.default in t
+    node = next(n for n in gm.graph.nodes if n.target == zt.zentorch_woq_linear.default)
+    assert node.args[3] is not None  # tinygemm zero points passed through
+    assert (len(node.args) > 4 and node.args[4] is not None) == bias
+    assert aten.add.Tensor not in t
+
+
+# ------------------------------------------------------------------ fusions
+def woq_inputs(M=4, N=64, K=256, gs=128, dtype=torch.bfloat16):
+    x = torch.randn(M, K).to(dtype)
+    wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), dtype=torch.int32).t()
+    s = torch.rand(K // gs, N).bfloat16()
+    return x, wp, s
+
+
+def _woq(x, wp, s, b=None):
+    return zt.zentorch_woq_linear(x, wp, s, None, b)
+
+
+@pytest.mark.parametrize("act,op", [
+    (lambda y: torch.nn.functional.gelu(y), "gelu_erf"),
+    (lambda y: torch.nn.functional.gelu(y, approximate="tanh"), "gelu_tanh"),
+    (torch.relu, "relu"),
+    (torch.sigmoid, "sigmoid"),
+])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_unary_fusions(cpu_passes, act, op, bias, dtype):
+    x, wp, s = woq_inputs(dtype=dtype)
+    b = torch.randn(wp.shape[1]).to(dtype)
+    gm = trace(lambda x, wp, s, b: act(_woq(x, wp, s, b if bias else None)), x, wp, s, b)
+    t = run_passes(gm)
+    key = f"zentorch_woq_linear_{op}"
+    assert counters["zentorch"][key] == 1, dict(counters["zentorch"])
+    assert getattr(zt, key).default in t and zt.zentorch_woq_linear.default not in t
+    # nothing of the activation is left
+    assert not {aten.erf.default, aten.tanh.default, aten.sigmoid.default,
+                aten.relu.default, aten.gelu.default} & set(t)
+
+
+def test_gelu_tanh_not_taken_for_erf(cpu_passes):
+    x, wp, s = woq_inputs()
+    gm = trace(lambda x, wp, s: torch.nn.functional.gelu(_woq(x, wp, s), approximate="tanh"), x, wp, s)
+    run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear_gelu_erf"] == 0
+    assert counters["zentorch"]["zentorch_woq_linear_gelu_tanh"] == 1
+
+
+@pytest.mark.parametrize("order", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_silu_mul_fusion(cpu_passes, order, dtype):
+    x, wp, s = woq_inputs(dtype=dtype)
+    up = torch.randn(x.shape[0], wp.shape[1]).to(dtype)
+
+    def f(x, wp, s, up):
+        g = torch.nn.functional.silu(_woq(x, wp, s))
+        return g * up if order == 0 else up * g
+
+    gm = trace(f, x, wp, s, up)
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear_silu_mul"] == 1
+    node = next(n for n in gm.graph.nodes if n.target == zt.zentorch_woq_linear_silu_mul.default)
+    assert node.args[4].name.startswith("up")
+    assert aten.mul.Tensor not in t
+
+
+def test_llama_mlp_gate_up_down(cpu_passes):
+    # down(silu(gate(x)) * up(x)) + residual: silu_mul on gate, plain up,
+    # residual add fused into down
+    x, wg, s = woq_inputs(N=128)
+    _, wu, _ = woq_inputs(N=128)
+    wd = torch.randint(-2 ** 31, 2 ** 31 - 1, (64, 128 // 8), dtype=torch.int32).t()
+    sd = torch.rand(1, 64).bfloat16()
+    res = torch.randn(4, 64).bfloat16()
+
+    def mlp(x, wg, wu, s, wd, sd, res):
+        h = torch.nn.functional.silu(_woq(x, wg, s)) * _woq(x, wu, s)
+        return _woq(h, wd, sd) + res
+
+    gm = trace(mlp, x, wg, wu, s, wd, sd, res)
+    t = run_passes(gm)
+    c = counters["zentorch"]
+    assert c["zentorch_woq_linear_silu_mul"] == 1 and c["zentorch_woq_linear_add"] == 1
+    assert t.count(zt.zentorch_woq_linear.default) == 1  # the up projection
+
+
+@pytest.mark.parametrize("inner,op", [("add", "add_add"), ("mul", "mul_add")])
+@pytest.mark.parametrize("order", range(4))
+@pytest.mark.parametrize("bias", [False, True])
+def test_binary_binary_fusions(cpu_passes, inner, op, order, bias):
+    x, wp, s = woq_inputs()
+    b = torch.randn(wp.shape[1]).bfloat16()
+    a1 = torch.randn(x.shape[0], wp.shape[1]).bfloat16()
+    a2 = torch.randn(x.shape[0], wp.shape[1]).bfloat16()
+    f_in = (lambda p, q: p + q) if inner == "add" else (lambda p, q: p * q)
+
+    def f(x, wp, s, b, a1, a2):
+        y = _woq(x, wp, s, b if bias else None)
+        t = f_in(y, a1) if order in (0, 2) else f_in(a1, y)
+        return t + a2 if order in (0, 1) else a2 + t
+
+    gm = trace(f, x, wp, s, b, a1, a2)
+    t = run_passes(gm)
+    key = f"zentorch_woq_linear_{op}"
+    assert counters["zentorch"][key] == 1, dict(counters["zentorch"])
+    node = next(n for n in gm.graph.nodes if n.target == getattr(zt, key).default)
+    # buffer order of the fused op: inner operand, then outer operand
+    assert node.args[4].name.startswith("a1") and node.args[5].name.startswith("a2")
+    assert (len(node.args) > 6 and node.args[6] is not None) == bias
+    assert aten.add.Tensor not in t and aten.mul.Tensor not in t
+
+
+def test_broadcast_or_promoting_operands_not_fused(cpu_passes):
+    x, wp, s = woq_inputs()
+    row = torch.randn(wp.shape[1]).bfloat16()            # broadcast
+    full32 = torch.randn(x.shape[0], wp.shape[1])        # fp32 -> promotes
+    gm = trace(lambda x, wp, s, r, f: (_woq(x, wp, s) + r, _woq(x, wp, s) + f),
+               x, wp, s, row, full32)
+    run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear_add"] == 0
+
+
+def test_compile_backend_runs_the_passes(cpu_passes):
+    # torch.compile(backend="zentorch") rewrites the graph; on the CPU the
+    # rewritten graph then fails loudly (no CPU kernels), which shows that
+    # nothing falls back to a CPU implementation.
+    import torch._dynamo
+
+    torch._dynamo.reset()
+    N, K = 64, 256
+    w, zp, s = quantized(N, K, 128)
+    x = torch.randn(4, K).bfloat16()
+
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.register_buffer("w", w)
+            self.register_buffer("zp", zp)
+            self.register_buffer("s", s)
+
+        def forward(self, x):
+            return torch.mm(x, dequant_t(self.w, self.zp, self.s, (N, K)))
+
+    with pytest.raises(Exception, match="zentorch|NotImplemented|CPU"):
+        with torch.no_grad():
+            torch.compile(M(), backend="zentorch")(x)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
+    torch._dynamo.reset()

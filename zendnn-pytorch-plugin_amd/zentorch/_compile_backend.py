@@ -1,47 +1,112 @@
 """The ``"zentorch"`` torch.compile backend.
 
-As in the reference (src/cpu/python/zentorch/_compile_backend.py:19-95) the
-backend installs the zentorch graph passes as Inductor's
-``joint_custom_post_pass`` and hands the FX graph to ``compile_fx``.  The
-reference's CPU-only pre-passes (mkldnn conv fusion, :79-84) have no GPU
-counterpart and are not run.
+The reference's backend (src/cpu/python/zentorch/_compile_backend.py:19-95)
+installs the zentorch graph passes as Inductor's ``joint_custom_post_pass``
+and compiles the rest of the graph with Inductor's CPU code generation.  On
+MI355X the hot ops are the hand-written HIP kernels, so this backend keeps
+Inductor's front half and drops its code generation:
+
+1. AOT autograd traces the dynamo graph to aten ops with Inductor's
+   decomposition table (the graph form the reference's patterns are written
+   against: ``prims.convert_element_type``, decomposed GELU/SiLU, ...);
+2. the WOQ replacement and fusion passes rewrite it (``optimize``);
+3. repacks (and the scale copies) of module parameters and buffers go
+   through the packed-weight cache (``_weight_cache``), so a forward
+   repacks a weight only when it changed;
+4. the rewritten graph runs op by op: the zentorch ops on their HIP
+   kernels, everything else on PyTorch's own kernels.  No Triton code is
+   generated.  Launch-bound callers capture the compiled forward in a HIP
+   graph (``torch.cuda.CUDAGraph``).
+
+The passes only rewrite GPU subgraphs; a CPU graph runs unchanged.
 """
-import base64
 from typing import Any, Callable, List
 
 import torch
 from torch._dynamo import register_backend
-from torch._inductor import config
-from torch._inductor.compile_fx import compile_fx
-from torch._inductor.custom_graph_pass import CustomGraphPass, get_hash_for_files
+from torch._functorch.aot_autograd import aot_module_simplified, make_boxed_func
+from torch._inductor.decomposition import select_decomp_table
 
 from ._logging import get_logger
 from ._optimize import optimize
+from ._weight_cache import cached_clone, cached_repack_from_int4pack, cached_repack_weight
 
 logger = get_logger(__name__)
 
+_CACHED = {
+    torch.ops.zentorch.zentorch_woq_repack_weight.default: cached_repack_weight,
+    torch.ops.zentorch.zentorch_woq_repack_from_int4pack.default: cached_repack_from_int4pack,
+    # the [G, N] scale / zero-point copies the replacement makes
+    torch.ops.aten.clone.default: cached_clone,
+}
 
-class OptimizePass(CustomGraphPass):
-    def __call__(self, graph: torch.fx.Graph):
-        optimize(graph)
-
-    def uuid(self) -> Any:
-        # Inductor's FX-graph cache keys on this: hash the pass sources.
-        import os
-        here = os.path.dirname(os.path.abspath(__file__))
-        files = tuple(os.path.join(here, f) for f in (
-            "_optimize.py", "_op_replacements_new.py",
-            "_woq_linear_unary_fusion.py", "_woq_linear_binary_binary_fusion.py"))
-        return base64.b64encode(get_hash_for_files(files)).decode()
+# aten ops that return a view of their first operand without copying
+_VIEW_OPS = {
+    torch.ops.aten.view.default, torch.ops.aten._unsafe_view.default,
+    torch.ops.aten.permute.default, torch.ops.aten.t.default,
+    torch.ops.aten.transpose.int, torch.ops.aten.alias.default,
+    torch.ops.aten.select.int, torch.ops.aten.slice.Tensor,
+}
 
 
-optimize_pass = OptimizePass()
+def _weight_placeholders(graph: torch.fx.Graph) -> set:
+    """Placeholders that carry module parameters or buffers: AOT autograd
+    marks them static (the same tensors on every call)."""
+    ctx = torch._guards.TracingContext.try_get()
+    idx = getattr(getattr(ctx, "fw_metadata", None), "static_input_indices", None) or []
+    ph = [n for n in graph.nodes if n.op == "placeholder"]
+    return {ph[i] for i in idx if i < len(ph)}
+
+
+def _from_weight(node: torch.fx.Node, weights: set) -> bool:
+    """True if ``node`` is a weight placeholder or a view chain of one."""
+    while node.op == "call_function" and node.target in _VIEW_OPS:
+        node = node.args[0]
+    return node in weights
+
+
+def _only_feeds_zentorch_ops(node: torch.fx.Node) -> bool:
+    """True if every use of ``node`` (through views) is an operand of a
+    zentorch op, so a cached tensor never leaves the graph where a caller
+    could modify it."""
+    for user in node.users:
+        if user.op == "call_function" and user.target in _VIEW_OPS:
+            if not _only_feeds_zentorch_ops(user):
+                return False
+        elif not (user.op == "call_function"
+                  and getattr(user.target, "namespace", None) == "zentorch"):
+            return False
+    return True
+
+
+def use_weight_cache(graph: torch.fx.Graph, weights: set) -> int:
+    """Route repacks (and contiguous copies) of module weights through the
+    packed-weight cache.  Other inputs change from call to call and are
+    never cached."""
+    n = 0
+    for node in graph.nodes:
+        if node.op == "call_function" and node.target in _CACHED \
+                and _from_weight(node.args[0], weights) and _only_feeds_zentorch_ops(node):
+            node.target = _CACHED[node.target]
+            n += 1
+    return n
+
+
+def _compile_forward(gm: torch.fx.GraphModule, example_inputs: List[Any]) -> Callable:
+    weights = _weight_placeholders(gm.graph)
+    optimize(gm.graph)
+    cached = use_weight_cache(gm.graph, weights)
+    gm.graph.eliminate_dead_code()
+    gm.recompile()
+    logger.info("zentorch graph ready (%d cached weight transforms)", cached)
+    return make_boxed_func(gm.forward)
 
 
 def zentorch_compile(gm: torch.fx.GraphModule, example_inputs: List[torch.Tensor]) -> Callable:
     logger.info("Called the zentorch backend.")
-    config.joint_custom_post_pass = optimize_pass
-    return compile_fx(gm, example_inputs)
+    return aot_module_simplified(
+        gm, example_inputs, fw_compiler=_compile_forward,
+        decompositions=select_decomp_table(), keep_inference_input_mutations=True)
 
 
 @register_backend

@@ -22,3 +22,23 @@ def _dump_counters():
 
 
 atexit.register(_dump_counters)
+
+
+def tensor_meta(node):
+    """The example value (FakeTensor) an FX node carries, or None."""
+    import torch
+
+    if not isinstance(node, torch.fx.Node):
+        return None
+    val = node.meta.get("val", None)
+    return val if isinstance(val, torch.Tensor) else None
+
+
+# Device types the graph passes rewrite for.  The ops have kernels for the
+# GPU only, so a subgraph on any other device is left to stock torch.
+PASS_DEVICE_TYPES = ("cuda",)
+
+
+def on_gpu(*vals):
+    """True if every example tensor lives on a device the ops run on."""
+    return all(v is not None and v.device.type in PASS_DEVICE_TYPES for v in vals)
