@@ -11,6 +11,8 @@
 //    y = ((float)acc * sx[m]) * sw[n] + bias[n] (+ post-ops), or the raw
 //    int32 accumulators.
 //  * s8_generic_kernel    K not a multiple of 16: one wave per output.
+#include <cstdlib>
+
 #include "zt_launch.hpp"
 
 namespace zt {
@@ -140,6 +142,204 @@ __global__ __launch_bounds__(256) void s8_gemm_kernel(DynArgs a) {
       }
 }
 
+// Large-M int8 GEMM.  A BM x BN output tile walks K in steps of BK = 128
+// with 4 waves (2 x 2), each owning a (BM/2) x (BN/2) sub-tile of
+// WTM x WTN 16x16x64 MFMAs.  LDS holds two stages of the qx [BM, BK] and
+// W [BN, BK] slabs (rows padded to 144 B); while a step computes from one
+// stage, every thread's 16-byte chunks of the next step are already in
+// flight into registers (raw buffer loads: rows past M/N and columns past
+// K read as zero), and are written to the other stage before the step's
+// single barrier.  Tiles are ordered in groups of GM m-tiles (so a group
+// reuses the same W tiles) and each XCD takes one contiguous range of that
+// order, so the tiles sharing W and qx rows share an L2.
+constexpr int kTBK = 128;
+constexpr int kTLDR = kTBK + 16;
+
+// int32 row pitch of the accumulator tile staged in LDS for the epilogue
+template <int BN>
+constexpr int acc_pitch() { return BN + 4; }
+
+template <int BM, int BN>
+constexpr size_t s8_tiled_lds() {
+  const size_t stages = 2 * (size_t)(BM + BN) * kTLDR;
+  const size_t acc = (size_t)BM * acc_pitch<BN>() * 4;
+  return stages > acc ? stages : acc;
+}
+
+// Epilogue of four consecutive columns n..n+3 of row m: one 8/16-byte store
+// when the row has them all, element by element otherwise.
+__device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i32x4_t v) {
+  const int N = (int)a.N;
+  if (n + 3 < N && (N & 3) == 0) {
+    if (a.y_dt == ZT_DT_S32) {
+      *reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(a.y) + (int64_t)m * N + n) = v;
+      return;
+    }
+    float f[4];
+    const float sxm = a.sx[m];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = (float)v[r] * sxm;
+      t = t * load_elem(a.sw, a.sw_dt, n + r);
+      if (a.bias) t = t + load_elem(a.bias, a.b_dt, n + r);
+      f[r] = apply_post_ops(t, a.post, m, n + r);
+    }
+    if (a.y_dt == ZT_DT_BF16) {
+      u32x2_t p;
+      p[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+      p[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = p;
+      return;
+    }
+    if (a.y_dt == ZT_DT_F32) {
+      *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
+          f32x4_t{f[0], f[1], f[2], f[3]};
+      return;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (n + r < N) dyn_epilogue(a, m, n + r, v[r]);
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void s8_gemm_tiled_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
+  constexpr int WTM = BM / 32, WTN = BN / 32;
+  constexpr int ACH = BM * (kTBK / 16) / 256, BCH = BN * (kTBK / 16) / 256;
+  constexpr int STAGE = (BM + BN) * kTLDR;
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // grouped tile order, contiguous per XCD
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const auto a_rs = make_rsrc(a.qx, (uint32_t)((int64_t)M * K));
+  const auto b_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+
+  // this thread's 16-byte chunks: row = idx / 8, column chunk = idx % 8
+  uint32_t a_off[ACH], b_off[BCH];
+  int a_col[ACH], b_col[BCH];
+#pragma unroll
+  for (int c = 0; c < ACH; ++c) {
+    const int idx = tid + 256 * c, row = idx >> 3;
+    a_col[c] = (idx & 7) * 16;
+    a_off[c] = m0 + row < M ? (uint32_t)((m0 + row) * K + a_col[c]) : kOobOffset;
+  }
+#pragma unroll
+  for (int c = 0; c < BCH; ++c) {
+    const int idx = tid + 256 * c, row = idx >> 3;
+    b_col[c] = (idx & 7) * 16;
+    b_off[c] = n0 + row < N ? (uint32_t)((n0 + row) * K + b_col[c]) : kOobOffset;
+  }
+
+  u32x4_t ra[ACH], rb[BCH];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      const uint32_t off = (a_off[c] == kOobOffset || k0 + a_col[c] >= K) ? kOobOffset
+                                                                         : a_off[c] + k0;
+      ra[c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, off, 0, 0));
+    }
+#pragma unroll
+    for (int c = 0; c < BCH; ++c) {
+      const uint32_t off = (b_off[c] == kOobOffset || k0 + b_col[c] >= K) ? kOobOffset
+                                                                         : b_off[c] + k0;
+      rb[c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, off, 0, 0));
+    }
+  };
+  auto swrite = [&](int stage) {
+    int8_t *base = s8_smem + stage * STAGE;
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      const int idx = tid + 256 * c;
+      *reinterpret_cast<u32x4_t *>(base + (idx >> 3) * kTLDR + (idx & 7) * 16) = ra[c];
+    }
+#pragma unroll
+    for (int c = 0; c < BCH; ++c) {
+      const int idx = tid + 256 * c;
+      *reinterpret_cast<u32x4_t *>(base + (BM + (idx >> 3)) * kTLDR + (idx & 7) * 16) = rb[c];
+    }
+  };
+
+  i32x4_t acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) acc[i][j] = i32x4_t{0, 0, 0, 0};
+
+  const int nk = (K + kTBK - 1) / kTBK;
+  gload(0);
+  swrite(0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ++ks) {
+    const int cur = ks & 1;
+    if (ks + 1 < nk) gload((ks + 1) * kTBK);
+    const int8_t *As = s8_smem + cur * STAGE + (wm * (BM / 2) + lr) * kTLDR + 16 * lg;
+    const int8_t *Bs = s8_smem + cur * STAGE + (BM + wn * (BN / 2) + lr) * kTLDR + 16 * lg;
+    // both 64-wide halves of the step's fragments are read up front, so the
+    // second half's LDS reads overlap the first half's MFMAs
+    i32x4_t Af[2][WTM], Bf[2][WTN];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        Bf[kk][j] = *reinterpret_cast<const i32x4_t *>(Bs + j * 16 * kTLDR + kk * 64);
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+        Af[kk][i] = *reinterpret_cast<const i32x4_t *>(As + i * 16 * kTLDR + kk * 64);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Af[kk][i], Bf[kk][j], acc[i][j],
+                                                             0, 0, 0);
+    if (ks + 1 < nk) swrite(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Stage the accumulator tile in LDS (static register indices only, so
+  // acc stays in registers), then write rows of four columns per thread.
+  constexpr int AP = acc_pitch<BN>();
+  int32_t *tile = reinterpret_cast<int32_t *>(s8_smem);
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * AP + wn * (BN / 2) + j * 16 + lr] =
+            acc[i][j][r];
+  __syncthreads();
+  for (int idx = tid; idx < BM * (BN / 4); idx += 256) {
+    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c4;
+    if (m < M && n < N)
+      dyn_epilogue4(a, m, n, *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4));
+  }
+}
+
+template <int BM, int BN>
+hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  s8_gemm_tiled_kernel<BM, BN><<<dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                                  s8_tiled_lds<BM, BN>(), s>>>(a, tiles_m, tiles_n, group_m);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
@@ -158,6 +358,16 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
     const int64_t blocks = (a.M * a.N + 3) / 4;
     hipLaunchKernelGGL(s8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
     return hipGetLastError();
+  }
+  // the tiled kernel addresses qx and W with 32-bit byte offsets
+  const bool fits32 = a.M * a.K < (int64_t)kOobOffset && a.N * a.K < (int64_t)kOobOffset;
+  const char *force = std::getenv("ZT_S8_FORCE");
+  const bool tiled = force ? force[0] == 't' : a.M >= 256;
+  if (tiled && fits32) {
+    const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
+    const char *tile = std::getenv("ZT_S8_TILE");
+    const bool big = tile ? tile[0] == '2' : t256 >= 256;
+    return big ? launch_s8_tiled<256, 128>(a, s) : launch_s8_tiled<128, 128>(a, s);
   }
   if (a.M <= 64) {
     dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 63) / 64));

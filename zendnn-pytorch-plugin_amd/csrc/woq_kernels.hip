@@ -143,12 +143,6 @@ __host__ __device__ inline size_t decode_slab_bytes(int NK, int NT, int TPW, int
   return (size_t)NK * NT * TPW * 16 * (16 * mt + 1) * sizeof(float);
 }
 
-// gfx9 raw buffer resource: 32-bit offsets from one SGPR base, hardware
-// range check (reads past num_records return 0).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
-}
-
 // Decode GEMV / skinny GEMM (M <= 32).
 //
 // Grid: one workgroup per row block of NT*TPW 16-row tiles, covering all of

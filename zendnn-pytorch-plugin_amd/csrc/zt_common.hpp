@@ -91,4 +91,22 @@ __device__ __forceinline__ float apply_post_ops(float v, const PostOps &p,
   return v;
 }
 
+// gfx9 raw buffer resource: 32-bit offsets from one SGPR base, hardware
+// range check (reads at offsets >= bytes return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+
+// An offset every raw buffer load treats as out of range (returns 0).
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs
+// on XCD b % 8, each with its own L2).  Map b to a tile index so that each
+// XCD works on one contiguous range of the n tiles.
+__device__ __forceinline__ int xcd_contiguous_tile(int b, int n) {
+  const int q = n >> 3, r = n & 7;
+  const int x = b & 7, i = b >> 3;
+  return x * q + (x < r ? x : r) + i;
+}
+
 }  // namespace zt
