@@ -331,6 +331,160 @@ void s8_gemm_tiled_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
   }
 }
 
+// The same tiling with the K slabs moved by the buffer unit straight into
+// LDS (buffer_load_dwordx4 ... lds, range-checked like the register loads),
+// S stages deep.  LDS rows are 128 B with no padding; the 16-byte chunk c
+// of row r sits at position c ^ (r & 7), so one wave's 1 KB load fills 8
+// whole rows and a fragment read (16 rows, one chunk) touches every bank
+// once per 8 rows.  Each step first reads all its fragments into registers,
+// then starts the loads of step ks + S - 1 into the stage read one step
+// earlier, then runs its MFMAs; only the loads of step ks + 1 are waited for
+// before the barrier.
+template <int BM, int BN, int S>
+constexpr size_t s8_dma_lds() {
+  const size_t stages = (size_t)S * (BM + BN) * kTBK;
+  const size_t acc = (size_t)BM * acc_pitch<BN>() * 4;
+  return stages > acc ? stages : acc;
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void s8_gemm_dma_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
+  constexpr int WTM = BM / 32, WTN = BN / 32;
+  constexpr int STAGE = (BM + BN) * kTBK;
+  constexpr int GROUPS = (BM + BN) / 8;      // 8-row groups per stage
+  constexpr int GPW = GROUPS / 4;            // per wave
+  static_assert(GROUPS % 4 == 0, "row groups must split over 4 waves");
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave index as a scalar, so the row groups (and A/B choice) are uniform
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const auto a_rs = make_rsrc(a.qx, (uint32_t)((int64_t)M * K));
+  const auto b_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+
+  // lane's source for each of the wave's row groups: row (group*8 + lane/8),
+  // logical chunk (lane%8) ^ (lane/8)
+  const int lrow = lane >> 3, lchunk = ((lane & 7) ^ lrow) * 16;
+  uint32_t src[GPW];
+  bool is_a[GPW];
+#pragma unroll
+  for (int q = 0; q < GPW; ++q) {
+    const int grp = wv * GPW + q;
+    const int row = grp * 8 + lrow;
+    is_a[q] = grp * 8 < BM;  // whole groups lie in A or in B
+    if (is_a[q])
+      src[q] = m0 + row < M ? (uint32_t)((m0 + row) * K + lchunk) : kOobOffset;
+    else
+      src[q] = n0 + row - BM < N ? (uint32_t)((n0 + row - BM) * K + lchunk) : kOobOffset;
+  }
+  auto dma = [&](int step) {
+    const int k0 = step * kTBK;
+    int8_t *stage = s8_smem + (step % S) * STAGE;
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) {
+      const uint32_t off = (src[q] == kOobOffset || k0 + lchunk >= K) ? kOobOffset : src[q] + k0;
+      lds_ptr_t dst = (lds_ptr_t)(stage + (wv * GPW + q) * 1024);
+      if (is_a[q])
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, dst, 16, off, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, dst, 16, off, 0, 0, 0);
+    }
+  };
+
+  i32x4_t acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) acc[i][j] = i32x4_t{0, 0, 0, 0};
+
+  const int nk = (K + kTBK - 1) / kTBK;
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p)
+    if (p < nk) dma(p);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // fragment rows of this lane: A rows wm*BM/2 + i*16 + lr, B rows likewise;
+  // row & 7 == lr & 7 for every i, j
+  const int sw = lr & 7;
+  for (int ks = 0; ks < nk; ++ks) {
+    const int8_t *stage = s8_smem + (ks % S) * STAGE;
+    const int8_t *As = stage + (wm * (BM / 2) + lr) * kTBK;
+    const int8_t *Bs = stage + (BM + wn * (BN / 2) + lr) * kTBK;
+    i32x4_t Af[2][WTM], Bf[2][WTN];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int pos = (((kk * 4 + lg) ^ sw) * 16);
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        Bf[kk][j] = *reinterpret_cast<const i32x4_t *>(Bs + j * 16 * kTBK + pos);
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+        Af[kk][i] = *reinterpret_cast<const i32x4_t *>(As + i * 16 * kTBK + pos);
+    }
+    if (ks + S - 1 < nk) dma(ks + S - 1);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Af[kk][i], Bf[kk][j], acc[i][j],
+                                                             0, 0, 0);
+    // keep the MFMAs ahead of the wait (the scheduler would otherwise hoist
+    // the wait and barrier above them and expose the load latency)
+    __builtin_amdgcn_sched_barrier(0);
+    // the loads of step ks + 1 have landed once at most the GPW loads issued
+    // this step are outstanding
+    if (S > 2 && ks + S - 1 < nk)
+      __builtin_amdgcn_s_waitcnt((GPW & 15) | ((GPW >> 4) << 14) | (7 << 4) | (15 << 8));
+    else
+      __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  constexpr int AP = acc_pitch<BN>();
+  int32_t *tile = reinterpret_cast<int32_t *>(s8_smem);
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * AP + wn * (BN / 2) + j * 16 + lr] =
+            acc[i][j][r];
+  __syncthreads();
+  for (int idx = tid; idx < BM * (BN / 4); idx += 256) {
+    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c4;
+    if (m < M && n < N)
+      dyn_epilogue4(a, m, n, *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4));
+  }
+}
+
+template <int BM, int BN, int S>
+hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  s8_gemm_dma_kernel<BM, BN, S><<<dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                                  s8_dma_lds<BM, BN, S>(), s>>>(a, tiles_m, tiles_n, group_m);
+  return hipGetLastError();
+}
+
 template <int BM, int BN>
 hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
@@ -364,10 +518,17 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
   const char *force = std::getenv("ZT_S8_FORCE");
   const bool tiled = force ? force[0] == 't' : a.M >= 256;
   if (tiled && fits32) {
+    // 256x128 tiles once there are half a round of them (measured on the
+    // Llama prefill shapes: 2-stage DMA 256x128 is fastest from M = 2048 up)
     const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
     const char *tile = std::getenv("ZT_S8_TILE");
-    const bool big = tile ? tile[0] == '2' : t256 >= 256;
-    return big ? launch_s8_tiled<256, 128>(a, s) : launch_s8_tiled<128, 128>(a, s);
+    const bool big = tile ? tile[0] == '2' : t256 >= 128;
+    const char *kind = std::getenv("ZT_S8_KIND");  // r: register staging, 2/3: DMA stages
+    if (kind && kind[0] == 'r')
+      return big ? launch_s8_tiled<256, 128>(a, s) : launch_s8_tiled<128, 128>(a, s);
+    if (kind && kind[0] == '3')
+      return big ? launch_s8_dma<256, 128, 3>(a, s) : launch_s8_dma<128, 128, 3>(a, s);
+    return big ? launch_s8_dma<256, 128, 2>(a, s) : launch_s8_dma<128, 128, 2>(a, s);
   }
   if (a.M <= 64) {
     dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 63) / 64));
