@@ -48,7 +48,9 @@ def test_quantize_bit_exact(M, K, x_dtype):
 @pytest.mark.parametrize("M,N,K", [(1, 8, 16), (5, 33, 48), (64, 96, 256), (128, 11008, 4096),
                                    (300, 130, 512), (2048, 256, 1024), (4, 17, 12),
                                    # large-M tiled kernel: ragged M, N and K % 128 != 0
-                                   (257, 200, 144), (520, 4160, 272), (1024, 1000, 2064)])
+                                   (257, 200, 144), (520, 4160, 272), (1024, 1000, 2064),
+                                   # skinny weight-streaming kernel: ragged N, K % 64 != 0
+                                   (33, 100, 4112), (100, 4100, 272), (17, 50, 80)])
 def test_s8_gemm_accumulators_bit_exact(M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)

@@ -11,6 +11,7 @@
 //    y = ((float)acc * sx[m]) * sw[n] + bias[n] (+ post-ops), or the raw
 //    int32 accumulators.
 //  * s8_generic_kernel    K not a multiple of 16: one wave per output.
+#include <cstdio>
 #include <cstdlib>
 
 #include "zt_launch.hpp"
@@ -485,6 +486,151 @@ hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Skinny int8 GEMM (M <= 16*MT tokens, weight-streaming: the whole of qx
+// is reused by every workgroup from L2, W is read once).  One workgroup per
+// block of TPW 16-row weight tiles over all of K; its NW waves split K into
+// 64-wide chunks.  Per chunk a lane loads one 16-byte fragment of each of
+// its TPW weight rows (A operand) and of each of the MT token tiles
+// (B operand) into a ring of PF register slots; a slot is refilled right
+// after its MFMAs, PF chunks ahead (a scheduling barrier keeps the compiler
+// from sinking the refills).  D[n][m] leaves each lane four consecutive n of
+// one token; the K partials meet in LDS in a fixed order (4 slabs; with 8
+// waves the upper four first add onto the lower four) and the epilogue
+// writes rows of 4 columns.
+constexpr int kSkPitchPad = 4;
+
+template <int MT, int TPW>
+constexpr size_t s8_skinny_lds() {
+  return (size_t)4 * (16 * MT) * (16 * TPW + kSkPitchPad) * 4;
+}
+
+template <int MT, int TPW, int PF, int NW>
+__global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunks_per_wave) {
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int n0 = blockIdx.x * (16 * TPW);
+  const auto q_rs = make_rsrc(a.qx, (uint32_t)((int64_t)M * K));
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+
+  uint32_t w_row[TPW], q_row[MT];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int n = n0 + t * 16 + lr;
+    w_row[t] = n < N ? (uint32_t)(n * K) : kOobOffset;
+  }
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const int m = j * 16 + lr;
+    q_row[j] = m < M ? (uint32_t)(m * K) : kOobOffset;
+  }
+  const int c_begin = wv * chunks_per_wave;
+  const int total = K / 64;
+  const int nch = max(0, min(chunks_per_wave, total - c_begin));
+
+  // K % 64 == 0 (host-checked): every lane's k of a chunk inside the wave's
+  // range is < K.  A row past M/N starts at kOobOffset and stays out of
+  // range after adding k; a chunk past the wave's range (c >= nch, the
+  // same for the whole wave) is read at kOobOffset too.  (A row past M/N in
+  // a chunk past the range wraps to a small in-range offset: the read is in
+  // bounds and only feeds an output row or column that is never stored.)
+  i32x4_t wf[PF][TPW], qf[PF][MT];
+  auto load = [&](int slot, int c) {
+    const uint32_t kc = c < nch ? (uint32_t)((c_begin + c) * 64) : kOobOffset;
+    const uint32_t k = kc + 16u * lg;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+      wf[slot][t] = __builtin_bit_cast(
+          i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, w_row[t] + k, 0, 0));
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+      qf[slot][j] = __builtin_bit_cast(
+          i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(q_rs, q_row[j] + k, 0, 0));
+  };
+
+  i32x4_t acc[TPW][MT];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[t][j] = i32x4_t{0, 0, 0, 0};
+
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load(p, p);
+  for (int c = 0; c < nch; c += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+          acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[p][t], qf[p][j], acc[t][j], 0, 0, 0);
+      load(p, c + p + PF);  // chunks past nch read as zero and are never used
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // K partials: slab[w][m][n_local], n_local = t*16 + 4*lg + r
+  constexpr int P = 16 * TPW + kSkPitchPad;
+  int32_t *slab = reinterpret_cast<int32_t *>(s8_smem);
+  auto slab_at = [&](int w, int t, int j) {
+    return reinterpret_cast<i32x4_t *>(slab + ((w * 16 * MT) + j * 16 + lr) * P + t * 16 + 4 * lg);
+  };
+  if (NW == 8 && wv >= 4) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) *slab_at(wv - 4, t, j) = acc[t][j];
+  }
+  if (NW == 8) __syncthreads();
+  if (wv < 4) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        i32x4_t v = acc[t][j];
+        if (NW == 8) v += *slab_at(wv, t, j);
+        *slab_at(wv, t, j) = v;
+      }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 16 * MT * 4 * TPW; idx += 64 * NW) {
+    const int m = idx / (4 * TPW), c4 = (idx % (4 * TPW)) * 4;
+    if (m >= M || n0 + c4 >= N) continue;
+    i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + c4);
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      v += *reinterpret_cast<const i32x4_t *>(slab + (w * 16 * MT + m) * P + c4);
+    dyn_epilogue4(a, m, n0 + c4, v);
+  }
+}
+
+template <int MT, int TPW, int PF, int NW>
+hipError_t launch_s8_skinny_t(const DynArgs &a, hipStream_t s) {
+  const int total = (int)(a.K / 64);
+  int cpw = (total + NW - 1) / NW;
+  cpw = (cpw + PF - 1) / PF * PF;
+  const int blocks = (int)((a.N + 16 * TPW - 1) / (16 * TPW));
+  s8_skinny_kernel<MT, TPW, PF, NW><<<dim3((unsigned)blocks), dim3(64 * NW),
+                                      s8_skinny_lds<MT, TPW>(), s>>>(a, cpw);
+  return hipGetLastError();
+}
+
+hipError_t launch_s8_skinny(const DynArgs &a, hipStream_t s) {
+  const int mt = (int)((a.M + 15) / 16);
+  const char *e = std::getenv("ZT_S8_SKINNY");  // "TPW,PF,NW"
+  int tpw = 0, pf = 0, nw = 0;
+  if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+#define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
+  if (mt <= MT_ && (!tpw || (tpw == TPW_ && pf == PF_ && nw == NW_)))          \
+    return launch_s8_skinny_t<MT_, TPW_, PF_, NW_>(a, s);
+  ZT_SK(1, 4, 4, 8) ZT_SK(2, 4, 4, 8) ZT_SK(4, 2, 4, 8)
+  ZT_SK(8, 2, 3, 8) ZT_SK(8, 3, 4, 4) ZT_SK(8, 2, 4, 4) ZT_SK(8, 3, 2, 8) ZT_SK(8, 1, 4, 8)
+#undef ZT_SK
+  return hipErrorInvalidValue;
+}
+
 template <int BM, int BN>
 hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
@@ -513,10 +659,12 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(s8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
     return hipGetLastError();
   }
-  // the tiled kernel addresses qx and W with 32-bit byte offsets
+  // the fast kernels address qx and W with 32-bit byte offsets
   const bool fits32 = a.M * a.K < (int64_t)kOobOffset && a.N * a.K < (int64_t)kOobOffset;
-  const char *force = std::getenv("ZT_S8_FORCE");
+  const char *force = std::getenv("ZT_S8_FORCE");  // t: tiled, s: skinny, o: old
   const bool tiled = force ? force[0] == 't' : a.M >= 256;
+  const bool skinny = force ? force[0] == 's' : a.M <= 128;
+  if (skinny && fits32 && a.K % 64 == 0) return launch_s8_skinny(a, s);
   if (tiled && fits32) {
     // 256x128 tiles once there are half a round of them (measured on the
     // Llama prefill shapes: 2-stage DMA 256x128 is fastest from M = 2048 up)

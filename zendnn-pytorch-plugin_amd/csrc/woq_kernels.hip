@@ -354,6 +354,124 @@ __global__ __launch_bounds__(decode_max_threads<CPW>()) void woq_decode_kernel(
   }
 }
 
+// Weight-streaming decode kernel (M <= 16 and the activations fit in LDS).
+//
+// One workgroup per TPW 16-row tiles over all of K; its NW waves split K
+// into slices of CPW 128-wide chunks.  A wave first issues every weight and
+// scale load of its slice (TPW x CPW 16-byte fragments per lane, all in
+// flight at once: few waves with many loads each keep HBM busier than many
+// waves with few), then the workgroup copies x [M, K] into LDS with
+// full-width loads, and the wave walks its chunks: B operands come from LDS
+// (lanes past M read zeros), A operands are the fragments dequantised in
+// registers.  K partials meet in LDS and are added in wave order.
+template <int NW>
+__host__ __device__ constexpr size_t stream_slab_bytes(int tpw) {
+  return (size_t)NW * tpw * 16 * 17 * sizeof(float);
+}
+__host__ __device__ inline int stream_x_pitch(int K) { return K + 8; }  // bf16
+
+template <int NW, int CPW, int TPW, int MODE>
+__global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_shift, int gmask) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int KW = K / 8, C = K / 128;
+  const int t0 = blockIdx.x * TPW;
+  const int c0 = wv * CPW;
+  const int zmode = zp_mode_of(a.zp, a.zp_dt);
+  const int s_bytes = MODE == kDecGenF32 ? 4 : 2;
+  const auto w_rsrc = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rsrc = make_rsrc(a.scales, (uint32_t)(a.G * N * s_bytes));
+
+  // 1. the slice's weights and scales, all in flight.  Rows past N are
+  //    clamped (their results are never stored); chunks past C read zeros.
+  u32x4_t wr[TPW][CPW];
+  uint32_t sr[TPW][CPW];
+  float zr[TPW][CPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int n = min((t0 + t) * 16 + lr, N - 1);
+    const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int kc = c0 + c;
+      const int kcs = min(kc, C - 1);
+      const uint32_t sidx = (uint32_t)((kcs >> cpg_shift) & gmask) * (uint32_t)N + (uint32_t)n;
+      wr[t][c] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                       w_rsrc, kc < C ? row_off + (uint32_t)kc * 64u : kOobOffset, 0, 0));
+      if (MODE == kDecGenF32)
+        sr[t][c] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, sidx * 4u, 0, 0);
+      else
+        sr[t][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, sidx * 2u, 0, 0);
+      zr[t][c] = (MODE != kDecFast && zmode) ? load_elem(a.zp, a.zp_dt, sidx) : 0.f;
+    }
+  }
+
+  // 2. x [M, K] -> LDS (row pitch K + 8 bf16)
+  const int XP = stream_x_pitch(K);
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes<NW>(TPW));
+  {
+    const uint16_t *xp = reinterpret_cast<const uint16_t *>(a.x);
+    const int per_row = K / 8;
+    for (int idx = tid; idx < M * per_row; idx += 64 * NW) {
+      const int m = idx / per_row, k8 = idx - m * per_row;
+      *reinterpret_cast<u32x4_t *>(xl + m * XP + k8 * 8) =
+          *reinterpret_cast<const u32x4_t *>(xp + (int64_t)m * a.ldx + k8 * 8);
+    }
+  }
+  __syncthreads();
+
+  // 3. the slice's MFMAs
+  f32x4_t acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int kc = c0 + c;
+    if (kc < C) {
+      u32x4_t xb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xb[i] = lr < M ? *reinterpret_cast<const u32x4_t *>(xl + lr * XP + kc * 128 + 32 * lg + 8 * i)
+                       : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const uint32_t sb = sr[t][c];
+        const float sc = MODE == kDecGenF32 ? __uint_as_float(sb) : __uint_as_float(sb << 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              dq_word<MODE>(wr[t][c][i], sc, zr[t][c], zmode),
+              __builtin_bit_cast(bf16x8_t, xb[i]), acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // 4. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t], then
+  //    each output adds the NW partials in wave order
+  float *slab = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][r];
+  __syncthreads();
+  const int n0 = t0 * 16;
+  for (int idx = tid; idx < TPW * 16 * M; idx += 64 * NW) {
+    const int m = idx / (TPW * 16), nr = idx - m * (TPW * 16);
+    const int n = n0 + nr;
+    if (n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += slab[((w * TPW) * 16 + nr) * 17 + m];
+    if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
+    v = apply_post_ops(v, a.post, m, n);
+    store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
+  }
+}
+
 // --------------------------------------------------------------- GEMM
 constexpr int kGemmBK = 64;
 
@@ -637,10 +755,65 @@ static hipError_t launch_decode_t(const WoqArgs &a, const DecodePlan &p, hipStre
   return hipGetLastError();
 }
 
+template <int NW, int CPW, int TPW>
+static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode) {
+  const int tiles = (int)((a.N + 15) / 16);
+  const size_t lds = stream_slab_bytes<NW>(TPW) + (size_t)a.M * stream_x_pitch((int)a.K) * 2;
+  dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
+  if (mode == kDecFast)
+    woq_stream_kernel<NW, CPW, TPW, kDecFast><<<grid, block, lds, s>>>(a, shift, gmask);
+  else if (mode == kDecGenBf16)
+    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16><<<grid, block, lds, s>>>(a, shift, gmask);
+  else
+    woq_stream_kernel<NW, CPW, TPW, kDecGenF32><<<grid, block, lds, s>>>(a, shift, gmask);
+  return hipGetLastError();
+}
+
+// The weight-streaming kernel, when it applies: M <= 16 and x [M, K] in at
+// most 64 KB of LDS.  Returns false when the caller should use the planned
+// decode kernel instead.
+static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
+                              hipError_t *err) {
+  const int C = (int)(a.K / 128);
+  const int tiles = (int)((a.N + 15) / 16);
+  if (a.M > 16 || (size_t)a.M * stream_x_pitch((int)a.K) * 2 > 64 * 1024) return false;
+  // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
+  // each, two tiles per wave once there are two rounds of tiles
+  int nw = 8, tpw = tiles >= 512 ? 2 : 1, cpw = 0;
+  const char *e = std::getenv("ZT_WOQ_STREAM");  // "0" disables; "NW,CPW,TPW" forces
+  if (e && e[0] == '0') return false;
+  if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
+  const int need = (C + nw - 1) / nw;
+  if (cpw == 0)
+    for (int c : {2, 4, 8, 12, 16})
+      if (c >= need) { cpw = c; break; }
+  if (cpw < need) return false;
+  if (std::getenv("ZT_WOQ_DEBUG"))
+    std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: NW=%d CPW=%d TPW=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, nw, cpw, tpw);
+#define ZT_STREAM_CASE(NW_, CPW_, TPW_) \
+  if (nw == NW_ && cpw == CPW_ && tpw == TPW_) { *err = launch_stream_t<NW_, CPW_, TPW_>(a, s, shift, gmask, mode); return true; }
+  ZT_STREAM_CASE(4, 2, 1) ZT_STREAM_CASE(4, 4, 1) ZT_STREAM_CASE(4, 8, 1) ZT_STREAM_CASE(4, 12, 1)
+  ZT_STREAM_CASE(4, 16, 1) ZT_STREAM_CASE(4, 8, 2) ZT_STREAM_CASE(4, 4, 2) ZT_STREAM_CASE(4, 16, 2)
+  ZT_STREAM_CASE(8, 4, 1) ZT_STREAM_CASE(8, 8, 1) ZT_STREAM_CASE(8, 12, 1) ZT_STREAM_CASE(8, 16, 1)
+  ZT_STREAM_CASE(8, 4, 2) ZT_STREAM_CASE(8, 8, 2) ZT_STREAM_CASE(8, 16, 2) ZT_STREAM_CASE(2, 16, 1)
+#undef ZT_STREAM_CASE
+  return false;
+}
+
 hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *workspace,
                              hipStream_t s) {
   (void)workspace;
   if (a.M == 0 || a.N == 0) return hipSuccess;
+  {
+    const int64_t cpg = a.G == 1 ? 0 : (a.K / a.G) / 128;
+    int shift = 0;
+    while (cpg > 1 && (1 << shift) < cpg) ++shift;
+    const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+    const int mode = a.s_dt == ZT_DT_F32 ? kDecGenF32 : (a.zp ? kDecGenBf16 : kDecFast);
+    hipError_t err = hipSuccess;
+    if (try_launch_stream(a, s, shift, gmask, mode, &err)) return err;
+  }
   if (std::getenv("ZT_WOQ_DEBUG"))
     std::fprintf(stderr,
                  "[zt] woq decode M=%lld N=%lld K=%lld: NK=%d NT=%d CPW=%d TPW=%d NI=%d xr=%d "
