@@ -64,6 +64,17 @@ def _torch_flags():
     return cflags, ldflags
 
 
+def _check_no_undefined_kernels(lib):
+    """A kernel whose host launch stub the compiler did not emit links fine
+    into a shared library and only fails when the library is loaded: refuse
+    such a library here."""
+    p = subprocess.run(["nm", "-u", lib], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True)
+    missing = [ln.split()[-1] for ln in p.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        raise RuntimeError(f"{lib}: kernel launch stubs not emitted: {missing}")
+
+
 def build(verbose=False, jobs=8):
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(PKG, exist_ok=True)
@@ -84,6 +95,7 @@ def build(verbose=False, jobs=8):
     hiplib = os.path.join(PKG, "libzentorch_hip.so")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", hiplib + ".tmp"]
          + hip_objs, verbose)
+    _check_no_undefined_kernels(hiplib + ".tmp")
     os.replace(hiplib + ".tmp", hiplib)
     clib = os.path.join(PKG, "_C.so")
     _run(["g++", "-shared", "-o", clib + ".tmp"] + torch_objs + ldflags, verbose)

@@ -354,6 +354,8 @@ __global__ __launch_bounds__(decode_max_threads<CPW>()) void woq_decode_kernel(
   }
 }
 
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
 // Weight-streaming decode kernel (M <= 16 and the activations fit in LDS).
 //
 // One workgroup per TPW 16-row tiles over all of K; its NW waves split K
@@ -470,6 +472,208 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     v = apply_post_ops(v, a.post, m, n);
     store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
   }
+}
+
+// ----------------------------------------------------- prefill GEMM (DMA)
+// BM x BN output tile, 4 waves (2 x 2) of (BM/2) x (BN/2), K in steps of
+// 128.  Per step the buffer unit moves straight into LDS:
+//  * the x slab [BM, 128] bf16: 256-byte rows whose sixteen 16-byte chunks
+//    are XOR-swizzled (chunk c of row r at position c ^ (r & 15)), so the 16
+//    rows of a fragment read hit every bank once;
+//  * the raw int4 slab [BN, 128] (64-byte rows of packed words).
+// A lane's B operand for a step is one 16-byte read (the 32 elements
+// [32g, 32g+32) of its row, g = lane / 16), dequantised in registers right
+// before its MFMAs -- exactly bf16_rne of the reference's fp32 dequantised
+// weight -- and its A operand for sub-step i is the 16 bytes of x at element
+// 32g + 8i, the same element order.  Two LDS stages; the step's reads are
+// issued before the next step's loads, the MFMAs after, one barrier a step.
+// The fp32 tile is staged in LDS for the epilogue (bias, post-ops, 8-byte
+// bf16 stores).
+constexpr int kXRow = 256;   // bytes of x per row per step
+constexpr int kWRow = 64;    // bytes of int4 per weight row per step
+
+template <int BM, int BN>
+constexpr size_t woq_dma_lds() {
+  const size_t stages = 2 * ((size_t)BM * kXRow + (size_t)BN * kWRow);
+  const size_t tile = (size_t)BM * (BN + 4) * 4;
+  return stages > tile ? stages : tile;
+}
+
+template <int BM, int BN, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void woq_gemm_dma_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg_shift,
+                         int gmask) {
+  constexpr int WTM = BM / 32, WTN = BN / 32;
+  constexpr int STAGE = BM * kXRow + BN * kWRow;
+  constexpr int XI = BM * kXRow / 1024;  // 1 KB loads per stage: x
+  constexpr int WI = BN * kWRow / 1024;  //                        weights
+  static_assert((XI + WI) % 4 == 0, "loads must split over 4 waves");
+  constexpr int LPW = (XI + WI) / 4;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int KW = K / 8;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int zmode = zp_mode_of(a.zp, a.zp_dt);
+  const int s_bytes = MODE == kDecGenF32 ? 4 : 2;
+
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)M * a.ldx * 2));
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * s_bytes));
+
+  // This wave's LPW 1 KB loads per stage: x loads cover 4 rows (16 lanes x
+  // 16 B each, chunk positions XOR-swizzled by row), weight loads 16 rows
+  // (4 lanes x 16 B each).
+  const int ldx2 = (int)a.ldx * 2;
+  auto dma = [&](int step) {
+    unsigned char *stage = smem + (step & 1) * STAGE;
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+      const int li = wv * LPW + q;
+      if (li < XI) {
+        const int row = li * 4 + (lane >> 4);
+        const int chunk = (lane & 15) ^ (row & 15);
+        const uint32_t off = m0 + row < M ? (uint32_t)((m0 + row) * ldx2 + step * kXRow + chunk * 16)
+                                          : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(stage + li * 1024), 16, off, 0, 0, 0);
+      } else {
+        const int wi = li - XI;
+        const int row = wi * 16 + (lane >> 2);
+        const uint32_t off = n0 + row < N ? (uint32_t)((n0 + row) * KW * 4 + step * kWRow + (lane & 3) * 16)
+                                          : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (lds_ptr_t)(stage + BM * kXRow + wi * 1024), 16,
+                                                 off, 0, 0, 0);
+      }
+    }
+  };
+
+  // this lane's weight rows (clamped: rows past N are computed, never stored)
+  uint32_t srow[WTN];
+#pragma unroll
+  for (int j = 0; j < WTN; ++j) srow[j] = (uint32_t)min(n0 + wn * (BN / 2) + j * 16 + lr, N - 1);
+
+  f32x4_t acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = K / 128;
+  dma(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ++ks) {
+    const unsigned char *stage = smem + (ks & 1) * STAGE;
+    // scales (and zero points) of this step, one per weight row
+    uint32_t sraw[WTN];
+    float zr[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const uint32_t sidx = (uint32_t)((ks >> cpg_shift) & gmask) * (uint32_t)N + srow[j];
+      sraw[j] = MODE == kDecGenF32 ? __builtin_amdgcn_raw_buffer_load_b32(s_rs, sidx * 4u, 0, 0)
+                                   : __builtin_amdgcn_raw_buffer_load_b16(s_rs, sidx * 2u, 0, 0);
+      zr[j] = (MODE != kDecFast && zmode) ? load_elem(a.zp, a.zp_dt, sidx) : 0.f;
+    }
+    // raw weight words: row (wn*BN/2 + j*16 + lr), 16 bytes at 16*lg
+    u32x4_t wraw[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+      wraw[j] = *reinterpret_cast<const u32x4_t *>(
+          stage + BM * kXRow + (wn * (BN / 2) + j * 16 + lr) * kWRow + 16 * lg);
+    // x fragments of all four sub-steps: row (wm*BM/2 + i*16 + lr), logical
+    // chunk 4*lg + sub (element 32*lg + 8*sub), swizzled by the row
+    u32x4_t xf[4][WTM];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < WTM; ++i) {
+        const int row = wm * (BM / 2) + i * 16 + lr;
+        xf[sub][i] = *reinterpret_cast<const u32x4_t *>(
+            stage + row * kXRow + (((4 * lg + sub) ^ (row & 15)) * 16));
+      }
+    if (ks + 1 < nk) dma(ks + 1);
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      bf16x8_t B[WTN];
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        const float sc = MODE == kDecGenF32 ? __uint_as_float(sraw[j]) : __uint_as_float(sraw[j] << 16);
+        B[j] = dq_word<MODE>(wraw[j][sub], sc, zr[j], zmode);
+      }
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, xf[sub][i]), B[j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // D[m = 4g + r][n = lane % 16] -> fp32 tile in LDS -> rows of 4 columns
+  constexpr int TP = BN + 4;
+  float *tile = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * TP + wn * (BN / 2) + j * 16 + lr] = acc[i][j][r];
+  __syncthreads();
+  for (int idx = tid; idx < BM * (BN / 4); idx += 256) {
+    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c4;
+    if (m >= M || n >= N) continue;
+    const f32x4_t v4 = *reinterpret_cast<const f32x4_t *>(tile + row * TP + c4);
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = v4[r];
+      if (n + r < N) {
+        if (a.bias) v = v + load_elem(a.bias, a.b_dt, n + r);
+        v = apply_post_ops(v, a.post, m, n + r);
+      }
+      f[r] = v;
+    }
+    if (a.y_dt == ZT_DT_BF16 && n + 3 < N && (a.ldy & 3) == 0) {
+      u32x2_t pk;
+      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * a.ldy + n) = pk;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n + r, f[r]);
+    }
+  }
+}
+
+template <int BM, int BN>
+static hipError_t launch_woq_dma_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  dim3 grid((unsigned)(tiles_m * tiles_n)), block(256);
+  const size_t lds = woq_dma_lds<BM, BN>();
+  if (mode == kDecFast)
+    woq_gemm_dma_kernel<BM, BN, kDecFast><<<grid, block, lds, s>>>(a, tiles_m, tiles_n, group_m, shift, gmask);
+  else if (mode == kDecGenBf16)
+    woq_gemm_dma_kernel<BM, BN, kDecGenBf16><<<grid, block, lds, s>>>(a, tiles_m, tiles_n, group_m, shift, gmask);
+  else
+    woq_gemm_dma_kernel<BM, BN, kDecGenF32><<<grid, block, lds, s>>>(a, tiles_m, tiles_n, group_m, shift, gmask);
+  return hipGetLastError();
 }
 
 // --------------------------------------------------------------- GEMM
@@ -839,6 +1043,28 @@ hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *worksp
 }
 
 hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
+  {
+    // the DMA kernel: bf16 x, K % 128 == 0, one scale per 128-chunk, 32-bit
+    // byte offsets for x and the weights
+    const int64_t gs = a.K / a.G, cpg = gs / 128;
+    const bool ok = a.x_dt == ZT_DT_BF16 && a.K % 128 == 0 && a.ldx % 8 == 0 &&
+                    aligned16(a.x) && aligned16(a.w) &&
+                    (a.G == 1 || (gs % 128 == 0 && (cpg & (cpg - 1)) == 0)) &&
+                    a.M * a.ldx * 2 < (int64_t)kOobOffset &&
+                    a.N * (a.K / 2) < (int64_t)kOobOffset;
+    const char *e = std::getenv("ZT_WOQ_GEMM");  // "old" disables, "128" forces 128x128
+    if (ok && !(e && e[0] == 'o')) {
+      int shift = 0;
+      while (cpg > 1 && (1 << shift) < cpg) ++shift;
+      const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+      const int mode = a.s_dt == ZT_DT_F32 ? kDecGenF32 : (a.zp ? kDecGenBf16 : kDecFast);
+      const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
+      // 256 x 128 only for the fast mode: the general dequant spills there
+      const bool big = mode == kDecFast && (e ? e[0] == '2' : t256 >= 128);
+      return big ? launch_woq_dma_t<256, 128>(a, s, shift, gmask, mode)
+                 : launch_woq_dma_t<128, 128>(a, s, shift, gmask, mode);
+    }
+  }
   if (a.M == 0 || a.N == 0) return hipSuccess;
   if (a.M <= 64) {
     dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 63) / 64));
