@@ -156,6 +156,41 @@ int zt_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out,
 int zt_woq_repack_from_int4pack(const uint8_t *packed, int64_t N, int64_t K,
                                 int32_t *out, zt_stream_t stream);
 
+/*
+ * Grouped int4 weight-only mixture of experts: for every token t and each
+ * of its topk experts e = topk_ids[t, k],
+ *   h = act(x[t] . dq(w13[e, :I])^T + b13[e, :I]) * (x[t] . dq(w13[e, I:])^T + b13[e, I:])
+ *   y = h . dq(w2[e])^T + b2[e]                      (h and y rounded to bf16)
+ *   out[t] = sum_k topk_weights[t, k] * y            (fp32, k in order; all
+ *                                                     weights 1 if skip_weighted)
+ * Replaces zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema
+ * :728-736) for int4-packed expert weights (the reference takes bf16 or int8
+ * experts); pairs whose id is outside [0, E) are dropped, as the reference's
+ * expert-parallel path drops remote ids (vllm/_int8_moe_patch.py:170-180).
+ *
+ *  x            [T, H] bf16;  out [T, H] bf16 (overwritten)
+ *  topk_ids     [T, topk] int32;  topk_weights [T, topk] fp32 or bf16
+ *  act          ZT_PO_SILU, ZT_PO_GELU_ERF or ZT_PO_GELU_TANH
+ *  w13          [E, 2I, H/8] int32 packed int4 (zt_woq_repack_weight per
+ *               expert), w13_scales [E, G13, 2I] bf16, w13_bias [E, 2I] bf16
+ *               or NULL
+ *  w2           [E, H, I/8], w2_scales [E, G2, H] bf16, w2_bias [E, H] or NULL
+ *  H, I multiples of 128; group sizes H/G13, I/G2 multiples of 128 (or one
+ *  group), powers of two times 128.  E <= 1024.
+ *  workspace    zt_woq_moe_workspace_size(T, H, topk, E, I) bytes; no host
+ *               synchronisation (the routing runs on the GPU).
+ */
+int zt_woq_moe(const void *x, int64_t T, int64_t H, const int32_t *topk_ids,
+               const void *topk_weights, int32_t weights_dtype, int64_t topk,
+               int32_t skip_weighted, int32_t act, const int32_t *w13,
+               const void *w13_scales, int64_t G13, const void *w13_bias,
+               const int32_t *w2, const void *w2_scales, int64_t G2,
+               const void *w2_bias, int64_t E, int64_t I, void *out,
+               void *workspace, size_t workspace_bytes, zt_stream_t stream);
+
+size_t zt_woq_moe_workspace_size(int64_t T, int64_t H, int64_t topk, int64_t E,
+                                 int64_t I);
+
 /* Message of the calling thread's last failed call ("" if none). */
 const char *zt_last_error_string(void);
 

@@ -51,6 +51,9 @@ def lib():
         L.zto_dynamic_qlinear.argtypes = [
             _vp, _int, _i64, _i64, _vp, _i64, _vp, _int, _vp, _int, _int, _vp,
             _vp, _vp, _vp, _vp, _int, _vp, _vp, _vp, _int]
+        L.zto_woq_moe.argtypes = [
+            _vp, _i64, _i64, _vp, _vp, _int, _i64, _int, _int, _vp, _vp, _i64, _vp, _vp,
+            _vp, _i64, _vp, _i64, _i64, _vp, _int]
         L.zto_max_threads.restype = _int
         _lib = L
     return _lib
@@ -173,3 +176,34 @@ def dynamic_qlinear(x, w, w_scales, bias=None, post_ops=(), post_bufs=(),
     if return_intermediates:
         return y, qx, sx, acc
     return y
+
+
+MOE_ACT = {"silu": PO["silu"], "gelu": PO["gelu_erf"], "gelu_tanh": PO["gelu_tanh"]}
+
+
+def woq_moe(x, topk_ids, topk_weights, w13, w13_scales, w2, w2_scales,
+            w13_bias=None, w2_bias=None, act="silu", skip_weighted=False, nthreads=0):
+    """Grouped int4 MoE (FusedMoE.cpp:443-700 with int4 experts).
+
+    x [T, H] bf16; topk_ids [T, k] int32; topk_weights [T, k]; w13 int32
+    [E, 2I, H/8]; w13_scales bf16 [E, G13, 2I]; w2 int32 [E, H, I/8];
+    w2_scales bf16 [E, G2, H]; biases bf16 [E, 2I] / [E, H].  Returns bf16 [T, H].
+    """
+    x = x.contiguous()
+    T, H = x.shape
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.contiguous()
+    topk = ids.shape[1]
+    E, N13, _ = w13.shape
+    I = N13 // 2
+    out = torch.empty(T, H, dtype=torch.bfloat16)
+    args = [w13.contiguous(), w13_scales.contiguous(), w2.contiguous(), w2_scales.contiguous(),
+            None if w13_bias is None else w13_bias.contiguous(),
+            None if w2_bias is None else w2_bias.contiguous()]
+    w13c, s13, w2c, s2, b13, b2 = args
+    rc = lib().zto_woq_moe(
+        _ptr(x), T, H, _ptr(ids), _ptr(wts), DT[wts.dtype], topk, int(skip_weighted),
+        MOE_ACT[act], _ptr(w13c), _ptr(s13), s13.shape[1], _ptr(b13), _ptr(w2c), _ptr(s2),
+        s2.shape[1], _ptr(b2), E, I, _ptr(out), nthreads)
+    _check(rc, "woq_moe")
+    return out

@@ -27,6 +27,13 @@
  *                           (compute=s8, transB=true, ldb=K).
  *   zto_dynamic_qlinear     DynamicQLinear.cpp:74-181: y = acc*sx[m]*sw[n] + b[n]
  *                           in fp32, rounded once to the output dtype.
+ *   zto_woq_moe             FusedMoE.cpp:443-700 and the per-expert loop of
+ *                           vllm/_int8_moe_patch.py:149-206 with int4 expert
+ *                           weights: per (token, k) pair of expert e,
+ *                           gate/up = zto_woq_linear (fp32), h = bf16(act(gate)
+ *                           * up), y = bf16(zto_woq_linear(h) + b2), out[t] =
+ *                           bf16(sum_k w[t,k] * y) in fp32, k ascending; ids
+ *                           outside [0, E) are dropped.
  *
  * Where the reference leaves numerics to ZenDNNL (accumulation order, the
  * rounding of the dequantised weight, the u4 zero-point convention) the
@@ -348,4 +355,66 @@ int zto_dynamic_qlinear(const void *x, int x_dt, int64_t M, int64_t K,
   if (!sx_out) free(sx);
   if (!acc_out) free(acc);
   return ZTO_OK;
+}
+
+/* ------------------------------------------------------------------ MoE */
+/* x [T, H] bf16; ids [T, topk] int32; wts [T, topk] (wts_dt); w13 [E, 2I,
+ * H/8] packed; s13 [E, G13, 2I] bf16; b13 [E, 2I] bf16 or NULL; w2 [E, H,
+ * I/8]; s2 [E, G2, H]; b2 [E, H] or NULL; out [T, H] bf16. */
+int zto_woq_moe(const uint16_t *x, int64_t T, int64_t H, const int32_t *ids,
+                const void *wts, int wts_dt, int64_t topk, int skip_weighted,
+                int act, const int32_t *w13, const uint16_t *s13, int64_t G13,
+                const uint16_t *b13, const int32_t *w2, const uint16_t *s2,
+                int64_t G2, const uint16_t *b2, int64_t E, int64_t I,
+                uint16_t *out, int nthreads) {
+  const int64_t P = T * topk;
+  float *acc = (float *)calloc((size_t)T * H, sizeof(float));
+  uint16_t *xe = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(P > 0 ? P : 1) * H);
+  int64_t *pe = (int64_t *)malloc(sizeof(int64_t) * (size_t)(P > 0 ? P : 1));
+  float *gu = (float *)malloc(sizeof(float) * (size_t)(P > 0 ? P : 1) * 2 * I);
+  uint16_t *h = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(P > 0 ? P : 1) * I);
+  uint16_t *y = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(P > 0 ? P : 1) * H);
+  int rc = ZTO_OK;
+  if (!acc || !xe || !pe || !gu || !h || !y) rc = ZTO_EINVAL;
+  float *yfull = rc == ZTO_OK ? (float *)malloc(sizeof(float) * (size_t)(P > 0 ? P : 1) * H) : NULL;
+  if (rc == ZTO_OK && !yfull) rc = ZTO_EINVAL;
+  for (int64_t e = 0; e < E && rc == ZTO_OK; ++e) {
+    /* the pairs of expert e, in pair order */
+    int64_t me = 0;
+    for (int64_t p = 0; p < P; ++p)
+      if (ids[p] == e) {
+        pe[me] = p;
+        memcpy(xe + me * H, x + (p / topk) * H, sizeof(uint16_t) * (size_t)H);
+        ++me;
+      }
+    if (me == 0) continue;
+    const int32_t *we13 = w13 + e * 2 * I * (H / 8);
+    const uint16_t *se13 = s13 + e * G13 * 2 * I;
+    rc = zto_woq_linear(xe, ZT_DT_BF16, me, H, H, we13, 2 * I, se13, ZT_DT_BF16, G13,
+                        NULL, ZT_DT_NONE, b13 ? (const void *)(b13 + e * 2 * I) : NULL,
+                        ZT_DT_BF16, 0, NULL, NULL, NULL, NULL, gu, ZT_DT_F32, 2 * I, nthreads);
+    if (rc != ZTO_OK) break;
+    for (int64_t m = 0; m < me; ++m)
+      for (int64_t j = 0; j < I; ++j)
+        h[m * I + j] = f32_to_bf16(unary(act, gu[m * 2 * I + j]) * gu[m * 2 * I + I + j]);
+    rc = zto_woq_linear(h, ZT_DT_BF16, me, I, I, w2 + e * H * (I / 8), H, s2 + e * G2 * H,
+                        ZT_DT_BF16, G2, NULL, ZT_DT_NONE,
+                        b2 ? (const void *)(b2 + e * H) : NULL, ZT_DT_BF16, 0, NULL, NULL,
+                        NULL, NULL, y, ZT_DT_BF16, H, nthreads);
+    if (rc != ZTO_OK) break;
+    for (int64_t m = 0; m < me; ++m)
+      for (int64_t j = 0; j < H; ++j) yfull[pe[m] * H + j] = bf16_to_f32(y[m * H + j]);
+  }
+  if (rc == ZTO_OK) {
+    for (int64_t t = 0; t < T; ++t)
+      for (int64_t k = 0; k < topk; ++k) {
+        const int64_t p = t * topk + k;
+        if (ids[p] < 0 || ids[p] >= E) continue;
+        const float wk = skip_weighted ? 1.f : load_f(wts, wts_dt, p);
+        for (int64_t j = 0; j < H; ++j) acc[t * H + j] += wk * yfull[p * H + j];
+      }
+    for (int64_t i = 0; i < T * H; ++i) out[i] = f32_to_bf16(acc[i]);
+  }
+  free(acc); free(xe); free(pe); free(gu); free(h); free(y); free(yfull);
+  return rc;
 }

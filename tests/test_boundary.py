@@ -64,6 +64,17 @@ def test_c_abi_validates_without_gpu():
     rc = L.zt_woq_repack_from_int4pack(None, 10, 64, None, None)
     assert rc == 1 and b"multiple of 64" in L.zt_last_error_string()
     assert L.zt_dynamic_qlinear_workspace_size(128, 4096) >= 128 * 4096 + 128 * 4
+    # MoE: H, I multiples of 128; E <= 1024; activations the kernels have
+    rc = L.zt_woq_moe(None, 4, 100, None, None, 0, 2, 0, 4, None, None, 1, None, None, None,
+                      1, None, 8, 256, None, None, 0, None)
+    assert rc == 1 and b"multiples of 128" in L.zt_last_error_string()
+    rc = L.zt_woq_moe(None, 4, 256, None, None, 0, 2, 0, 1, None, None, 1, None, None, None,
+                      1, None, 8, 256, None, None, 0, None)
+    assert rc == 2 and b"act" in L.zt_last_error_string()
+    rc = L.zt_woq_moe(None, 4, 256, None, None, 0, 2, 0, 4, None, None, 1, None, None, None,
+                      1, None, 2048, 256, None, None, 0, None)
+    assert rc == 2 and b"1024 experts" in L.zt_last_error_string()
+    assert L.zt_woq_moe_workspace_size(256, 4096, 2, 8, 14336) >= 512 * (14336 + 4096) * 2
     # the WOQ kernels reduce K inside a workgroup: no device workspace
     assert L.zt_woq_linear_workspace_size(16, 14336, 4096, 112) == 0
     assert L.zt_woq_linear_workspace_size(2048, 4096, 4096, 32) == 0
@@ -83,6 +94,9 @@ REFERENCE_SCHEMAS = {
     "zentorch_woq_repack_weight": "zentorch::zentorch_woq_repack_weight(Tensor unpacked_weight) -> Tensor",
     "zentorch_woq_repack_from_int4pack": "zentorch::zentorch_woq_repack_from_int4pack(Tensor packed_weight) -> Tensor",
     "zentorch_dynamic_qlinear": "zentorch::zentorch_dynamic_qlinear(Tensor input, Tensor weight, Tensor weight_scales, Tensor? bias=None, *, str zentorch_op_name=\"zentorch::zentorch_dynamic_qlinear\") -> Tensor",
+    # src/cpu/cpp/FusedMoE.cpp:729-741
+    "zentorch_fused_moe": "zentorch::zentorch_fused_moe(Tensor(a!) output, Tensor input, Tensor w13, Tensor w2, Tensor? w13_bias, Tensor? w2_bias, Tensor topk_weights, Tensor topk_id, bool skip_weighted, str act, Tensor? w13_scales=None, Tensor? w2_scales=None, *, str zentorch_op_name=\"zentorch::zentorch_fused_moe\") -> ()",
+    "zentorch_flush_moe_weight_cache": "zentorch::zentorch_flush_moe_weight_cache() -> ()",
 }
 
 
@@ -120,6 +134,13 @@ def test_meta_shapes():
     assert r.shape == (64, 32) and r.dtype == torch.int32
     r = ops.zentorch_woq_repack_from_int4pack(torch.empty(64, 128, dtype=torch.uint8, **m))
     assert r.shape == (64, 32) and r.dtype == torch.int32
+    xm = torch.empty(8, 256, dtype=torch.bfloat16, **m)
+    assert ops.zentorch_fused_moe(
+        torch.empty_like(xm), xm, torch.empty(4, 256, 32, dtype=torch.int32, **m),
+        torch.empty(4, 256, 16, dtype=torch.int32, **m), None, None,
+        torch.empty(8, 2, **m), torch.empty(8, 2, dtype=torch.int32, **m), False, "silu",
+        torch.empty(4, 1, 256, dtype=torch.bfloat16, **m),
+        torch.empty(4, 1, 256, dtype=torch.bfloat16, **m)) is None
 
 
 def test_cpu_tensors_are_rejected_not_computed():

@@ -256,3 +256,76 @@ def test_oracle_reproduces_golden_fixtures():
     assert torch.equal(y, c["y"])
     qb, sb = O.dynamic_quantize(c["x_bf16"])
     assert torch.equal(qb, c["qx_bf16"]) and torch.equal(sb, c["sx_bf16"])
+
+
+
+# ------------------------------------------------------------------ MoE
+def _dequant_rows(q, s):
+    """q int [N, K] (signed int4 values), s [G, N] -> bf16-rounded q*s in fp32
+    (the dequantised weight of the reference test, test_woq_linear.py:118-128)."""
+    N, K = q.shape
+    G = s.shape[0]
+    return (q.float().view(N, G, K // G) * s.float().t().unsqueeze(-1)).view(N, K).bfloat16().float()
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu", "gelu_tanh"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_oracle_vs_torch_composition(act, bias):
+    # independent restatement with torch ops: per pair, gated activation of
+    # the w13 product, bf16 h, bf16 w2 product, weighted sum over k
+    g = torch.Generator().manual_seed(11)
+    T, H, I, E, k = 12, 256, 128, 4, 2
+    x = torch.randn(T, H, generator=g).bfloat16()
+    q13 = torch.randint(-8, 8, (E, 2 * I, H), generator=g, dtype=torch.int8)
+    q2 = torch.randint(-8, 8, (E, H, I), generator=g, dtype=torch.int8)
+    s13 = (torch.rand(E, H // 128, 2 * I, generator=g) * 0.01 + 0.005).bfloat16()
+    s2 = (torch.rand(E, I // 128, H, generator=g) * 0.01 + 0.005).bfloat16()
+    b13 = (torch.randn(E, 2 * I, generator=g) * 0.1).bfloat16() if bias else None
+    b2 = (torch.randn(E, H, generator=g) * 0.1).bfloat16() if bias else None
+    wts, ids = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), k)
+    ids[3, 1] = -1  # dropped pair (expert-parallel remote id)
+    w13 = torch.stack([O.woq_repack_weight(q13[e]) for e in range(E)])
+    w2 = torch.stack([O.woq_repack_weight(q2[e]) for e in range(E)])
+    y = O.woq_moe(x, ids.int(), wts, w13, s13, w2, s2, b13, b2, act=act)
+    f = {"silu": torch.nn.functional.silu,
+         "gelu": torch.nn.functional.gelu,
+         "gelu_tanh": lambda v: torch.nn.functional.gelu(v, approximate="tanh")}[act]
+    ref = torch.zeros(T, H)
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            if e < 0:
+                continue
+            gu = x[t].float() @ _dequant_rows(q13[e], s13[e]).t()
+            if bias:
+                gu = gu + b13[e].float()
+            h = (f(gu[:I]) * gu[I:]).bfloat16().float()
+            yy = h @ _dequant_rows(q2[e], s2[e]).t()
+            if bias:
+                yy = yy + b2[e].float()
+            ref[t] += wts[t, j] * yy.bfloat16().float()
+    torch.testing.assert_close(y.float(), ref, rtol=1e-2, atol=1e-2)
+
+
+def test_moe_oracle_single_expert_is_the_woq_pipeline():
+    # k = 1, skip_weighted: out = w2(act(w13 x)) exactly as two woq_linear
+    # calls and the gated activation (a closed special case)
+    g = torch.Generator().manual_seed(5)
+    T, H, I, E = 6, 256, 128, 3
+    x = torch.randn(T, H, generator=g).bfloat16()
+    q13 = torch.randint(-8, 8, (E, 2 * I, H), generator=g, dtype=torch.int8)
+    q2 = torch.randint(-8, 8, (E, H, I), generator=g, dtype=torch.int8)
+    s13 = (torch.rand(E, 1, 2 * I, generator=g) * 0.01 + 0.005).bfloat16()
+    s2 = (torch.rand(E, 1, H, generator=g) * 0.01 + 0.005).bfloat16()
+    w13 = torch.stack([O.woq_repack_weight(q13[e]) for e in range(E)])
+    w2 = torch.stack([O.woq_repack_weight(q2[e]) for e in range(E)])
+    ids = torch.tensor([[1], [0], [2], [1], [1], [0]], dtype=torch.int32)
+    y = O.woq_moe(x, ids, torch.ones(T, 1), w13, s13, w2, s2, skip_weighted=True)
+    for t in range(T):
+        e = int(ids[t, 0])
+        gu = O.woq_linear(x[t:t + 1], w13[e], s13[e]).float()  # bf16-rounded gate/up
+        gu32 = x[t:t + 1].float() @ _dequant_rows(q13[e], s13[e]).t()
+        h = (torch.nn.functional.silu(gu32[:, :I]) * gu32[:, I:]).bfloat16()
+        yy = O.woq_linear(h, w2[e], s2[e])
+        assert torch.equal(y[t:t + 1], yy)
+        del gu

@@ -48,6 +48,10 @@ def lib():
         L.zt_s8s8s32_gemm.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp]
         L.zt_woq_repack_weight.argtypes = [_vp, _i64, _i64, _vp, _vp]
         L.zt_woq_repack_from_int4pack.argtypes = [_vp, _i64, _i64, _vp, _vp]
+        L.zt_woq_moe.argtypes = [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp,
+                                 _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _sz, _vp]
+        L.zt_woq_moe_workspace_size.argtypes = [_i64, _i64, _i64, _i64, _i64]
+        L.zt_woq_moe_workspace_size.restype = _sz
         L.zt_last_error_string.restype = ctypes.c_char_p
         L.zt_version.restype = ctypes.c_int32
         _lib = L
@@ -163,4 +167,28 @@ def woq_repack_from_int4pack(packed):
     out = torch.empty(N, K // 8, dtype=torch.int32, device=packed.device)
     _check(lib().zt_woq_repack_from_int4pack(_p(packed), N, K, _p(out), _stream()))
     torch.cuda.synchronize()
+    return out
+
+
+MOE_ACT = {"silu": PO["silu"], "gelu": PO["gelu_erf"], "gelu_tanh": PO["gelu_tanh"]}
+
+
+def woq_moe(x, topk_ids, topk_weights, w13, w13_scales, w2, w2_scales, w13_bias=None,
+            w2_bias=None, act="silu", skip_weighted=False, sync=True):
+    """zt_woq_moe on device tensors; returns bf16 [T, H]."""
+    T, H = x.shape
+    topk = topk_ids.shape[1]
+    E, N13, _ = w13.shape
+    I = N13 // 2
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=x.device)
+    ws_bytes = lib().zt_woq_moe_workspace_size(T, H, topk, E, I)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    ids = topk_ids.to(torch.int32).contiguous()
+    _check(lib().zt_woq_moe(
+        _p(x), T, H, _p(ids), _p(topk_weights), DT[topk_weights.dtype], topk,
+        int(skip_weighted), MOE_ACT[act], _p(w13), _p(w13_scales), w13_scales.shape[1],
+        _p(w13_bias), _p(w2), _p(w2_scales), w2_scales.shape[1], _p(w2_bias), E, I, _p(out),
+        _p(ws), ws_bytes, _stream()))
+    if sync:
+        torch.cuda.synchronize()
     return out

@@ -24,7 +24,7 @@ BUILD = os.path.join(HERE, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-HIP_SOURCES = ["woq_kernels.hip", "dynq_kernels.hip", "capi.hip"]
+HIP_SOURCES = ["woq_kernels.hip", "dynq_kernels.hip", "moe_kernels.hip", "capi.hip"]
 TORCH_SOURCES = ["ops.cpp", "shim_cuda_zentorch.cpp"]
 
 # -packed-fp32-ops: no v_pk_*_f32 from the compiler (hipcc's host pass warns

@@ -5,6 +5,8 @@
 #include <cstring>
 #include <string>
 
+#include <algorithm>
+
 #include "zt_launch.hpp"
 
 namespace {
@@ -63,6 +65,109 @@ int convert_post_ops(const zt_post_ops *in, zt::PostOps *out, const char *op) {
 extern "C" {
 
 const char *zt_last_error_string(void) { return g_last_error.c_str(); }
+
+}  // extern "C"
+
+namespace {
+
+// Byte layout of the MoE workspace (every region 256-byte aligned).
+struct MoeLayout {
+  size_t pair_order, pair_pos, expert_off, mt_expert, mt_row0, num_mt, h1, y, total;
+};
+
+MoeLayout moe_layout(int64_t T, int64_t H, int64_t topk, int64_t E, int64_t I) {
+  const int64_t P = T * topk;
+  const int64_t tiles = zt::moe_max_tiles(P, E);
+  MoeLayout l{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  l.pair_order = take(P * 4);
+  l.pair_pos = take(P * 4);
+  l.expert_off = take((E + 1) * 4);
+  l.mt_expert = take(tiles * 4);
+  l.mt_row0 = take(tiles * 4);
+  l.num_mt = take(4);
+  l.h1 = take((size_t)P * I * 2);
+  l.y = take((size_t)P * H * 2);
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t zt_woq_moe_workspace_size(int64_t T, int64_t H, int64_t topk, int64_t E, int64_t I) {
+  if (T <= 0 || H <= 0 || topk <= 0 || E <= 0 || I <= 0) return 0;
+  return moe_layout(T, H, topk, E, I).total;
+}
+
+int zt_woq_moe(const void *x, int64_t T, int64_t H, const int32_t *topk_ids,
+               const void *topk_weights, int32_t weights_dtype, int64_t topk,
+               int32_t skip_weighted, int32_t act, const int32_t *w13,
+               const void *w13_scales, int64_t G13, const void *w13_bias,
+               const int32_t *w2, const void *w2_scales, int64_t G2,
+               const void *w2_bias, int64_t E, int64_t I, void *out,
+               void *workspace, size_t workspace_bytes, zt_stream_t stream) {
+  static const char *op = "zt_woq_moe";
+  if (T < 0 || H <= 0 || I <= 0 || topk <= 0 || E <= 0)
+    return fail(ZT_EINVAL, "%s: need T >= 0 and H, I, topk, E > 0", op);
+  if (H % 128 || I % 128)
+    return fail(ZT_EINVAL, "%s: H=%lld and I=%lld must be multiples of 128", op,
+                (long long)H, (long long)I);
+  if (E > 1024) return fail(ZT_EUNSUPPORTED, "%s: at most 1024 experts (E=%lld)", op, (long long)E);
+  auto groups_ok = [](int64_t K, int64_t G) {
+    if (G < 1 || K % G) return false;
+    if (G == 1) return true;
+    const int64_t gs = K / G, c = gs / 128;
+    return gs % 128 == 0 && (c & (c - 1)) == 0;
+  };
+  if (!groups_ok(H, G13) || !groups_ok(I, G2))
+    return fail(ZT_EINVAL, "%s: scale groups must be one group or a power of two times 128 "
+                "columns (H=%lld G13=%lld, I=%lld G2=%lld)", op, (long long)H, (long long)G13,
+                (long long)I, (long long)G2);
+  if (!is_float_dt(weights_dtype))
+    return fail(ZT_EINVAL, "%s: topk_weights must be fp32 or bf16", op);
+  if (act != ZT_PO_SILU && act != ZT_PO_GELU_ERF && act != ZT_PO_GELU_TANH)
+    return fail(ZT_EUNSUPPORTED, "%s: act must be silu, gelu or gelu_tanh", op);
+  const int64_t P = T * topk;
+  if (P * std::max(H, I) * 2 >= (int64_t)zt::kOobOffset || 2 * I * (H / 8) * 4 >= (int64_t)zt::kOobOffset ||
+      H * (I / 8) * 4 >= (int64_t)zt::kOobOffset)
+    return fail(ZT_EUNSUPPORTED, "%s: operands exceed 32-bit offsets", op);
+  if (T == 0) return ZT_OK;
+  if (!x || !topk_ids || !topk_weights || !w13 || !w13_scales || !w2 || !w2_scales || !out)
+    return fail(ZT_EINVAL, "%s: null tensor pointer", op);
+  const MoeLayout l = moe_layout(T, H, topk, E, I);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, l.total,
+                workspace ? workspace_bytes : (size_t)0);
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  zt::MoeWork w{};
+  w.pair_order = reinterpret_cast<int32_t *>(ws + l.pair_order);
+  w.pair_pos = reinterpret_cast<int32_t *>(ws + l.pair_pos);
+  w.expert_off = reinterpret_cast<int32_t *>(ws + l.expert_off);
+  w.mt_expert = reinterpret_cast<int32_t *>(ws + l.mt_expert);
+  w.mt_row0 = reinterpret_cast<int32_t *>(ws + l.mt_row0);
+  w.num_mt = reinterpret_cast<int32_t *>(ws + l.num_mt);
+  w.h1 = reinterpret_cast<uint16_t *>(ws + l.h1);
+  w.y = reinterpret_cast<uint16_t *>(ws + l.y);
+  zt::MoeArgs a{};
+  a.x = x, a.T = T, a.H = H, a.topk = topk, a.E = E, a.I = I;
+  a.ids = topk_ids, a.wts = topk_weights, a.wts_dt = weights_dtype;
+  a.skip_weighted = skip_weighted != 0, a.act = act;
+  a.w13 = reinterpret_cast<const uint32_t *>(w13);
+  a.s13 = static_cast<const uint16_t *>(w13_scales), a.G13 = G13;
+  a.b13 = static_cast<const uint16_t *>(w13_bias);
+  a.w2 = reinterpret_cast<const uint32_t *>(w2);
+  a.s2 = static_cast<const uint16_t *>(w2_scales), a.G2 = G2;
+  a.b2 = static_cast<const uint16_t *>(w2_bias);
+  a.out = static_cast<uint16_t *>(out);
+  return hip_status(zt::launch_woq_moe(a, w, reinterpret_cast<hipStream_t>(stream)), op);
+}
 
 int32_t zt_version(void) { return 100; }
 

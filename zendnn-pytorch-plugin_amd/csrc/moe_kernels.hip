@@ -1,0 +1,344 @@
+// Grouped int4 weight-only MoE for gfx950 (zentorch_fused_moe with packed
+// int4 expert weights).
+//
+// The reference (src/cpu/cpp/FusedMoE.cpp:289-433, 508-700) groups the
+// (token, k) pairs by expert on the host, runs each active expert's
+// w13 GEMM + gated activation and w2 GEMM, and reduces
+// out[t] = sum_k topk_weights[t, k] * y[t, k].  Here every step runs on the
+// GPU without a host round trip (so the op can be captured in a HIP graph):
+//
+//  * moe_route_kernel   one workgroup: per-expert counts, a stable order of
+//    the pairs by expert (pair_order), each pair's row in that order
+//    (pair_pos, -1 for ids outside [0, E)), expert row offsets, and a table
+//    of (expert, first row) for every BM-row tile of the grouped GEMMs.
+//  * woq_moe_gemm_kernel<GATED>  the DMA int4 GEMM of the dense prefill path
+//    over that tile table.  A rows are gathered (w13: input row of the
+//    pair's token; w2: the pair's row of the intermediate), the weight
+//    pointer is the tile's expert.  GATED tiles pair 64 gate rows n with
+//    their 64 up rows I + n, so the epilogue writes act(g) * u directly.
+//  * moe_combine_kernel out[t] = sum over k (in k order) of
+//    w[t, k] * y[pair_pos[t, k]], fp32, rounded once.
+#include <cstdio>
+#include <cstdlib>
+
+#include "woq_dequant.hpp"
+#include "zt_launch.hpp"
+
+namespace zt {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+constexpr int kMoeBM = 64;    // grouped-GEMM rows (pairs) per tile
+constexpr int kMoeBN = 128;   // weight rows per tile
+constexpr int kXRowB = 256;   // bytes of A per row per 128-wide K step
+constexpr int kWRowB = 64;    // bytes of int4 per weight row per step
+
+__global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int P, int E,
+                                                          MoeWork w) {
+  __shared__ int cnt[1024];
+  __shared__ int base[1024];
+  __shared__ int chunk_e[1024];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < P; i += 1024) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, nt = 0;
+    for (int e = 0; e < E; ++e) {
+      w.expert_off[e] = off;
+      base[e] = off;
+      for (int m0 = 0; m0 < cnt[e]; m0 += kMoeBM) {
+        w.mt_expert[nt] = e;
+        w.mt_row0[nt] = off + m0;
+        ++nt;
+      }
+      off += cnt[e];
+    }
+    w.expert_off[E] = off;
+    w.num_mt[0] = nt;
+  }
+  __syncthreads();
+  // stable positions: rank of pair i among the earlier pairs of its expert
+  for (int c0 = 0; c0 < P; c0 += 1024) {
+    const int i = c0 + tid;
+    int e = i < P ? ids[i] : -1;
+    if (e >= E) e = -1;
+    chunk_e[tid] = e;
+    __syncthreads();
+    int rank = 0;
+    bool last = true;
+    if (e >= 0) {
+      for (int j = 0; j < tid; ++j) rank += chunk_e[j] == e;
+      for (int j = tid + 1; j < 1024 && c0 + j < P; ++j)
+        if (chunk_e[j] == e) { last = false; break; }
+    }
+    int pos = -1;
+    if (e >= 0) {
+      pos = base[e] + rank;
+      w.pair_order[pos] = i;
+    }
+    if (i < P) w.pair_pos[i] = pos;
+    __syncthreads();
+    if (e >= 0 && last) base[e] += rank + 1;
+    __syncthreads();
+  }
+}
+
+template <bool GATED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
+  constexpr int BM = kMoeBM, BN = kMoeBN;
+  constexpr int WTM = BM / 32, WTN = BN / 32;
+  constexpr int STAGE = BM * kXRowB + BN * kWRowB;
+  constexpr int XI = BM * kXRowB / 1024, WI = BN * kWRowB / 1024;
+  constexpr int LPW = (XI + WI) / 4;
+  static_assert((XI + WI) % 4 == 0, "loads must split over 4 waves");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  const int total = g.mt_max * tiles_n;
+  const int t = xcd_contiguous_tile(blockIdx.x, total);
+  const int mt = t / tiles_n, tn = t - mt * tiles_n;
+  if (mt >= g.w.num_mt[0]) return;  // uniform: the whole workgroup leaves
+  const int e = g.w.mt_expert[mt];
+  const int r0 = g.w.mt_row0[mt];
+  const int r_end = g.w.expert_off[e + 1];
+  const int K = g.K, KW = K / 8, N = g.N;
+  const int n0 = GATED ? tn * (BN / 2) : tn * BN;
+  const uint32_t *wexp = g.w_packed + (size_t)e * N * KW;
+  const uint16_t *sexp = g.scales + (size_t)e * g.G * N;
+
+  const auto a_rs = make_rsrc(g.a, (uint32_t)((int64_t)g.a_rows * g.lda * 2));
+  const auto w_rs = make_rsrc(wexp, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(sexp, (uint32_t)(g.G * N * 2));
+
+  // tile weight row j -> expert weight row
+  auto wrow = [&](int j) {
+    if (GATED) return j < BN / 2 ? n0 + j : g.I + n0 + (j - BN / 2);
+    return n0 + j;
+  };
+  // A row of sorted row gr: the token's input row (w13) or the row itself
+  auto arow = [&](int gr) {
+    return GATED ? g.w.pair_order[gr] / g.topk : gr;
+  };
+
+  // byte offset of this lane's A row for each of its x loads (gathered once)
+  const int lda2 = g.lda * 2;
+  int a_base[LPW];
+#pragma unroll
+  for (int q = 0; q < LPW; ++q) {
+    const int li = wv * LPW + q;
+    const int row = li * 4 + (lane >> 4);
+    const int gr = r0 + row;
+    a_base[q] = (li < XI && gr < r_end) ? arow(gr) * lda2 + ((lane & 15) ^ (row & 15)) * 16 : -1;
+  }
+  auto dma = [&](int step) {
+    unsigned char *stage = smem + (step & 1) * STAGE;
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+      const int li = wv * LPW + q;
+      if (li < XI) {
+        const uint32_t off = a_base[q] >= 0 ? (uint32_t)(a_base[q] + step * kXRowB) : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_ptr_t)(stage + li * 1024), 16, off, 0,
+                                                 0, 0);
+      } else {
+        const int wi = li - XI;
+        const int j = wi * 16 + (lane >> 2);
+        const int n = wrow(j);
+        const uint32_t off =
+            n < N ? (uint32_t)(n * KW * 4 + step * kWRowB + (lane & 3) * 16) : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            w_rs, (lds_ptr_t)(stage + BM * kXRowB + wi * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+
+  uint32_t srow[WTN];
+#pragma unroll
+  for (int j = 0; j < WTN; ++j) srow[j] = (uint32_t)min(wrow(wn * (BN / 2) + j * 16 + lr), N - 1);
+
+  f32x4_t acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = K / 128;
+  dma(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ++ks) {
+    const unsigned char *stage = smem + (ks & 1) * STAGE;
+    uint32_t sraw[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const uint32_t sidx = (uint32_t)((ks >> g.cpg_shift) & g.gmask) * (uint32_t)N + srow[j];
+      sraw[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, sidx * 2u, 0, 0);
+    }
+    u32x4_t wraw[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+      wraw[j] = *reinterpret_cast<const u32x4_t *>(
+          stage + BM * kXRowB + (wn * (BN / 2) + j * 16 + lr) * kWRowB + 16 * lg);
+    u32x4_t xf[4][WTM];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < WTM; ++i) {
+        const int row = wm * (BM / 2) + i * 16 + lr;
+        xf[sub][i] = *reinterpret_cast<const u32x4_t *>(
+            stage + row * kXRowB + (((4 * lg + sub) ^ (row & 15)) * 16));
+      }
+    if (ks + 1 < nk) dma(ks + 1);
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      bf16x8_t B[WTN];
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        const float sc = __uint_as_float(sraw[j] << 16);
+        B[j] = __builtin_bit_cast(
+            bf16x8_t, dq8_s4_bf16scale(wraw[j][sub], sc, sc * 0.0625f, -1032.f * sc, -72.f * sc));
+      }
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, xf[sub][i]), B[j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  constexpr int TP = BN + 4;
+  float *tile = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * TP + wn * (BN / 2) + j * 16 + lr] = acc[i][j][r];
+  __syncthreads();
+  const uint16_t *bexp = g.bias ? g.bias + (size_t)e * N : nullptr;
+  constexpr int COLS = GATED ? BN / 2 : BN;
+  for (int idx = tid; idx < BM * (COLS / 4); idx += 256) {
+    const int row = idx / (COLS / 4), c4 = (idx % (COLS / 4)) * 4;
+    const int gr = r0 + row;
+    const int n = n0 + c4;
+    if (gr >= r_end || n >= (GATED ? g.I : N)) continue;
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = tile[row * TP + c4 + r];
+      if (GATED) {
+        float u = tile[row * TP + BN / 2 + c4 + r];
+        if (bexp) {
+          v += bf16_bits_to_f32(bexp[n + r]);
+          u += bf16_bits_to_f32(bexp[g.I + n + r]);
+        }
+        v = unary_op(g.act, v) * u;
+      } else if (bexp) {
+        v += bf16_bits_to_f32(bexp[n + r]);
+      }
+      f[r] = v;
+    }
+    u32x2_t pk;
+    pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+    pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+    *reinterpret_cast<u32x2_t *>(g.out + (size_t)gr * g.ldo + n) = pk;
+  }
+}
+
+// out[t, h] = sum_k w[t, k] * y[pair_pos[t*topk + k], h], k in order.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *y, int H,
+                                                          const int32_t *pair_pos,
+                                                          const void *wts, int wts_dt,
+                                                          int topk, bool skip_weighted,
+                                                          uint16_t *out) {
+  const int t = blockIdx.x;
+  for (int h = threadIdx.x * 8; h < H; h += 256 * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < topk; ++k) {
+      const int p = pair_pos[t * topk + k];
+      if (p < 0) continue;
+      const float wk = skip_weighted ? 1.f : load_elem(wts, wts_dt, (int64_t)t * topk + k);
+      const u32x4_t v = *reinterpret_cast<const u32x4_t *>(y + (size_t)p * H + h);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += wk * __uint_as_float(v[i] << 16);
+        acc[2 * i + 1] += wk * __uint_as_float(v[i] & 0xffff0000u);
+      }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = (uint32_t)f32_to_bf16_bits(acc[2 * i]) | ((uint32_t)f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x4_t *>(out + (size_t)t * H + h) = o;
+  }
+}
+
+template <bool GATED>
+hipError_t launch_moe_gemm(const MoeGemm &g, int tiles_n, hipStream_t s) {
+  const size_t stages = 2 * ((size_t)kMoeBM * kXRowB + (size_t)kMoeBN * kWRowB);
+  const size_t tile = (size_t)kMoeBM * (kMoeBN + 4) * 4;
+  woq_moe_gemm_kernel<GATED><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(256),
+                               stages > tile ? stages : tile, s>>>(g, tiles_n);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int moe_max_tiles(int64_t P, int64_t E) { return (int)((P + kMoeBM - 1) / kMoeBM + E); }
+
+hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
+  const int P = (int)(a.T * a.topk);
+  const int mt_max = moe_max_tiles(P, a.E);
+  moe_route_kernel<<<1, 1024, 0, s>>>(a.ids, P, (int)a.E, w);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+
+  auto shift_of = [](int64_t K, int64_t G) {
+    const int64_t cpg = G == 1 ? 0 : (K / G) / 128;
+    int sh = 0;
+    while (cpg > 1 && (1 << sh) < cpg) ++sh;
+    return sh;
+  };
+  MoeGemm g1{};
+  g1.w = w;
+  g1.a = reinterpret_cast<const uint16_t *>(a.x), g1.lda = (int)a.H, g1.a_rows = (int)a.T;
+  g1.topk = (int)a.topk, g1.K = (int)a.H, g1.N = (int)(2 * a.I), g1.I = (int)a.I;
+  g1.w_packed = a.w13, g1.scales = a.s13, g1.G = (int)a.G13;
+  g1.cpg_shift = shift_of(a.H, a.G13), g1.gmask = a.G13 == 1 ? 0 : 0x7fffffff;
+  g1.bias = a.b13, g1.act = a.act;
+  g1.out = w.h1, g1.ldo = (int)a.I, g1.mt_max = mt_max;
+  err = launch_moe_gemm<true>(g1, (int)(a.I / (kMoeBN / 2)), s);
+  if (err != hipSuccess) return err;
+
+  MoeGemm g2 = g1;
+  g2.a = w.h1, g2.lda = (int)a.I, g2.a_rows = P;
+  g2.K = (int)a.I, g2.N = (int)a.H, g2.I = 0;
+  g2.w_packed = a.w2, g2.scales = a.s2, g2.G = (int)a.G2;
+  g2.cpg_shift = shift_of(a.I, a.G2), g2.gmask = a.G2 == 1 ? 0 : 0x7fffffff;
+  g2.bias = a.b2;
+  g2.out = w.y, g2.ldo = (int)a.H;
+  err = launch_moe_gemm<false>(g2, (int)((a.H + kMoeBN - 1) / kMoeBN), s);
+  if (err != hipSuccess) return err;
+
+  moe_combine_kernel<<<dim3((unsigned)a.T), dim3(256), 0, s>>>(
+      w.y, (int)a.H, w.pair_pos, a.wts, a.wts_dt, (int)a.topk, a.skip_weighted, a.out);
+  return hipGetLastError();
+}
+
+}  // namespace zt

@@ -386,6 +386,95 @@ at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
   return result;
 }
 
+// zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema :728-736)
+// for int4-packed expert weights: w13 int32 [E, 2I, H/8], w2 int32
+// [E, H, I/8] (each expert packed by zentorch_woq_repack_weight) with bf16
+// group scales w13_scales [E, G13, 2I], w2_scales [E, G2, H].  The
+// reference's bf16 / int8 expert weights are refused with a message.
+// `output` ([T, H], the input's dtype) is overwritten with the result, which
+// equals the reference's accumulation into its zero-initialised output.
+void fused_moe(at::Tensor &output, const at::Tensor &input, const at::Tensor &w13,
+               const at::Tensor &w2, const c10::optional<at::Tensor> &w13_bias,
+               const c10::optional<at::Tensor> &w2_bias, const at::Tensor &topk_weights,
+               const at::Tensor &topk_id, bool skip_weighted, c10::string_view act,
+               const c10::optional<at::Tensor> &w13_scales,
+               const c10::optional<at::Tensor> &w2_scales, c10::string_view zentorch_op_name) {
+  (void)zentorch_op_name;
+  const char *op = "zentorch_fused_moe";
+  TORCH_CHECK(input.dim() == 2 && input.scalar_type() == at::kBFloat16,
+              op, ": input must be a 2D bfloat16 tensor [T, H]");
+  TORCH_CHECK(w13.scalar_type() == at::kInt && w2.scalar_type() == at::kInt,
+              op, ": this build runs int4-packed expert weights (int32 [E, 2I, H/8] and "
+              "[E, H, I/8] from zentorch_woq_repack_weight per expert); got w13 ",
+              w13.scalar_type(), " and w2 ", w2.scalar_type());
+  TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, op, ": w13 and w2 must be 3D");
+  const int64_t T = input.size(0), H = input.size(1);
+  const int64_t E = w13.size(0), I = w13.size(1) / 2;
+  TORCH_CHECK(w13.size(1) == 2 * I && w13.size(2) * 8 == H, op,
+              ": w13 must be [E, 2I, H/8] for H=", H, ", got ", w13.sizes());
+  TORCH_CHECK(w2.size(0) == E && w2.size(1) == H && w2.size(2) * 8 == I, op,
+              ": w2 must be [E, H, I/8] = [", E, ", ", H, ", ", I / 8, "], got ", w2.sizes());
+  TORCH_CHECK(w13_scales.has_value() && w13_scales->defined() && w2_scales.has_value() &&
+                  w2_scales->defined(),
+              op, ": int4 experts need w13_scales and w2_scales");
+  const at::Tensor s13 = w13_scales->contiguous(), s2 = w2_scales->contiguous();
+  TORCH_CHECK(s13.scalar_type() == at::kBFloat16 && s2.scalar_type() == at::kBFloat16,
+              op, ": scales must be bfloat16");
+  TORCH_CHECK(s13.dim() == 3 && s13.size(0) == E && s13.size(2) == 2 * I, op,
+              ": w13_scales must be [E, G13, 2I], got ", s13.sizes());
+  TORCH_CHECK(s2.dim() == 3 && s2.size(0) == E && s2.size(2) == H, op,
+              ": w2_scales must be [E, G2, H], got ", s2.sizes());
+  TORCH_CHECK(topk_id.dim() == 2 && topk_id.size(0) == T, op, ": topk_id must be [T, K]");
+  const int64_t topk = topk_id.size(1);
+  TORCH_CHECK(topk_weights.sizes() == topk_id.sizes(), op,
+              ": topk_weights must have topk_id's shape ", topk_id.sizes());
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat || topk_weights.scalar_type() == at::kBFloat16,
+              op, ": topk_weights must be float32 or bfloat16");
+  TORCH_CHECK(!skip_weighted || topk == 1, op, ": skip_weighted requires K == 1 (got K=", topk, ")");
+  int32_t act_id;
+  if (act == "silu") act_id = ZT_PO_SILU;
+  else if (act == "gelu") act_id = ZT_PO_GELU_ERF;
+  else if (act == "gelu_tanh") act_id = ZT_PO_GELU_TANH;
+  else TORCH_CHECK(false, op, ": activation '", std::string(act), "' is not supported here "
+                   "(silu, gelu, gelu_tanh)");
+  TORCH_CHECK(output.sizes() == input.sizes() && output.scalar_type() == input.scalar_type() &&
+                  output.is_contiguous(),
+              op, ": output must be a contiguous tensor like input");
+  at::Tensor b13, b2;
+  if (w13_bias.has_value() && w13_bias->defined()) {
+    b13 = w13_bias->contiguous();
+    TORCH_CHECK(b13.scalar_type() == at::kBFloat16 && b13.numel() == E * 2 * I, op,
+                ": w13_bias must be bfloat16 [E, 2I]");
+  }
+  if (w2_bias.has_value() && w2_bias->defined()) {
+    b2 = w2_bias->contiguous();
+    TORCH_CHECK(b2.scalar_type() == at::kBFloat16 && b2.numel() == E * H, op,
+                ": w2_bias must be bfloat16 [E, H]");
+  }
+  for (const at::Tensor *t : std::initializer_list<const at::Tensor *>{
+           &input, &w13, &w2, &s13, &s2, &topk_id, &topk_weights, &output})
+    check_device(*t, input, op, "argument");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
+  if (T == 0) return;
+  const at::Tensor x = input.contiguous();
+  const at::Tensor ids = topk_id.to(at::kInt).contiguous();
+  const at::Tensor wts = topk_weights.contiguous();
+  const at::Tensor w13c = w13.contiguous(), w2c = w2.contiguous();
+  const size_t ws_bytes = zt_woq_moe_workspace_size(T, H, topk, E, I);
+  at::Tensor ws = at::empty({(int64_t)ws_bytes}, input.options().dtype(at::kByte));
+  const int rc = zt_woq_moe(
+      x.data_ptr(), T, H, ids.data_ptr<int32_t>(), wts.data_ptr(), zt_dtype_of(wts), topk,
+      skip_weighted ? 1 : 0, act_id, w13c.data_ptr<int32_t>(), s13.data_ptr(), s13.size(1),
+      b13.defined() ? b13.data_ptr() : nullptr, w2c.data_ptr<int32_t>(), s2.data_ptr(),
+      s2.size(1), b2.defined() ? b2.data_ptr() : nullptr, E, I, output.data_ptr(),
+      ws.data_ptr(), ws_bytes, reinterpret_cast<zt_stream_t>(current_stream()));
+  TORCH_CHECK(rc == ZT_OK, op, ": ", zt_last_error_string());
+}
+
+// The reference drops its per-expert weight-view caches here
+// (FusedMoE.cpp:726); this build keeps no such cache.
+void flush_moe_weight_cache() {}
+
 }  // namespace zentorch_hip
 
 TORCH_LIBRARY(zentorch, m) {
@@ -437,6 +526,14 @@ TORCH_LIBRARY(zentorch, m) {
         "Tensor weight_scales, Tensor? bias=None, *, "
         "str zentorch_op_name="
         "'zentorch::zentorch_dynamic_qlinear') -> Tensor");
+  m.def("zentorch_fused_moe(Tensor(a!) output, Tensor input, "
+        "Tensor w13, Tensor w2, "
+        "Tensor? w13_bias, Tensor? w2_bias, "
+        "Tensor topk_weights, Tensor topk_id, "
+        "bool skip_weighted, str act, "
+        "Tensor? w13_scales=None, Tensor? w2_scales=None, "
+        "*, str zentorch_op_name='zentorch::zentorch_fused_moe') -> ()");
+  m.def("zentorch_flush_moe_weight_cache() -> ()", &zentorch_hip::flush_moe_weight_cache);
 }
 
 TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
@@ -453,4 +550,5 @@ TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
   m.impl("zentorch_woq_repack_weight", woq_repack_weight);
   m.impl("zentorch_woq_repack_from_int4pack", woq_repack_from_int4pack);
   m.impl("zentorch_dynamic_qlinear", dynamic_qlinear);
+  m.impl("zentorch_fused_moe", fused_moe);
 }

@@ -78,4 +78,51 @@ hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                                int8_t *qx, float *sx, hipStream_t s);
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);
 
+// Grouped int4 MoE (moe_kernels.hip).  Device scratch of one call.
+struct MoeWork {
+  int32_t *pair_order;  // [P] pair index (t*topk + k) in expert order
+  int32_t *pair_pos;    // [P] row of each pair in that order, -1 if dropped
+  int32_t *expert_off;  // [E + 1]
+  int32_t *mt_expert;   // [tiles] expert of each grouped-GEMM row tile
+  int32_t *mt_row0;     // [tiles] its first row
+  int32_t *num_mt;      // [1] tiles in use
+  uint16_t *h1;         // [P, I] bf16 activated intermediate
+  uint16_t *y;          // [P, H] bf16 expert outputs
+};
+
+struct MoeArgs {
+  const void *x;  // [T, H] bf16
+  int64_t T, H, topk, E, I;
+  const int32_t *ids;  // [T, topk]
+  const void *wts;     // [T, topk] bf16 or fp32
+  int wts_dt;
+  bool skip_weighted;
+  int act;  // ZT_PO_SILU, ZT_PO_GELU_ERF or ZT_PO_GELU_TANH on the gate half
+  const uint32_t *w13;  // [E, 2I, H/8] packed int4
+  const uint16_t *s13;  // [E, G13, 2I] bf16
+  const uint16_t *b13;  // [E, 2I] bf16 or null
+  int64_t G13;
+  const uint32_t *w2;   // [E, H, I/8]
+  const uint16_t *s2;   // [E, G2, H] bf16
+  const uint16_t *b2;   // [E, H] bf16 or null
+  int64_t G2;
+  uint16_t *out;        // [T, H] bf16
+};
+
+struct MoeGemm {
+  MoeWork w;
+  const uint16_t *a;  // A rows (gathered through pair_order when gated)
+  int lda, a_rows, topk, K, N, I;
+  const uint32_t *w_packed;
+  const uint16_t *scales;
+  int G, cpg_shift, gmask;
+  const uint16_t *bias;
+  int act;
+  uint16_t *out;
+  int ldo, mt_max;
+};
+
+int moe_max_tiles(int64_t P, int64_t E);
+hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s);
+
 }  // namespace zt

@@ -83,3 +83,11 @@ def meta_zentorch_woq_repack_weight(unpacked_weight):
 def meta_zentorch_woq_repack_from_int4pack(packed_weight):
     K = packed_weight.size(1) * 2
     return packed_weight.new_empty((packed_weight.size(0), K // 8), dtype=torch.int32)
+
+
+@register_meta("zentorch_fused_moe")
+def meta_zentorch_fused_moe(output, input, w13, w2, w13_bias, w2_bias, topk_weights, topk_id,
+                            skip_weighted, act, w13_scales=None, w2_scales=None,
+                            zentorch_op_name="zentorch::zentorch_fused_moe"):
+    # writes `output` in place and returns nothing (FusedMoE.cpp:728-736)
+    return None
