@@ -11,7 +11,8 @@ resident in HBM before timing starts.
 
 Secondary workloads in the same line (``workloads``): the Llama-3-8B decode
 layer at M in {1, 8, 16, 64} (config 2), dynamic int8 qlinear at M=128
-(config 1) and the M=2048 prefill layer through both paths (config 3).
+(config 1), the M=2048 prefill layer through both paths (config 3) and the
+Mixtral-shaped int4 MoE FFN over 256 tokens (config 4).
 
 ``roofline`` is for the dominant kernel of the headline workload (the
 decode GEMV, one launch per call): ``achieved`` = algorithmic bytes per
@@ -241,6 +242,42 @@ def bench_woq_prefill(args, gen):
             "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS}
 
 
+def bench_moe(args, gen):
+    """Mixtral-shaped int4 MoE FFN, 8 experts, hidden 4096,
+    intermediate 14336, top-2 of router logits over 256 tokens, through
+    zentorch_fused_moe (routing, gathered gate_up GEMM with fused silu_mul,
+    down GEMM, weighted combine; one op call = one step)."""
+    T, H, I, E, k = 256, 4096, 14336, 8, 2
+    dev = "cuda"
+    ops = torch.ops.zentorch
+    w13, w2, s13, s2 = [], [], [], []
+    for _ in range(E):
+        w13.append(ops.zentorch_woq_repack_weight(
+            torch.randint(-8, 8, (2 * I, H), dtype=torch.int8, device=dev)))
+        w2.append(ops.zentorch_woq_repack_weight(
+            torch.randint(-8, 8, (H, I), dtype=torch.int8, device=dev)))
+        s13.append((torch.rand(H // 128, 2 * I, device=dev) * 0.015 + 0.005).bfloat16())
+        s2.append((torch.rand(I // 128, H, device=dev) * 0.015 + 0.005).bfloat16())
+    w13, w2, s13, s2 = (torch.stack(t) for t in (w13, w2, s13, s2))
+    x = torch.randn(T, H, generator=gen).bfloat16().to(dev)
+    logits = torch.randn(T, E, generator=gen)
+    top, ids = torch.topk(logits, k)
+    wts = torch.softmax(top, dim=-1).to(dev)
+    ids = ids.int().to(dev)
+    out = torch.empty_like(x)
+    call = lambda: ops.zentorch_fused_moe(out, x, w13, w2, None, None, wts, ids, False,
+                                          "silu", s13, s2)
+    reps = max(2, args.steps // 64)
+    t = graph_time([call], reps, args.warmup)
+    wbytes = E * (2 * I * H // 2 + H * I // 2) + E * (H // 128 * 2 * I + I // 128 * H) * 2
+    byts = wbytes + T * H * 2 * 2
+    flops = 2 * T * k * (2 * I * H + H * I)
+    return {"T": T, "H": H, "I": I, "E": E, "topk": k, "s_per_layer": t,
+            "GBps": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / HBM_PEAK_GBS,
+            "TFLOPS": flops / t / 1e12, "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS,
+            "weight_bytes": wbytes}
+
+
 def cpu_baseline(budget_s=12.0):
     """CPU oracle (port of the reference semantics) on config 0's shape."""
     from oracle import oracle as O
@@ -284,7 +321,7 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default=None,
-                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | traffic")
+                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | moe | traffic")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -311,6 +348,8 @@ def main():
                 2048, [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)], args, gen)
         if only in (None, "prefill_int4"):
             res["prefill_int4_m2048"] = bench_woq_prefill(args, gen)
+        if only in (None, "moe"):
+            res["moe_mixtral_t256"] = bench_moe(args, gen)
 
     c0 = res.get("config0")
     line = {

@@ -45,6 +45,60 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(
   }
 }
 
+// The same per-row quantisation for bf16 rows with K % 8 == 0, 16-byte
+// aligned: each thread holds up to VPT 8-element vectors of its row in
+// registers between the amax and the quantise pass and writes 8 bytes of qx
+// at a time.  Bit-identical to dyn_quantize_kernel.
+template <int VPT>
+__global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *x, int64_t K,
+                                                                 int8_t *qx, float *sx) {
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t m = blockIdx.x;
+  const u32x4_t *row = reinterpret_cast<const u32x4_t *>(x + m * K);
+  const int nv = (int)(K / 8);
+  u32x4_t v[VPT];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int j = tid + 256 * i;
+    v[i] = j < nv ? row[j] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[i][w] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[i][w] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if (lane == 0) wmax[wv] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (!(amax >= 1e-12f)) amax = 1e-12f;
+  const float s = __fdiv_rn(amax, 127.0f);
+  if (tid == 0) sx[m] = s;
+  auto q1 = [&](float f) {
+    float r = rintf(__fdiv_rn(f, s));
+    r = fminf(fmaxf(r, -128.f), 127.f);
+    return (uint32_t)(uint8_t)(int8_t)(int)r;
+  };
+  u32x2_t *out = reinterpret_cast<u32x2_t *>(qx + m * K);
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int j = tid + 256 * i;
+    if (j >= nv) break;
+    u32x2_t o;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t a0 = v[i][2 * h], a1 = v[i][2 * h + 1];
+      o[h] = q1(__uint_as_float(a0 << 16)) | (q1(__uint_as_float(a0 & 0xffff0000u)) << 8) |
+             (q1(__uint_as_float(a1 << 16)) << 16) | (q1(__uint_as_float(a1 & 0xffff0000u)) << 24);
+    }
+    out[j] = o;
+  }
+}
+
 __device__ __forceinline__ void dyn_epilogue(const DynArgs &a, int64_t m,
                                              int64_t n, int32_t acc) {
   if (a.y_dt == ZT_DT_S32) {
@@ -163,7 +217,7 @@ constexpr int acc_pitch() { return BN + 4; }
 template <int BM, int BN>
 constexpr size_t s8_tiled_lds() {
   const size_t stages = 2 * (size_t)(BM + BN) * kTLDR;
-  const size_t acc = (size_t)BM * acc_pitch<BN>() * 4;
+  const size_t acc = (size_t)BM * acc_pitch<BN>() * 4 + (size_t)BM * 4;
   return stages > acc ? stages : acc;
 }
 
@@ -201,6 +255,66 @@ __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i3
 #pragma unroll
   for (int r = 0; r < 4; ++r)
     if (n + r < N) dyn_epilogue(a, m, n + r, v[r]);
+}
+
+// Epilogue of a BM x BN int32 tile staged in LDS (row pitch acc_pitch),
+// 256 threads.  BN/4 divides 256, so each thread keeps the same four columns
+// for all its rows: their weight scales and bias are loaded once, and the
+// row scales come from LDS (sx_l).  Same arithmetic as dyn_epilogue:
+// ((float)acc * sx[m]) * sw[n] + bias[n].  Post-ops, int32 output and a row
+// length that is not a multiple of 4 take the general path.
+template <int BM, int BN>
+__device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t *tile,
+                                                 const float *sx_l, int m0, int n0, int tid) {
+  constexpr int AP = acc_pitch<BN>();
+  constexpr int G4 = BN / 4;
+  static_assert(256 % G4 == 0, "four-column groups must divide the threads");
+  const int M = (int)a.M, N = (int)a.N;
+  const int c4 = (tid % G4) * 4, n = n0 + c4;
+  if (a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0) {
+    if (n >= N) return;
+    float sw[4], b[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sw[r] = load_elem(a.sw, a.sw_dt, n + r);
+      b[r] = a.bias ? load_elem(a.bias, a.b_dt, n + r) : 0.f;
+    }
+    for (int row = tid / G4; row < BM && m0 + row < M; row += 256 / G4) {
+      const int m = m0 + row;
+      const i32x4_t v = *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4);
+      const float sxm = sx_l[row];
+      float f[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = (float)v[r] * sxm;
+        t = t * sw[r];
+        f[r] = a.bias ? t + b[r] : t;
+      }
+      if (a.y_dt == ZT_DT_BF16) {
+        u32x2_t pk;
+        pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+        pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+        *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
+      } else {
+        *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
+            f32x4_t{f[0], f[1], f[2], f[3]};
+      }
+    }
+    return;
+  }
+  for (int idx = tid; idx < BM * G4; idx += 256) {
+    const int row = idx / G4, cc = (idx % G4) * 4;
+    const int m = m0 + row, nn = n0 + cc;
+    if (m < M && nn < N)
+      dyn_epilogue4(a, m, nn, *reinterpret_cast<const i32x4_t *>(tile + row * AP + cc));
+  }
+}
+
+// Stage the row scales of rows m0..m0+BM of the tile for s8_tile_epilogue.
+template <int BM>
+__device__ __forceinline__ void s8_stage_row_scales(const DynArgs &a, float *sx_l, int m0, int tid) {
+  if (a.y_dt == ZT_DT_S32) return;
+  for (int r = tid; r < BM; r += 256) sx_l[r] = m0 + r < (int)a.M ? a.sx[m0 + r] : 0.f;
 }
 
 template <int BM, int BN>
@@ -323,13 +437,10 @@ void s8_gemm_tiled_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
       for (int r = 0; r < 4; ++r)
         tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * AP + wn * (BN / 2) + j * 16 + lr] =
             acc[i][j][r];
+  float *sx_l = reinterpret_cast<float *>(tile + BM * AP);
+  s8_stage_row_scales<BM>(a, sx_l, m0, tid);
   __syncthreads();
-  for (int idx = tid; idx < BM * (BN / 4); idx += 256) {
-    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
-    const int m = m0 + row, n = n0 + c4;
-    if (m < M && n < N)
-      dyn_epilogue4(a, m, n, *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4));
-  }
+  s8_tile_epilogue<BM, BN>(a, tile, sx_l, m0, n0, tid);
 }
 
 // The same tiling with the K slabs moved by the buffer unit straight into
@@ -344,7 +455,7 @@ void s8_gemm_tiled_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
 template <int BM, int BN, int S>
 constexpr size_t s8_dma_lds() {
   const size_t stages = (size_t)S * (BM + BN) * kTBK;
-  const size_t acc = (size_t)BM * acc_pitch<BN>() * 4;
+  const size_t acc = (size_t)BM * acc_pitch<BN>() * 4 + (size_t)BM * 4;
   return stages > acc ? stages : acc;
 }
 
@@ -468,13 +579,10 @@ void s8_gemm_dma_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
       for (int r = 0; r < 4; ++r)
         tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * AP + wn * (BN / 2) + j * 16 + lr] =
             acc[i][j][r];
+  float *sx_l = reinterpret_cast<float *>(tile + BM * AP);
+  s8_stage_row_scales<BM>(a, sx_l, m0, tid);
   __syncthreads();
-  for (int idx = tid; idx < BM * (BN / 4); idx += 256) {
-    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
-    const int m = m0 + row, n = n0 + c4;
-    if (m < M && n < N)
-      dyn_epilogue4(a, m, n, *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4));
-  }
+  s8_tile_epilogue<BM, BN>(a, tile, sx_l, m0, n0, tid);
 }
 
 template <int BM, int BN, int S>
@@ -595,14 +703,58 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunk
       }
   }
   __syncthreads();
-  for (int idx = tid; idx < 16 * MT * 4 * TPW; idx += 64 * NW) {
-    const int m = idx / (4 * TPW), c4 = (idx % (4 * TPW)) * 4;
-    if (m >= M || n0 + c4 >= N) continue;
+  // 4*TPW four-column groups divide the 64*NW threads: a thread keeps its
+  // columns, so their weight scales and bias are loaded once
+  constexpr int G4 = 4 * TPW;
+  if ((64 * NW) % G4 != 0) {  // groups do not divide the threads: general loop
+    for (int idx = tid; idx < 16 * MT * G4; idx += 64 * NW) {
+      const int m = idx / G4, cc = (idx % G4) * 4;
+      if (m >= M || n0 + cc >= N) continue;
+      i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + cc);
+#pragma unroll
+      for (int w = 1; w < 4; ++w)
+        v += *reinterpret_cast<const i32x4_t *>(slab + (w * 16 * MT + m) * P + cc);
+      dyn_epilogue4(a, m, n0 + cc, v);
+    }
+    return;
+  }
+  const int c4 = (tid % G4) * 4, n = n0 + c4;
+  if (n >= N) return;
+  const bool fast = a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0;
+  float sw[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+  if (fast) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sw[r] = load_elem(a.sw, a.sw_dt, n + r);
+      if (a.bias) b[r] = load_elem(a.bias, a.b_dt, n + r);
+    }
+  }
+  for (int m = tid / G4; m < M && m < 16 * MT; m += (64 * NW) / G4) {
     i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + c4);
 #pragma unroll
     for (int w = 1; w < 4; ++w)
       v += *reinterpret_cast<const i32x4_t *>(slab + (w * 16 * MT + m) * P + c4);
-    dyn_epilogue4(a, m, n0 + c4, v);
+    if (!fast) {
+      dyn_epilogue4(a, m, n, v);
+      continue;
+    }
+    const float sxm = a.sx[m];
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = (float)v[r] * sxm;
+      t = t * sw[r];
+      f[r] = a.bias ? t + b[r] : t;
+    }
+    if (a.y_dt == ZT_DT_BF16) {
+      u32x2_t pk;
+      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
+    } else {
+      *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
+          f32x4_t{f[0], f[1], f[2], f[3]};
+    }
   }
 }
 
@@ -626,7 +778,8 @@ hipError_t launch_s8_skinny(const DynArgs &a, hipStream_t s) {
   if (mt <= MT_ && (!tpw || (tpw == TPW_ && pf == PF_ && nw == NW_)))          \
     return launch_s8_skinny_t<MT_, TPW_, PF_, NW_>(a, s);
   ZT_SK(1, 4, 4, 8) ZT_SK(2, 4, 4, 8) ZT_SK(4, 2, 4, 8)
-  ZT_SK(8, 2, 3, 8) ZT_SK(8, 3, 4, 4) ZT_SK(8, 2, 4, 4) ZT_SK(8, 3, 2, 8) ZT_SK(8, 1, 4, 8)
+  ZT_SK(8, 3, 2, 8) ZT_SK(8, 2, 3, 8) ZT_SK(8, 2, 4, 4) ZT_SK(8, 1, 4, 8) ZT_SK(8, 4, 2, 8)
+  ZT_SK(8, 3, 4, 4)
 #undef ZT_SK
   return hipErrorInvalidValue;
 }
@@ -645,6 +798,19 @@ hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                                int8_t *qx, float *sx, hipStream_t s) {
   if (M == 0) return hipSuccess;
+  const bool vec = x_dt == ZT_DT_BF16 && K % 8 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(qx)) & 15u) == 0;
+  const int64_t per = (K / 8 + 255) / 256;  // 8-element vectors per thread
+  if (vec && per <= 8) {
+    const uint16_t *xb = static_cast<const uint16_t *>(x);
+    if (per <= 2)
+      dyn_quantize_bf16_kernel<2><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx);
+    else if (per <= 4)
+      dyn_quantize_bf16_kernel<4><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx);
+    else
+      dyn_quantize_bf16_kernel<8><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)M), dim3(256), 0, s, x,
                      x_dt, K, qx, sx);
   return hipGetLastError();
