@@ -31,7 +31,6 @@ namespace {
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 constexpr int kMoeBM = 64;    // grouped-GEMM rows (pairs) per tile
-constexpr int kMoeBN = 128;   // weight rows per tile
 constexpr int kXRowB = 256;   // bytes of A per row per 128-wide K step
 constexpr int kWRowB = 64;    // bytes of int4 per weight row per step
 
@@ -90,11 +89,17 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int
   }
 }
 
-template <bool GATED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
-  constexpr int BM = kMoeBM, BN = kMoeBN;
-  constexpr int WTM = BM / 32, WTN = BN / 32;
+// BM = 64 rows (pairs) x BN weight rows per tile, 4 waves split along N
+// only: each wave owns all four 16-row token tiles and BN/4 weight rows, so
+// every weight fragment is dequantised once and feeds four MFMAs (the
+// dequantisation, not the MFMA, bounds a 64-row tile).  GATED tiles hold
+// BN/2 gate rows n0.. and their BN/2 up rows I + n0..; waves 0-1 own the
+// gate half, waves 2-3 the up half, and the epilogue pairs column c with
+// column BN/2 + c.
+template <bool GATED, int BN>
+__global__ __launch_bounds__(256) void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
+  constexpr int BM = kMoeBM;
+  constexpr int WTM = BM / 16, WTN = BN / 64;  // 16x16 tiles per wave
   constexpr int STAGE = BM * kXRowB + BN * kWRowB;
   constexpr int XI = BM * kXRowB / 1024, WI = BN * kWRowB / 1024;
   constexpr int LPW = (XI + WI) / 4;
@@ -103,7 +108,6 @@ void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv >> 1, wn = wv & 1;
   const int lr = lane & 15, lg = lane >> 4;
 
   const int total = g.mt_max * tiles_n;
@@ -127,10 +131,6 @@ void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
     if (GATED) return j < BN / 2 ? n0 + j : g.I + n0 + (j - BN / 2);
     return n0 + j;
   };
-  // A row of sorted row gr: the token's input row (w13) or the row itself
-  auto arow = [&](int gr) {
-    return GATED ? g.w.pair_order[gr] / g.topk : gr;
-  };
 
   // byte offset of this lane's A row for each of its x loads (gathered once)
   const int lda2 = g.lda * 2;
@@ -140,7 +140,10 @@ void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
     const int li = wv * LPW + q;
     const int row = li * 4 + (lane >> 4);
     const int gr = r0 + row;
-    a_base[q] = (li < XI && gr < r_end) ? arow(gr) * lda2 + ((lane & 15) ^ (row & 15)) * 16 : -1;
+    int off = -1;
+    if (li < XI && gr < r_end)
+      off = (GATED ? g.w.pair_order[gr] / g.topk : gr) * lda2 + ((lane & 15) ^ (row & 15)) * 16;
+    a_base[q] = off;
   }
   auto dma = [&](int step) {
     unsigned char *stage = smem + (step & 1) * STAGE;
@@ -163,9 +166,10 @@ void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
     }
   };
 
+  // this wave's weight rows: tile rows wv*(BN/4) + j*16 + lr
   uint32_t srow[WTN];
 #pragma unroll
-  for (int j = 0; j < WTN; ++j) srow[j] = (uint32_t)min(wrow(wn * (BN / 2) + j * 16 + lr), N - 1);
+  for (int j = 0; j < WTN; ++j) srow[j] = (uint32_t)min(wrow(wv * (BN / 4) + j * 16 + lr), N - 1);
 
   f32x4_t acc[WTM][WTN];
 #pragma unroll
@@ -189,13 +193,13 @@ void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
 #pragma unroll
     for (int j = 0; j < WTN; ++j)
       wraw[j] = *reinterpret_cast<const u32x4_t *>(
-          stage + BM * kXRowB + (wn * (BN / 2) + j * 16 + lr) * kWRowB + 16 * lg);
+          stage + BM * kXRowB + (wv * (BN / 4) + j * 16 + lr) * kWRowB + 16 * lg);
     u32x4_t xf[4][WTM];
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
       for (int i = 0; i < WTM; ++i) {
-        const int row = wm * (BM / 2) + i * 16 + lr;
+        const int row = i * 16 + lr;
         xf[sub][i] = *reinterpret_cast<const u32x4_t *>(
             stage + row * kXRowB + (((4 * lg + sub) ^ (row & 15)) * 16));
       }
@@ -229,7 +233,7 @@ void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
     for (int j = 0; j < WTN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * TP + wn * (BN / 2) + j * 16 + lr] = acc[i][j][r];
+        tile[(i * 16 + 4 * lg + r) * TP + wv * (BN / 4) + j * 16 + lr] = acc[i][j][r];
   __syncthreads();
   const uint16_t *bexp = g.bias ? g.bias + (size_t)e * N : nullptr;
   constexpr int COLS = GATED ? BN / 2 : BN;
@@ -289,12 +293,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *y, int
   }
 }
 
-template <bool GATED>
+template <bool GATED, int BN>
 hipError_t launch_moe_gemm(const MoeGemm &g, int tiles_n, hipStream_t s) {
-  const size_t stages = 2 * ((size_t)kMoeBM * kXRowB + (size_t)kMoeBN * kWRowB);
-  const size_t tile = (size_t)kMoeBM * (kMoeBN + 4) * 4;
-  woq_moe_gemm_kernel<GATED><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(256),
-                               stages > tile ? stages : tile, s>>>(g, tiles_n);
+  const size_t stages = 2 * ((size_t)kMoeBM * kXRowB + (size_t)BN * kWRowB);
+  const size_t tile = (size_t)kMoeBM * (BN + 4) * 4;
+  woq_moe_gemm_kernel<GATED, BN><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(256),
+                                   stages > tile ? stages : tile, s>>>(g, tiles_n);
   return hipGetLastError();
 }
 
@@ -323,7 +327,8 @@ hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
   g1.cpg_shift = shift_of(a.H, a.G13), g1.gmask = a.G13 == 1 ? 0 : 0x7fffffff;
   g1.bias = a.b13, g1.act = a.act;
   g1.out = w.h1, g1.ldo = (int)a.I, g1.mt_max = mt_max;
-  err = launch_moe_gemm<true>(g1, (int)(a.I / (kMoeBN / 2)), s);
+  // gate_up: 128 gate + 128 up rows per tile; I % 128 == 0 (host-checked)
+  err = launch_moe_gemm<true, 256>(g1, (int)(a.I / 128), s);
   if (err != hipSuccess) return err;
 
   MoeGemm g2 = g1;
@@ -333,7 +338,7 @@ hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
   g2.cpg_shift = shift_of(a.I, a.G2), g2.gmask = a.G2 == 1 ? 0 : 0x7fffffff;
   g2.bias = a.b2;
   g2.out = w.y, g2.ldo = (int)a.H;
-  err = launch_moe_gemm<false>(g2, (int)((a.H + kMoeBN - 1) / kMoeBN), s);
+  err = launch_moe_gemm<false, 128>(g2, (int)((a.H + 127) / 128), s);
   if (err != hipSuccess) return err;
 
   moe_combine_kernel<<<dim3((unsigned)a.T), dim3(256), 0, s>>>(
