@@ -30,9 +30,11 @@ namespace {
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-constexpr int kMoeBM = 64;    // grouped-GEMM rows (pairs) per tile
+constexpr int kMoeBM = 128;   // grouped-GEMM rows (pairs) per tile
 constexpr int kXRowB = 256;   // bytes of A per row per 128-wide K step
 constexpr int kWRowB = 64;    // bytes of int4 per weight row per step
+constexpr int kXStage = kMoeBM * kXRowB;  // one LDS buffer of A rows
+constexpr int kMoeDepth = 4;  // K steps of weights loaded ahead
 
 __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int P, int E,
                                                           MoeWork w) {
@@ -89,179 +91,271 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int
   }
 }
 
-// BM = 64 rows (pairs) x BN weight rows per tile, 4 waves split along N
-// only: each wave owns all four 16-row token tiles and BN/4 weight rows, so
-// every weight fragment is dequantised once and feeds four MFMAs (the
-// dequantisation, not the MFMA, bounds a 64-row tile).  GATED tiles hold
-// BN/2 gate rows n0.. and their BN/2 up rows I + n0..; waves 0-1 own the
-// gate half, waves 2-3 the up half, and the epilogue pairs column c with
-// column BN/2 + c.
-template <bool GATED, int BN>
-__global__ __launch_bounds__(256) void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
-  constexpr int BM = kMoeBM;
-  constexpr int WTM = BM / 16, WTN = BN / 64;  // 16x16 tiles per wave
-  constexpr int STAGE = BM * kXRowB + BN * kWRowB;
-  constexpr int XI = BM * kXRowB / 1024, WI = BN * kWRowB / 1024;
-  constexpr int LPW = (XI + WI) / 4;
-  static_assert((XI + WI) % 4 == 0, "loads must split over 4 waves");
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+// s_waitcnt immediate that waits for at most n outstanding vector-memory
+// loads (n < 64) and nothing else
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// One grouped-GEMM tile: NB 16-row blocks of the expert's pairs (rows
+// r0 .. r0 + 16 NB; the blocks of the 128-row tile past the expert's last
+// pair cost nothing) times BN weight rows.
+//  * The 4 waves split along N only: each wave owns BN/4 weight rows, so
+//    every weight fragment is dequantised once and feeds NB MFMAs.
+//  * Weights and scales go straight from HBM to registers two K steps
+//    ahead, in three rotating register sets: they never touch LDS and no
+//    barrier waits on them.
+//  * The gathered A rows go to LDS by DMA (16-byte chunks XOR-swizzled by
+//    the row's low 4 bits), double-buffered: x(ks + 1) is issued at the top
+//    of step ks, after the barrier that retires step ks - 1's reads of that
+//    buffer.
+//  * GATED tiles hold BN/2 gate rows n0.. and their BN/2 up rows I + n0..;
+//    each wave owns BN/8 of each, so act(g) * u is formed in registers.
+// The loop's vector-memory order per step is [x(ks + 1): NB loads]
+// [weights + scales of ks + 2: 2 WTN loads]; x(ks) (and everything issued
+// before it) has landed once at most 2 WTN loads are outstanding.
+template <bool GATED, int BN, int NB>
+__device__ __forceinline__ void moe_tile(const MoeGemm &g, int e, int r0, int r_end, int tn,
+                                         unsigned char *smem) {
+  constexpr int WTN = BN / 64;  // 16-column tiles per wave
+  constexpr int WR = BN / 4;    // weight rows per wave
+  constexpr int HALF = GATED ? WTN / 2 : WTN;
+  static_assert(!GATED || WTN % 2 == 0, "gated tiles pair gate and up column tiles");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
-
-  const int total = g.mt_max * tiles_n;
-  const int t = xcd_contiguous_tile(blockIdx.x, total);
-  const int mt = t / tiles_n, tn = t - mt * tiles_n;
-  if (mt >= g.w.num_mt[0]) return;  // uniform: the whole workgroup leaves
-  const int e = g.w.mt_expert[mt];
-  const int r0 = g.w.mt_row0[mt];
-  const int r_end = g.w.expert_off[e + 1];
   const int K = g.K, KW = K / 8, N = g.N;
   const int n0 = GATED ? tn * (BN / 2) : tn * BN;
+  const int nk = K / 128;
   const uint32_t *wexp = g.w_packed + (size_t)e * N * KW;
   const uint16_t *sexp = g.scales + (size_t)e * g.G * N;
-
   const auto a_rs = make_rsrc(g.a, (uint32_t)((int64_t)g.a_rows * g.lda * 2));
   const auto w_rs = make_rsrc(wexp, (uint32_t)((int64_t)N * KW * 4));
   const auto s_rs = make_rsrc(sexp, (uint32_t)(g.G * N * 2));
 
-  // tile weight row j -> expert weight row
-  auto wrow = [&](int j) {
-    if (GATED) return j < BN / 2 ? n0 + j : g.I + n0 + (j - BN / 2);
-    return n0 + j;
-  };
-
-  // byte offset of this lane's A row for each of its x loads (gathered once)
-  const int lda2 = g.lda * 2;
-  int a_base[LPW];
+  // this lane's B column (expert weight row) in each of the wave's tiles;
+  // only the last tile of a non-gated GEMM can pass N (not stored)
+  uint32_t srow2[WTN], woff[WTN];
 #pragma unroll
-  for (int q = 0; q < LPW; ++q) {
-    const int li = wv * LPW + q;
-    const int row = li * 4 + (lane >> 4);
-    const int gr = r0 + row;
-    int off = -1;
-    if (li < XI && gr < r_end)
-      off = (GATED ? g.w.pair_order[gr] / g.topk : gr) * lda2 + ((lane & 15) ^ (row & 15)) * 16;
-    a_base[q] = off;
+  for (int j = 0; j < WTN; ++j) {
+    int n;
+    if (GATED)
+      n = (j < HALF ? n0 : g.I + n0) + wv * (WR / 2) + (j % HALF) * 16 + lr;
+    else
+      n = n0 + wv * WR + j * 16 + lr;
+    n = min(n, N - 1);
+    srow2[j] = 2u * (uint32_t)n;
+    woff[j] = (uint32_t)n * (uint32_t)(KW * 4) + 16u * (uint32_t)lg;
   }
-  auto dma = [&](int step) {
-    unsigned char *stage = smem + (step & 1) * STAGE;
+  // byte offset of this lane's A row in each of its DMA loads (load q of
+  // wave wv fills tile rows 16 q + 4 wv .. + 3, 16 bytes per lane); rows
+  // past the expert's last pair start at kOobOffset and so read 0
+  uint32_t a_off[NB];
 #pragma unroll
-    for (int q = 0; q < LPW; ++q) {
-      const int li = wv * LPW + q;
-      if (li < XI) {
-        const uint32_t off = a_base[q] >= 0 ? (uint32_t)(a_base[q] + step * kXRowB) : kOobOffset;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_ptr_t)(stage + li * 1024), 16, off, 0,
-                                                 0, 0);
-      } else {
-        const int wi = li - XI;
-        const int j = wi * 16 + (lane >> 2);
-        const int n = wrow(j);
-        const uint32_t off =
-            n < N ? (uint32_t)(n * KW * 4 + step * kWRowB + (lane & 3) * 16) : kOobOffset;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            w_rs, (lds_ptr_t)(stage + BM * kXRowB + wi * 1024), 16, off, 0, 0, 0);
-      }
-    }
+  for (int q = 0; q < NB; ++q) {
+    const int row = 16 * q + 4 * wv + lg;
+    const int gr = r0 + row;
+    a_off[q] = gr < r_end ? (uint32_t)((GATED ? g.w.pair_order[gr] / g.topk : gr) *
+                                           (2 * g.lda) +
+                                       ((lr ^ (row & 15)) * 16))
+                          : kOobOffset;
+  }
+
+  // the per-lane offsets are fixed; the step's offset is the uniform
+  // soffset, so issuing a step's loads costs no VALU
+  // Every step issues the same loads (the waits count on it): past the
+  // last step they re-read step nk - 1, which the L2 still holds, into a
+  // buffer or register set nothing reads again.
+  auto issue_x = [&](int step) {
+    unsigned char *st = smem + (step & 1) * kXStage;
+    const int ds = min(step, nk - 1);
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs,
+                                               (lds_ptr_t)(st + (16 * q + 4 * wv) * kXRowB), 16,
+                                               a_off[q], ds * kXRowB, 0, 0);
+  };
+  auto issue_w = [&](int step, u32x4_t (&w)[WTN], uint32_t (&s)[WTN]) {
+    step = min(step, nk - 1);
+    const int sb = ((step >> g.cpg_shift) & g.gmask) * N * 2;
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+      w[j] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[j], step * kWRowB, 0));
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+      s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, srow2[j], sb, 0);
   };
 
-  // this wave's weight rows: tile rows wv*(BN/4) + j*16 + lr
-  uint32_t srow[WTN];
+  f32x4_t acc[NB][WTN];
 #pragma unroll
-  for (int j = 0; j < WTN; ++j) srow[j] = (uint32_t)min(wrow(wv * (BN / 4) + j * 16 + lr), N - 1);
-
-  f32x4_t acc[WTM][WTN];
-#pragma unroll
-  for (int i = 0; i < WTM; ++i)
+  for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int j = 0; j < WTN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = K / 128;
-  dma(0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int ks = 0; ks < nk; ++ks) {
-    const unsigned char *stage = smem + (ks & 1) * STAGE;
-    uint32_t sraw[WTN];
+  auto dequant = [&](const u32x4_t (&w)[WTN], const uint32_t (&s)[WTN], int sub,
+                     bf16x8_t (&B)[WTN]) {
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
-      const uint32_t sidx = (uint32_t)((ks >> g.cpg_shift) & g.gmask) * (uint32_t)N + srow[j];
-      sraw[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, sidx * 2u, 0, 0);
+      const float sc = __uint_as_float(s[j] << 16);
+      B[j] = __builtin_bit_cast(
+          bf16x8_t, dq8_s4_bf16scale(w[j][sub], sc, sc * 0.0625f, -1032.f * sc, -72.f * sc));
     }
-    u32x4_t wraw[WTN];
+  };
+  // A fragments of one 32-wide K sub-step: row 16 i + lr, k 32 lg + 8 sub ..
+  auto read_x = [&](const unsigned char *st, int sub, u32x4_t (&xf)[NB]) {
 #pragma unroll
-    for (int j = 0; j < WTN; ++j)
-      wraw[j] = *reinterpret_cast<const u32x4_t *>(
-          stage + BM * kXRowB + (wv * (BN / 4) + j * 16 + lr) * kWRowB + 16 * lg);
-    u32x4_t xf[4][WTM];
+    for (int i = 0; i < NB; ++i)
+      xf[i] = *reinterpret_cast<const u32x4_t *>(st + (16 * i + lr) * kXRowB +
+                                                 (((4 * lg + sub) ^ lr) * 16));
+  };
+  auto mfmas = [&](const u32x4_t (&xf)[NB], const bf16x8_t (&B)[WTN]) {
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int i = 0; i < WTM; ++i) {
-        const int row = i * 16 + lr;
-        xf[sub][i] = *reinterpret_cast<const u32x4_t *>(
-            stage + row * kXRowB + (((4 * lg + sub) ^ (row & 15)) * 16));
-      }
-    if (ks + 1 < nk) dma(ks + 1);
+      for (int j = 0; j < WTN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xf[i]),
+                                                            B[j], acc[i][j], 0, 0, 0);
+  };
+  // Issue order of one sub-step: each MFMA is followed by V VALU
+  // instructions (the dequantisation of the next sub-step's B fragments
+  // runs in the MFMA shadow) and, while there are any, one LDS read of the
+  // next sub-step's A fragments.
+  auto interleave = [&](bool reads) {
+    constexpr int M = NB * WTN;
+    constexpr int V = (16 * WTN + M - 1) / M;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+      if (reads && m < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+
+  // D + 1 rotating register sets of weights and scales (D = kMoeDepth):
+  // step ks computes on set ks % (D + 1), dequantises sub-step 0 of step
+  // ks + 1 from the next set during its last sub-step, and loads step
+  // ks + D into the set step ks - 1 used.  D steps of loads in flight per
+  // wave keep enough bytes outstanding per CU to stream at HBM rate.
+  constexpr int D = kMoeDepth;
+  u32x4_t wq[D + 1][WTN];
+  uint32_t sq[D + 1][WTN];
+  bf16x8_t Bn[WTN];  // B fragments of the next sub-step to run
+  issue_x(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < D; ++p) issue_w(p, wq[p], sq[p]);
+  dequant(wq[0], sq[0], 0, Bn);
+  auto step = [&](int ks, const u32x4_t (&wc)[WTN], const uint32_t (&sc)[WTN],
+                  const u32x4_t (&wx)[WTN], const uint32_t (&sx)[WTN], u32x4_t (&wn)[WTN],
+                  uint32_t (&sn)[WTN]) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * WTN));
+    // A bare s_barrier: this wave's x(ks) DMA has landed (the wait above)
+    // and its reads of the other buffer were consumed by step ks - 1's
+    // MFMAs.  __syncthreads() would add a release fence, which waits for
+    // every outstanding load, the weight prefetch included.  The memory
+    // clobber keeps the compiler from moving LDS accesses across it.
+    asm volatile("s_barrier" ::: "memory");
+    // sub-step 0's A fragments first: their latency overlaps the load issue
+    const unsigned char *st = smem + (ks & 1) * kXStage;
+    u32x4_t xa[NB], xb[NB];
+    read_x(st, 0, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_x(ks + 1);
+    // the waits count on x(ks + 1) being issued before these loads
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(ks + D, wn, sn);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
-      bf16x8_t B[WTN];
+      bf16x8_t Bc[WTN];
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        const float sc = __uint_as_float(sraw[j] << 16);
-        B[j] = __builtin_bit_cast(
-            bf16x8_t, dq8_s4_bf16scale(wraw[j][sub], sc, sc * 0.0625f, -1032.f * sc, -72.f * sc));
+      for (int j = 0; j < WTN; ++j) Bc[j] = Bn[j];
+      if (sub < 3) {
+        read_x(st, sub + 1, sub & 1 ? xa : xb);
+        dequant(wc, sc, sub + 1, Bn);
+      } else {
+        dequant(wx, sx, 0, Bn);
       }
-#pragma unroll
-      for (int i = 0; i < WTM; ++i)
-#pragma unroll
-        for (int j = 0; j < WTN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, xf[sub][i]), B[j], acc[i][j], 0, 0, 0);
+      mfmas(sub & 1 ? xb : xa, Bc);
+      interleave(sub < 3);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  };
+  for (int k0 = 0; k0 < nk; k0 += D + 1) {
+#pragma unroll
+    for (int p = 0; p <= D; ++p)
+      if (k0 + p < nk)
+        step(k0 + p, wq[p], sq[p], wq[(p + 1) % (D + 1)], sq[(p + 1) % (D + 1)],
+             wq[(p + D) % (D + 1)], sq[(p + D) % (D + 1)]);
   }
-
-  constexpr int TP = BN + 4;
-  float *tile = reinterpret_cast<float *>(smem);
-#pragma unroll
-  for (int i = 0; i < WTM; ++i)
-#pragma unroll
-    for (int j = 0; j < WTN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        tile[(i * 16 + 4 * lg + r) * TP + wv * (BN / 4) + j * 16 + lr] = acc[i][j][r];
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+
+  // epilogue: the fp32 sums (+ bias) go through an LDS tile; one loop then
+  // applies act(g) * u, rounds to bf16 and stores 8 bytes per thread
+  constexpr int COLS = GATED ? BN / 2 : BN;  // output columns of the tile
+  constexpr int TPF = (GATED ? 2 * COLS : COLS) + 4;  // fp32 pitch
+  float *tile = reinterpret_cast<float *>(smem);
   const uint16_t *bexp = g.bias ? g.bias + (size_t)e * N : nullptr;
-  constexpr int COLS = GATED ? BN / 2 : BN;
-  for (int idx = tid; idx < BM * (COLS / 4); idx += 256) {
+  const int NO = GATED ? g.I : N;  // output columns of the GEMM
+#pragma unroll
+  for (int j = 0; j < HALF; ++j) {
+    const int c = GATED ? wv * (WR / 2) + j * 16 + lr : wv * WR + j * 16 + lr;
+    const int n = n0 + c;
+    float bg = 0.f, bu = 0.f;
+    if (bexp && n < NO) {
+      bg = bf16_bits_to_f32(bexp[n]);
+      if (GATED) bu = bf16_bits_to_f32(bexp[g.I + n]);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float *t = tile + (16 * i + 4 * lg + r) * TPF + c;
+        t[0] = acc[i][j][r] + bg;
+        if (GATED) t[COLS] = acc[i][j + HALF][r] + bu;
+      }
+  }
+  __syncthreads();
+  const int rows = min(16 * NB, r_end - r0);
+  for (int idx = tid; idx < rows * (COLS / 4); idx += 256) {
     const int row = idx / (COLS / 4), c4 = (idx % (COLS / 4)) * 4;
-    const int gr = r0 + row;
     const int n = n0 + c4;
-    if (gr >= r_end || n >= (GATED ? g.I : N)) continue;
+    if (n >= NO) continue;
+    const float *t = tile + row * TPF + c4;
     float f[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = tile[row * TP + c4 + r];
-      if (GATED) {
-        float u = tile[row * TP + BN / 2 + c4 + r];
-        if (bexp) {
-          v += bf16_bits_to_f32(bexp[n + r]);
-          u += bf16_bits_to_f32(bexp[g.I + n + r]);
-        }
-        v = unary_op(g.act, v) * u;
-      } else if (bexp) {
-        v += bf16_bits_to_f32(bexp[n + r]);
-      }
-      f[r] = v;
-    }
+    for (int r = 0; r < 4; ++r) f[r] = GATED ? unary_op(g.act, t[r]) * t[COLS + r] : t[r];
     u32x2_t pk;
     pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
     pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
-    *reinterpret_cast<u32x2_t *>(g.out + (size_t)gr * g.ldo + n) = pk;
+    *reinterpret_cast<u32x2_t *>(g.out + (size_t)(r0 + row) * g.ldo + n) = pk;
+  }
+}
+
+// Grid: mt_max * tiles_n workgroups (the route kernel's tile count is only
+// known on the device).  The first num_mt * tiles_n blocks take the live
+// tiles, XCD-contiguously (consecutive column tiles of one row tile share
+// an XCD's L2 copy of its A rows); the rest leave at once.
+template <bool GATED, int BN>
+__global__ __launch_bounds__(256) void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int live = g.w.num_mt[0] * tiles_n;
+  if ((int)blockIdx.x >= live) return;  // uniform: the whole workgroup leaves
+  const int t = xcd_contiguous_tile(blockIdx.x, live);
+  const int mt = t / tiles_n, tn = t - mt * tiles_n;
+  const int e = g.w.mt_expert[mt];
+  const int r0 = g.w.mt_row0[mt];
+  const int r_end = min(g.w.expert_off[e + 1], r0 + kMoeBM);
+  switch ((r_end - r0 + 15) >> 4) {
+    case 1: moe_tile<GATED, BN, 1>(g, e, r0, r_end, tn, smem); break;
+    case 2: moe_tile<GATED, BN, 2>(g, e, r0, r_end, tn, smem); break;
+    case 3: moe_tile<GATED, BN, 3>(g, e, r0, r_end, tn, smem); break;
+    case 4: moe_tile<GATED, BN, 4>(g, e, r0, r_end, tn, smem); break;
+    case 5: moe_tile<GATED, BN, 5>(g, e, r0, r_end, tn, smem); break;
+    case 6: moe_tile<GATED, BN, 6>(g, e, r0, r_end, tn, smem); break;
+    case 7: moe_tile<GATED, BN, 7>(g, e, r0, r_end, tn, smem); break;
+    default: moe_tile<GATED, BN, 8>(g, e, r0, r_end, tn, smem); break;
   }
 }
 
@@ -293,13 +387,28 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *y, int
   }
 }
 
+// N is a multiple of the tile's column count (host-checked: I, H % 128 == 0)
 template <bool GATED, int BN>
-hipError_t launch_moe_gemm(const MoeGemm &g, int tiles_n, hipStream_t s) {
-  const size_t stages = 2 * ((size_t)kMoeBM * kXRowB + (size_t)BN * kWRowB);
-  const size_t tile = (size_t)kMoeBM * (BN + 4) * 4;
-  woq_moe_gemm_kernel<GATED, BN><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(256),
-                                   stages > tile ? stages : tile, s>>>(g, tiles_n);
+hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s) {
+  const int cols = GATED ? BN / 2 : BN;
+  const int tiles_n = (GATED ? g.I : g.N + cols - 1) / cols;
+  const size_t tile = (size_t)kMoeBM * (BN + 4) * 4;  // fp32 epilogue tile
+  const size_t lds = tile > 2 * (size_t)kXStage ? tile : 2 * (size_t)kXStage;
+  woq_moe_gemm_kernel<GATED, BN><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(256), lds, s>>>(
+      g, tiles_n);
   return hipGetLastError();
+}
+
+// weight rows per workgroup of the gate_up and down GEMMs; ZT_MOE_BN="g,d"
+// (each 128 or 256) overrides them for tuning
+void moe_tile_widths(int &bn1, int &bn2) {
+  bn1 = 128, bn2 = 128;
+  if (const char *v = std::getenv("ZT_MOE_BN")) {
+    int a = 0, b = 0;
+    if (std::sscanf(v, "%d,%d", &a, &b) == 2 && (a == 128 || a == 256) &&
+        (b == 128 || b == 256))
+      bn1 = a, bn2 = b;
+  }
 }
 
 }  // namespace
@@ -327,8 +436,9 @@ hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
   g1.cpg_shift = shift_of(a.H, a.G13), g1.gmask = a.G13 == 1 ? 0 : 0x7fffffff;
   g1.bias = a.b13, g1.act = a.act;
   g1.out = w.h1, g1.ldo = (int)a.I, g1.mt_max = mt_max;
-  // gate_up: 128 gate + 128 up rows per tile; I % 128 == 0 (host-checked)
-  err = launch_moe_gemm<true, 256>(g1, (int)(a.I / 128), s);
+  int bn1, bn2;
+  moe_tile_widths(bn1, bn2);
+  err = bn1 == 256 ? launch_moe_gemm<true, 256>(g1, s) : launch_moe_gemm<true, 128>(g1, s);
   if (err != hipSuccess) return err;
 
   MoeGemm g2 = g1;
@@ -338,7 +448,7 @@ hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
   g2.cpg_shift = shift_of(a.I, a.G2), g2.gmask = a.G2 == 1 ? 0 : 0x7fffffff;
   g2.bias = a.b2;
   g2.out = w.y, g2.ldo = (int)a.H;
-  err = launch_moe_gemm<false, 128>(g2, (int)((a.H + 127) / 128), s);
+  err = bn2 == 256 ? launch_moe_gemm<false, 256>(g2, s) : launch_moe_gemm<false, 128>(g2, s);
   if (err != hipSuccess) return err;
 
   moe_combine_kernel<<<dim3((unsigned)a.T), dim3(256), 0, s>>>(
