@@ -72,7 +72,7 @@ namespace {
 
 // Byte layout of the MoE workspace (every region 256-byte aligned).
 struct MoeLayout {
-  size_t pair_order, pair_pos, expert_off, mt_expert, mt_row0, num_mt, h1, y, total;
+  size_t pair_token, pair_pos, expert_off, mt_info, num_mt, h1, y, total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t H, int64_t topk, int64_t E, int64_t I) {
@@ -85,11 +85,10 @@ MoeLayout moe_layout(int64_t T, int64_t H, int64_t topk, int64_t E, int64_t I) {
     off += (bytes + 255) / 256 * 256;
     return at;
   };
-  l.pair_order = take(P * 4);
+  l.pair_token = take(P * 4);
   l.pair_pos = take(P * 4);
   l.expert_off = take((E + 1) * 4);
-  l.mt_expert = take(tiles * 4);
-  l.mt_row0 = take(tiles * 4);
+  l.mt_info = take(tiles * 16);
   l.num_mt = take(4);
   l.h1 = take((size_t)P * I * 2);
   l.y = take((size_t)P * H * 2);
@@ -147,11 +146,10 @@ int zt_woq_moe(const void *x, int64_t T, int64_t H, const int32_t *topk_ids,
                 workspace ? workspace_bytes : (size_t)0);
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   zt::MoeWork w{};
-  w.pair_order = reinterpret_cast<int32_t *>(ws + l.pair_order);
+  w.pair_token = reinterpret_cast<int32_t *>(ws + l.pair_token);
   w.pair_pos = reinterpret_cast<int32_t *>(ws + l.pair_pos);
   w.expert_off = reinterpret_cast<int32_t *>(ws + l.expert_off);
-  w.mt_expert = reinterpret_cast<int32_t *>(ws + l.mt_expert);
-  w.mt_row0 = reinterpret_cast<int32_t *>(ws + l.mt_row0);
+  w.mt_info = reinterpret_cast<int32_t *>(ws + l.mt_info);
   w.num_mt = reinterpret_cast<int32_t *>(ws + l.num_mt);
   w.h1 = reinterpret_cast<uint16_t *>(ws + l.h1);
   w.y = reinterpret_cast<uint16_t *>(ws + l.y);

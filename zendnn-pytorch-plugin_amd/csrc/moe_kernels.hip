@@ -8,14 +8,15 @@
 // GPU without a host round trip (so the op can be captured in a HIP graph):
 //
 //  * moe_route_kernel   one workgroup: per-expert counts, a stable order of
-//    the pairs by expert (pair_order), each pair's row in that order
-//    (pair_pos, -1 for ids outside [0, E)), expert row offsets, and a table
-//    of (expert, first row) for every BM-row tile of the grouped GEMMs.
-//  * woq_moe_gemm_kernel<GATED>  the DMA int4 GEMM of the dense prefill path
-//    over that tile table.  A rows are gathered (w13: input row of the
+//    the pairs by expert (the token of each row in that order: pair_token),
+//    each pair's row in that order (pair_pos, -1 for ids outside [0, E)),
+//    expert row offsets, and a table of (expert, first row, end row) for
+//    every BM-row tile of the grouped GEMMs.
+//  * woq_moe_gemm_kernel<GATED, BN>  an int4 GEMM over that tile table on
+//    32x32x16 bf16 MFMAs.  A rows are gathered (w13: the input row of the
 //    pair's token; w2: the pair's row of the intermediate), the weight
-//    pointer is the tile's expert.  GATED tiles pair 64 gate rows n with
-//    their 64 up rows I + n, so the epilogue writes act(g) * u directly.
+//    pointer is the tile's expert.  GATED tiles pair gate rows n with their
+//    up rows I + n, so the epilogue writes act(g) * u directly.
 //  * moe_combine_kernel out[t] = sum over k (in k order) of
 //    w[t, k] * y[pair_pos[t, k]], fp32, rounded once.
 #include <cstdio>
@@ -30,14 +31,17 @@ namespace {
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-constexpr int kMoeBM = 128;   // grouped-GEMM rows (pairs) per tile
+constexpr int kMoeBM = 96;    // grouped-GEMM rows (pairs) per tile
 constexpr int kXRowB = 256;   // bytes of A per row per 128-wide K step
 constexpr int kWRowB = 64;    // bytes of int4 per weight row per step
 constexpr int kXStage = kMoeBM * kXRowB;  // one LDS buffer of A rows
-constexpr int kMoeDepth = 4;  // K steps of weights loaded ahead
+constexpr int kXStages = 3;               // x prefetched two steps ahead
+constexpr int kMoeDepth = 2;  // K steps of weights loaded ahead
+constexpr int kMoeComputeWaves = 4;
+constexpr int kMoeThreads = 64 * (kMoeComputeWaves + 1);  // + the x producer
 
 __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int P, int E,
-                                                          MoeWork w) {
+                                                          int topk, MoeWork w) {
   __shared__ int cnt[1024];
   __shared__ int base[1024];
   __shared__ int chunk_e[1024];
@@ -55,8 +59,10 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int
       w.expert_off[e] = off;
       base[e] = off;
       for (int m0 = 0; m0 < cnt[e]; m0 += kMoeBM) {
-        w.mt_expert[nt] = e;
-        w.mt_row0[nt] = off + m0;
+        w.mt_info[4 * nt] = e;
+        w.mt_info[4 * nt + 1] = off + m0;
+        w.mt_info[4 * nt + 2] = off + min(cnt[e], m0 + kMoeBM);
+        w.mt_info[4 * nt + 3] = 0;
         ++nt;
       }
       off += cnt[e];
@@ -82,7 +88,7 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int
     int pos = -1;
     if (e >= 0) {
       pos = base[e] + rank;
-      w.pair_order[pos] = i;
+      w.pair_token[pos] = i / topk;
     }
     if (i < P) w.pair_pos[i] = pos;
     __syncthreads();
@@ -95,230 +101,261 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int
 // loads (n < 64) and nothing else
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// One grouped-GEMM tile: NB 16-row blocks of the expert's pairs (rows
-// r0 .. r0 + 16 NB; the blocks of the 128-row tile past the expert's last
-// pair cost nothing) times BN weight rows.
-//  * The 4 waves split along N only: each wave owns BN/4 weight rows, so
-//    every weight fragment is dequantised once and feeds NB MFMAs.
-//  * Weights and scales go straight from HBM to registers two K steps
-//    ahead, in three rotating register sets: they never touch LDS and no
-//    barrier waits on them.
-//  * The gathered A rows go to LDS by DMA (16-byte chunks XOR-swizzled by
-//    the row's low 4 bits), double-buffered: x(ks + 1) is issued at the top
-//    of step ks, after the barrier that retires step ks - 1's reads of that
-//    buffer.
-//  * GATED tiles hold BN/2 gate rows n0.. and their BN/2 up rows I + n0..;
-//    each wave owns BN/8 of each, so act(g) * u is formed in registers.
-// The loop's vector-memory order per step is [x(ks + 1): NB loads]
-// [weights + scales of ks + 2: 2 WTN loads]; x(ks) (and everything issued
-// before it) has landed once at most 2 WTN loads are outstanding.
+// One grouped-GEMM tile: NB 32-row blocks of the expert's pairs (rows
+// r0 .. r0 + 32 NB; the blocks of the 96-row tile past the expert's last
+// pair cost nothing) times BN weight rows, on v_mfma_f32_32x32x16_bf16
+// (the 32x32 shape sustains twice the 16x16x32 shape's rate on gfx950).
+//  * kMoeComputeWaves waves split along N only: each owns BN/4 weight rows
+//    (WTN 32-column MFMA tiles), so every weight fragment is dequantised
+//    once and feeds NB MFMAs.  Their weights and scales go straight from
+//    HBM to registers kMoeDepth K steps ahead in rotating register sets.
+//  * One more wave only moves the gathered A rows to LDS by DMA (16-byte
+//    chunks XOR-swizzled by the row's low 4 bits) into kXStages buffers,
+//    two steps ahead (an L2-resident tile still takes about 2 us to land
+//    under this load).  A wave's loads retire in issue order, so a wave
+//    that waited for its own x DMA would also wait for every weight load
+//    issued before it; keeping the x DMA in a wave of its own leaves D
+//    steps of weights in flight.  The waves meet at one barrier per step:
+//    the producer arrives once x(ks + 1) has landed, the compute waves
+//    once step ks is done.
+//  * K order inside a 128-wide step: lane (c, kb) of a B fragment holds the
+//    row's bytes 32 kb .. 32 kb + 31, and sub-step s (0..7) multiplies its
+//    word s, i.e. k = 64 kb + 8 s + 0..7; the A fragment of lane (m, kb)
+//    holds x[m][64 kb + 8 s .. + 7] to match.
+//  * GATED: every 32-column tile holds 16 gate rows n and their 16 up rows
+//    I + n; the epilogue pairs them through the LDS tile.
 template <bool GATED, int BN, int NB>
 __device__ __forceinline__ void moe_tile(const MoeGemm &g, int e, int r0, int r_end, int tn,
                                          unsigned char *smem) {
-  constexpr int WTN = BN / 64;  // 16-column tiles per wave
-  constexpr int WR = BN / 4;    // weight rows per wave
-  constexpr int HALF = GATED ? WTN / 2 : WTN;
-  static_assert(!GATED || WTN % 2 == 0, "gated tiles pair gate and up column tiles");
+  constexpr int WTN = BN / 128;  // 32-column tiles per compute wave
+  static_assert(WTN >= 1, "a wave owns at least one 32-column tile");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lr = lane & 15, lg = lane >> 4;
+  const int lc = lane & 31, kb = lane >> 5;
   const int K = g.K, KW = K / 8, N = g.N;
   const int n0 = GATED ? tn * (BN / 2) : tn * BN;
   const int nk = K / 128;
-  const uint32_t *wexp = g.w_packed + (size_t)e * N * KW;
-  const uint16_t *sexp = g.scales + (size_t)e * g.G * N;
-  const auto a_rs = make_rsrc(g.a, (uint32_t)((int64_t)g.a_rows * g.lda * 2));
-  const auto w_rs = make_rsrc(wexp, (uint32_t)((int64_t)N * KW * 4));
-  const auto s_rs = make_rsrc(sexp, (uint32_t)(g.G * N * 2));
+  // s_waitcnt lgkmcnt(0) alone
+  constexpr int kLgkm0 = 15 | (3 << 14) | (7 << 4);
 
-  // this lane's B column (expert weight row) in each of the wave's tiles;
-  // only the last tile of a non-gated GEMM can pass N (not stored)
-  uint32_t srow2[WTN], woff[WTN];
+  f32x16_t acc[NB][WTN];
+  if (wv == kMoeComputeWaves) {
+    // ---- producer: x(0) .. x(nk - 1), one step ahead of the compute waves
+    const auto a_rs = make_rsrc(g.a, (uint32_t)((int64_t)g.a_rows * g.lda * 2));
+    // load q fills tile rows 4 q .. 4 q + 3, 16 bytes per lane; rows past
+    // the expert's last pair start at kOobOffset and so read 0
+    // (the token loads are unconditional, clamped to a live row, and the
+    // out-of-range bit is ORed in, so the loads issue back to back rather
+    // than one round trip each behind a branch)
+    uint32_t a_off[8 * NB];
 #pragma unroll
-  for (int j = 0; j < WTN; ++j) {
-    int n;
-    if (GATED)
-      n = (j < HALF ? n0 : g.I + n0) + wv * (WR / 2) + (j % HALF) * 16 + lr;
-    else
-      n = n0 + wv * WR + j * 16 + lr;
-    n = min(n, N - 1);
-    srow2[j] = 2u * (uint32_t)n;
-    woff[j] = (uint32_t)n * (uint32_t)(KW * 4) + 16u * (uint32_t)lg;
-  }
-  // byte offset of this lane's A row in each of its DMA loads (load q of
-  // wave wv fills tile rows 16 q + 4 wv .. + 3, 16 bytes per lane); rows
-  // past the expert's last pair start at kOobOffset and so read 0
-  uint32_t a_off[NB];
+    for (int q = 0; q < 8 * NB; ++q) {
+      const int row = 4 * q + (lane >> 4);
+      const int gr = r0 + row;
+      const int src = GATED ? g.w.pair_token[min(gr, r_end - 1)] : gr;
+      a_off[q] = (uint32_t)(src * (2 * g.lda) + (((lane & 15) ^ (row & 15)) * 16)) |
+                 (gr < r_end ? 0u : kOobOffset);
+    }
+    auto issue_x = [&](int step) {
+      unsigned char *st = smem + (step % kXStages) * kXStage;
 #pragma unroll
-  for (int q = 0; q < NB; ++q) {
-    const int row = 16 * q + 4 * wv + lg;
-    const int gr = r0 + row;
-    a_off[q] = gr < r_end ? (uint32_t)((GATED ? g.w.pair_order[gr] / g.topk : gr) *
-                                           (2 * g.lda) +
-                                       ((lr ^ (row & 15)) * 16))
-                          : kOobOffset;
-  }
-
-  // the per-lane offsets are fixed; the step's offset is the uniform
-  // soffset, so issuing a step's loads costs no VALU
-  // Every step issues the same loads (the waits count on it): past the
-  // last step they re-read step nk - 1, which the L2 still holds, into a
-  // buffer or register set nothing reads again.
-  auto issue_x = [&](int step) {
-    unsigned char *st = smem + (step & 1) * kXStage;
-    const int ds = min(step, nk - 1);
-#pragma unroll
-    for (int q = 0; q < NB; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs,
-                                               (lds_ptr_t)(st + (16 * q + 4 * wv) * kXRowB), 16,
-                                               a_off[q], ds * kXRowB, 0, 0);
-  };
-  auto issue_w = [&](int step, u32x4_t (&w)[WTN], uint32_t (&s)[WTN]) {
-    step = min(step, nk - 1);
-    const int sb = ((step >> g.cpg_shift) & g.gmask) * N * 2;
-#pragma unroll
-    for (int j = 0; j < WTN; ++j)
-      w[j] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[j], step * kWRowB, 0));
-#pragma unroll
-    for (int j = 0; j < WTN; ++j)
-      s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, srow2[j], sb, 0);
-  };
-
-  f32x4_t acc[NB][WTN];
-#pragma unroll
-  for (int i = 0; i < NB; ++i)
-#pragma unroll
-    for (int j = 0; j < WTN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto dequant = [&](const u32x4_t (&w)[WTN], const uint32_t (&s)[WTN], int sub,
-                     bf16x8_t (&B)[WTN]) {
+      for (int q = 0; q < 8 * NB; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_ptr_t)(st + 4 * q * kXRowB), 16,
+                                                 a_off[q], step * kXRowB, 0, 0);
+    };
+    static_assert(kXStages == 3, "the waits below are written for x two steps ahead");
+    issue_x(0);
+    if (nk > 1) {
+      issue_x(1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 * NB));  // x(0) has landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    asm volatile("s_barrier" ::: "memory");
+    for (int ks = 0; ks < nk; ++ks) {
+      // buffer (ks + 2) % 3 was last read in step ks - 1, which every
+      // compute wave finished before the barrier just passed; x(ks + 1)
+      // (issued before x(ks + 2)) must land before the next barrier
+      if (ks + 2 < nk) {
+        issue_x(ks + 2);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 * NB));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      asm volatile("s_barrier" ::: "memory");
+    }
+  } else {
+    // ---- compute waves
+    const uint32_t *wexp = g.w_packed + (size_t)e * N * KW;
+    const uint16_t *sexp = g.scales + (size_t)e * g.G * N;
+    const auto w_rs = make_rsrc(wexp, (uint32_t)((int64_t)N * KW * 4));
+    const auto s_rs = make_rsrc(sexp, (uint32_t)(g.G * N * 2));
+    // this lane's B column (expert weight row) in each of the wave's tiles;
+    // only the last tile of a non-gated GEMM can pass N (not stored)
+    uint32_t srow2[WTN], woff[WTN];
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
-      const float sc = __uint_as_float(s[j] << 16);
-      B[j] = __builtin_bit_cast(
-          bf16x8_t, dq8_s4_bf16scale(w[j][sub], sc, sc * 0.0625f, -1032.f * sc, -72.f * sc));
+      const int t = wv * WTN + j;  // 32-column tile of the workgroup
+      int n = GATED ? (lc < 16 ? n0 : g.I + n0) + t * 16 + (lc & 15) : n0 + t * 32 + lc;
+      n = min(n, N - 1);
+      srow2[j] = 2u * (uint32_t)n;
+      woff[j] = (uint32_t)n * (uint32_t)(KW * 4) + 32u * (uint32_t)kb;
     }
-  };
-  // A fragments of one 32-wide K sub-step: row 16 i + lr, k 32 lg + 8 sub ..
-  auto read_x = [&](const unsigned char *st, int sub, u32x4_t (&xf)[NB]) {
+    // the per-lane offsets are fixed; the step's offset is the uniform
+    // soffset.  Steps past the last one re-read step nk - 1 (an L2 hit)
+    // into a register set nothing reads again.
+    auto issue_w = [&](int step, u32x4_t (&w)[WTN][2], uint32_t (&s)[WTN]) {
+      step = min(step, nk - 1);
+      const int sb = ((step >> g.cpg_shift) & g.gmask) * N * 2;
 #pragma unroll
-    for (int i = 0; i < NB; ++i)
-      xf[i] = *reinterpret_cast<const u32x4_t *>(st + (16 * i + lr) * kXRowB +
-                                                 (((4 * lg + sub) ^ lr) * 16));
-  };
-  auto mfmas = [&](const u32x4_t (&xf)[NB], const bf16x8_t (&B)[WTN]) {
+      for (int j = 0; j < WTN; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          w[j][h] = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[j] + 16u * h,
+                                                             step * kWRowB, 0));
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, srow2[j], sb, 0);
+    };
+
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
       for (int j = 0; j < WTN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xf[i]),
-                                                            B[j], acc[i][j], 0, 0, 0);
-  };
-  // Issue order of one sub-step: each MFMA is followed by V VALU
-  // instructions (the dequantisation of the next sub-step's B fragments
-  // runs in the MFMA shadow) and, while there are any, one LDS read of the
-  // next sub-step's A fragments.
-  auto interleave = [&](bool reads) {
-    constexpr int M = NB * WTN;
-    constexpr int V = (16 * WTN + M - 1) / M;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
-      if (reads && m < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-  };
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // D + 1 rotating register sets of weights and scales (D = kMoeDepth):
-  // step ks computes on set ks % (D + 1), dequantises sub-step 0 of step
-  // ks + 1 from the next set during its last sub-step, and loads step
-  // ks + D into the set step ks - 1 used.  D steps of loads in flight per
-  // wave keep enough bytes outstanding per CU to stream at HBM rate.
-  constexpr int D = kMoeDepth;
-  u32x4_t wq[D + 1][WTN];
-  uint32_t sq[D + 1][WTN];
-  bf16x8_t Bn[WTN];  // B fragments of the next sub-step to run
-  issue_x(0);
-  __builtin_amdgcn_sched_barrier(0);
+    auto dequant = [&](const u32x4_t (&w)[WTN][2], const uint32_t (&s)[WTN], int sub,
+                       bf16x8_t (&B)[WTN]) {
 #pragma unroll
-  for (int p = 0; p < D; ++p) issue_w(p, wq[p], sq[p]);
-  dequant(wq[0], sq[0], 0, Bn);
-  auto step = [&](int ks, const u32x4_t (&wc)[WTN], const uint32_t (&sc)[WTN],
-                  const u32x4_t (&wx)[WTN], const uint32_t (&sx)[WTN], u32x4_t (&wn)[WTN],
-                  uint32_t (&sn)[WTN]) {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * WTN));
-    // A bare s_barrier: this wave's x(ks) DMA has landed (the wait above)
-    // and its reads of the other buffer were consumed by step ks - 1's
-    // MFMAs.  __syncthreads() would add a release fence, which waits for
-    // every outstanding load, the weight prefetch included.  The memory
-    // clobber keeps the compiler from moving LDS accesses across it.
-    asm volatile("s_barrier" ::: "memory");
-    // sub-step 0's A fragments first: their latency overlaps the load issue
-    const unsigned char *st = smem + (ks & 1) * kXStage;
-    u32x4_t xa[NB], xb[NB];
-    read_x(st, 0, xa);
-    __builtin_amdgcn_sched_barrier(0);
-    issue_x(ks + 1);
-    // the waits count on x(ks + 1) being issued before these loads
-    __builtin_amdgcn_sched_barrier(0);
-    issue_w(ks + D, wn, sn);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-      bf16x8_t Bc[WTN];
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) Bc[j] = Bn[j];
-      if (sub < 3) {
-        read_x(st, sub + 1, sub & 1 ? xa : xb);
-        dequant(wc, sc, sub + 1, Bn);
-      } else {
-        dequant(wx, sx, 0, Bn);
+      for (int j = 0; j < WTN; ++j) {
+        const float sc = __uint_as_float(s[j] << 16);
+        B[j] = __builtin_bit_cast(bf16x8_t, dq8_s4_bf16scale(w[j][sub >> 2][sub & 3], sc,
+                                                              sc * 0.0625f, -1032.f * sc,
+                                                              -72.f * sc));
       }
-      mfmas(sub & 1 ? xb : xa, Bc);
-      interleave(sub < 3);
-    }
-  };
-  for (int k0 = 0; k0 < nk; k0 += D + 1) {
+    };
+    // A fragments of one 16-wide K sub-step: row 32 i + lc, k 64 kb + 8 sub ..
+    auto read_x = [&](const unsigned char *st, int sub, u32x4_t (&xf)[NB]) {
 #pragma unroll
-    for (int p = 0; p <= D; ++p)
+      for (int i = 0; i < NB; ++i)
+        xf[i] = *reinterpret_cast<const u32x4_t *>(st + (32 * i + lc) * kXRowB +
+                                                   (((8 * kb + sub) ^ (lc & 15)) * 16));
+    };
+    auto mfmas = [&](const u32x4_t (&xf)[NB], const bf16x8_t (&B)[WTN]) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, xf[i]), B[j], acc[i][j], 0, 0, 0);
+    };
+    // Issue order of one sub-step: each MFMA is followed by V VALU
+    // instructions (the dequantisation of the next sub-step's B fragments
+    // runs in the MFMA shadow) and, while there are any, one LDS read of
+    // the next sub-step's A fragments.
+    auto interleave = [&](bool reads) {
+      constexpr int M = NB * WTN;
+      constexpr int V = (16 * WTN + M - 1) / M;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+        if (reads && m < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    };
+
+    // D + 1 rotating register sets of weights and scales (D = kMoeDepth):
+    // step ks computes on set ks % (D + 1), dequantises sub-step 0 of step
+    // ks + 1 from the next set during its last sub-step, and loads step
+    // ks + D into the set step ks - 1 used.
+    constexpr int D = kMoeDepth;
+    u32x4_t wq[D + 1][WTN][2];
+    uint32_t sq[D + 1][WTN];
+    bf16x8_t Bn[WTN];  // B fragments of the next sub-step to run
+#pragma unroll
+    for (int p = 0; p < D; ++p) issue_w(p, wq[p], sq[p]);
+    asm volatile("s_barrier" ::: "memory");  // x(0) has landed
+    dequant(wq[0], sq[0], 0, Bn);
+    auto step = [&](int ks, const u32x4_t (&wc)[WTN][2], const uint32_t (&sc)[WTN],
+                    const u32x4_t (&wx)[WTN][2], const uint32_t (&sx)[WTN],
+                    u32x4_t (&wn)[WTN][2], uint32_t (&sn)[WTN]) {
+      const unsigned char *st = smem + (ks % kXStages) * kXStage;
+      u32x4_t xa[NB], xb[NB];
+      read_x(st, 0, xa);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_w(ks + D, wn, sn);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int sub = 0; sub < 8; ++sub) {
+        bf16x8_t Bc[WTN];
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) Bc[j] = Bn[j];
+        if (sub < 7) {
+          read_x(st, sub + 1, sub & 1 ? xa : xb);
+          dequant(wc, sc, sub + 1, Bn);
+        } else {
+          dequant(wx, sx, 0, Bn);
+        }
+        mfmas(sub & 1 ? xb : xa, Bc);
+        interleave(sub < 7);
+      }
+      // every read of buffer ks % 3 has returned before the producer may
+      // refill it (after the next barrier).  A bare s_barrier: no fence, so
+      // the weight prefetch stays in flight; the memory clobber keeps the
+      // compiler from moving LDS accesses across it.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kLgkm0);
+      asm volatile("s_barrier" ::: "memory");
+    };
+    // whole rounds of D + 1 steps, then the rest outside the loop: a
+    // guarded step inside the loop would make the compiler's wait counts at
+    // the loop head conservative (a full drain of the prefetch)
+    int k0 = 0;
+    for (; k0 + D + 1 <= nk; k0 += D + 1) {
+#pragma unroll
+      for (int p = 0; p <= D; ++p)
+        step(k0 + p, wq[p], sq[p], wq[(p + 1) % (D + 1)], sq[(p + 1) % (D + 1)],
+             wq[(p + D) % (D + 1)], sq[(p + D) % (D + 1)]);
+    }
+#pragma unroll
+    for (int p = 0; p < D; ++p)
       if (k0 + p < nk)
         step(k0 + p, wq[p], sq[p], wq[(p + 1) % (D + 1)], sq[(p + 1) % (D + 1)],
              wq[(p + D) % (D + 1)], sq[(p + D) % (D + 1)]);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
 
-  // epilogue: the fp32 sums (+ bias) go through an LDS tile; one loop then
-  // applies act(g) * u, rounds to bf16 and stores 8 bytes per thread
-  constexpr int COLS = GATED ? BN / 2 : BN;  // output columns of the tile
+  // epilogue: the fp32 sums (+ bias) go through an LDS tile (the x buffers
+  // are free: the producer's last DMA landed before the last barrier); one
+  // loop then applies act(g) * u, rounds to bf16 and stores 8 bytes per
+  // thread.  Accumulator register r of lane (lc, kb) is row
+  // 8 (r / 4) + 4 kb + r % 4 of its 32-row block, column lc.
+  constexpr int COLS = GATED ? BN / 2 : BN;           // output columns of the tile
   constexpr int TPF = (GATED ? 2 * COLS : COLS) + 4;  // fp32 pitch
   float *tile = reinterpret_cast<float *>(smem);
-  const uint16_t *bexp = g.bias ? g.bias + (size_t)e * N : nullptr;
   const int NO = GATED ? g.I : N;  // output columns of the GEMM
+  if (wv < kMoeComputeWaves) {
+    const uint16_t *bexp = g.bias ? g.bias + (size_t)e * N : nullptr;
 #pragma unroll
-  for (int j = 0; j < HALF; ++j) {
-    const int c = GATED ? wv * (WR / 2) + j * 16 + lr : wv * WR + j * 16 + lr;
-    const int n = n0 + c;
-    float bg = 0.f, bu = 0.f;
-    if (bexp && n < NO) {
-      bg = bf16_bits_to_f32(bexp[n]);
-      if (GATED) bu = bf16_bits_to_f32(bexp[g.I + n]);
+    for (int j = 0; j < WTN; ++j) {
+      const int t = wv * WTN + j;
+      // gated: column lc < 16 is gate output t * 16 + lc, lc >= 16 its up row
+      const int oc = GATED ? t * 16 + (lc & 15) : t * 32 + lc;
+      const int c = GATED && lc >= 16 ? COLS + oc : oc;
+      const int n = n0 + oc;
+      float b = 0.f;
+      if (bexp && n < NO) b = bf16_bits_to_f32(bexp[GATED && lc >= 16 ? g.I + n : n]);
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          tile[(32 * i + 8 * (r >> 2) + 4 * kb + (r & 3)) * TPF + c] = acc[i][j][r] + b;
     }
-#pragma unroll
-    for (int i = 0; i < NB; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float *t = tile + (16 * i + 4 * lg + r) * TPF + c;
-        t[0] = acc[i][j][r] + bg;
-        if (GATED) t[COLS] = acc[i][j + HALF][r] + bu;
-      }
   }
   __syncthreads();
-  const int rows = min(16 * NB, r_end - r0);
-  for (int idx = tid; idx < rows * (COLS / 4); idx += 256) {
+  const int rows = min(32 * NB, r_end - r0);
+  for (int idx = tid; idx < rows * (COLS / 4); idx += kMoeThreads) {
     const int row = idx / (COLS / 4), c4 = (idx % (COLS / 4)) * 4;
     const int n = n0 + c4;
     if (n >= NO) continue;
@@ -338,24 +375,19 @@ __device__ __forceinline__ void moe_tile(const MoeGemm &g, int e, int r0, int r_
 // tiles, XCD-contiguously (consecutive column tiles of one row tile share
 // an XCD's L2 copy of its A rows); the rest leave at once.
 template <bool GATED, int BN>
-__global__ __launch_bounds__(256) void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
+__global__ __launch_bounds__(kMoeThreads) void woq_moe_gemm_kernel(MoeGemm g, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int live = g.w.num_mt[0] * tiles_n;
   if ((int)blockIdx.x >= live) return;  // uniform: the whole workgroup leaves
   const int t = xcd_contiguous_tile(blockIdx.x, live);
   const int mt = t / tiles_n, tn = t - mt * tiles_n;
-  const int e = g.w.mt_expert[mt];
-  const int r0 = g.w.mt_row0[mt];
-  const int r_end = min(g.w.expert_off[e + 1], r0 + kMoeBM);
-  switch ((r_end - r0 + 15) >> 4) {
+  const i32x4_t info = reinterpret_cast<const i32x4_t *>(g.w.mt_info)[mt];
+  const int e = info[0], r0 = info[1], r_end = info[2];
+  static_assert(kMoeBM == 96, "tiles are 1 to 3 blocks of 32 rows");
+  switch ((r_end - r0 + 31) >> 5) {
     case 1: moe_tile<GATED, BN, 1>(g, e, r0, r_end, tn, smem); break;
     case 2: moe_tile<GATED, BN, 2>(g, e, r0, r_end, tn, smem); break;
-    case 3: moe_tile<GATED, BN, 3>(g, e, r0, r_end, tn, smem); break;
-    case 4: moe_tile<GATED, BN, 4>(g, e, r0, r_end, tn, smem); break;
-    case 5: moe_tile<GATED, BN, 5>(g, e, r0, r_end, tn, smem); break;
-    case 6: moe_tile<GATED, BN, 6>(g, e, r0, r_end, tn, smem); break;
-    case 7: moe_tile<GATED, BN, 7>(g, e, r0, r_end, tn, smem); break;
-    default: moe_tile<GATED, BN, 8>(g, e, r0, r_end, tn, smem); break;
+    default: moe_tile<GATED, BN, 3>(g, e, r0, r_end, tn, smem); break;
   }
 }
 
@@ -393,8 +425,8 @@ hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s) {
   const int cols = GATED ? BN / 2 : BN;
   const int tiles_n = (GATED ? g.I : g.N + cols - 1) / cols;
   const size_t tile = (size_t)kMoeBM * (BN + 4) * 4;  // fp32 epilogue tile
-  const size_t lds = tile > 2 * (size_t)kXStage ? tile : 2 * (size_t)kXStage;
-  woq_moe_gemm_kernel<GATED, BN><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(256), lds, s>>>(
+  const size_t lds = tile > (size_t)kXStages * kXStage ? tile : (size_t)kXStages * kXStage;
+  woq_moe_gemm_kernel<GATED, BN><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(kMoeThreads), lds, s>>>(
       g, tiles_n);
   return hipGetLastError();
 }
@@ -418,7 +450,7 @@ int moe_max_tiles(int64_t P, int64_t E) { return (int)((P + kMoeBM - 1) / kMoeBM
 hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
   const int P = (int)(a.T * a.topk);
   const int mt_max = moe_max_tiles(P, a.E);
-  moe_route_kernel<<<1, 1024, 0, s>>>(a.ids, P, (int)a.E, w);
+  moe_route_kernel<<<1, 1024, 0, s>>>(a.ids, P, (int)a.E, (int)a.topk, w);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
 

@@ -80,11 +80,11 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);
 
 // Grouped int4 MoE (moe_kernels.hip).  Device scratch of one call.
 struct MoeWork {
-  int32_t *pair_order;  // [P] pair index (t*topk + k) in expert order
+  int32_t *pair_token;  // [P] token of the pair at each row of the expert order
   int32_t *pair_pos;    // [P] row of each pair in that order, -1 if dropped
   int32_t *expert_off;  // [E + 1]
-  int32_t *mt_expert;   // [tiles] expert of each grouped-GEMM row tile
-  int32_t *mt_row0;     // [tiles] its first row
+  int32_t *mt_info;     // [tiles][4] per grouped-GEMM row tile: expert, first
+                        // row, end row (its expert's end or first + BM), 0
   int32_t *num_mt;      // [1] tiles in use
   uint16_t *h1;         // [P, I] bf16 activated intermediate
   uint16_t *y;          // [P, H] bf16 expert outputs
@@ -111,7 +111,7 @@ struct MoeArgs {
 
 struct MoeGemm {
   MoeWork w;
-  const uint16_t *a;  // A rows (gathered through pair_order when gated)
+  const uint16_t *a;  // A rows (gathered through pair_token when gated)
   int lda, a_rows, topk, K, N, I;
   const uint32_t *w_packed;
   const uint16_t *scales;
