@@ -359,13 +359,15 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // Weight-streaming decode kernel (M <= 16 and the activations fit in LDS).
 //
 // One workgroup per TPW 16-row tiles over all of K; its NW waves split K
-// into slices of CPW 128-wide chunks.  A wave first issues every weight and
-// scale load of its slice (TPW x CPW 16-byte fragments per lane, all in
-// flight at once: few waves with many loads each keep HBM busier than many
-// waves with few), then the workgroup copies x [M, K] into LDS with
-// full-width loads, and the wave walks its chunks: B operands come from LDS
-// (lanes past M read zeros), A operands are the fragments dequantised in
-// registers.  K partials meet in LDS and are added in wave order.
+// into slices of CPW 128-wide chunks.  The workgroup first starts the copy
+// of x [M, K] into LDS by DMA (when the rows are 16-byte aligned), then a
+// wave issues every weight and scale load of its slice (TPW x CPW 16-byte
+// fragments per lane, all in flight at once: few waves with many loads each
+// keep HBM busier than many waves with few).  A wave's loads retire in
+// issue order, so x (from L2) lands while its weights are still in flight.
+// The wave then walks its chunks: B operands come from LDS (lanes past M
+// read zeros), A operands are the fragments dequantised in registers.  K
+// partials meet in LDS and are added in wave order.
 template <int NW>
 __host__ __device__ constexpr size_t stream_slab_bytes(int tpw) {
   return (size_t)NW * tpw * 16 * 17 * sizeof(float);
@@ -387,7 +389,25 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   const auto w_rsrc = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
   const auto s_rsrc = make_rsrc(a.scales, (uint32_t)(a.G * N * s_bytes));
 
-  // 1. the slice's weights and scales, all in flight.  Rows past N are
+  // 1. x [M, K] -> LDS (row pitch K + 8 bf16).  By DMA when every row
+  //    starts 16-byte aligned: instruction i moves 64 16-byte chunks of one
+  //    row (K % 128 == 0, so a row is whole 1 KB pieces).
+  const int XP = stream_x_pitch(K);
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes<NW>(TPW));
+  const bool x_dma = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) == 0 &&
+                     (int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2 < (int64_t)kOobOffset;
+  if (x_dma) {
+    const auto x_rsrc = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
+    const int per_row = K / 512;  // 1 KB pieces per row
+    for (int i = wv; i < M * per_row; i += NW) {
+      const int m = i / per_row, p = i - m * per_row;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          x_rsrc, (lds_ptr_t)(xl + m * XP + p * 512), 16,
+          (uint32_t)(m * a.ldx * 2 + p * 1024 + lane * 16), 0, 0, 0);
+    }
+  }
+
+  // 2. the slice's weights and scales, all in flight.  Rows past N are
   //    clamped (their results are never stored); chunks past C read zeros.
   u32x4_t wr[TPW][CPW];
   uint32_t sr[TPW][CPW];
@@ -412,10 +432,10 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
 
-  // 2. x [M, K] -> LDS (row pitch K + 8 bf16)
-  const int XP = stream_x_pitch(K);
-  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes<NW>(TPW));
-  {
+  // 3. copy x by loads when the DMA does not apply, and wait for it either
+  //    way (the barrier's fence waits for this wave's x DMA and the weight
+  //    loads issued after it; they are needed next anyway)
+  if (!x_dma) {
     const uint16_t *xp = reinterpret_cast<const uint16_t *>(a.x);
     const int per_row = K / 8;
     for (int idx = tid; idx < M * per_row; idx += 64 * NW) {
@@ -426,7 +446,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   }
   __syncthreads();
 
-  // 3. the slice's MFMAs
+  // 4. the slice's MFMAs
   f32x4_t acc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -452,7 +472,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
 
-  // 4. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t], then
+  // 5. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t], then
   //    each output adds the NW partials in wave order
   float *slab = reinterpret_cast<float *>(smem);
 #pragma unroll
