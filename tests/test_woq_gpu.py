@@ -136,6 +136,29 @@ def test_llama_decode_shapes_m16(N, K):
     run_case(16, K, N, K // 128, seed=N + K)
 
 
+# M = 33..64 runs as blocks of 16 rows on the decode kernels, with x, y and
+# the binary post-op buffers offset to each block's first row
+@pytest.mark.parametrize("M", [33, 40, 64])
+@pytest.mark.parametrize("post,nbuf", [((), 0), (("mul", "add"), 2), (("silu", "mul"), 1)])
+def test_row_blocks_vs_oracle(M, post, nbuf):
+    run_case(M, 1024, 112, 8, post=post, nbuf=nbuf, seed=M + 5 * nbuf, bias=True)
+
+
+def test_row_blocks_strided_x_down_shape():
+    # M = 64 rows of a down-projection-shaped call (K = 14336, 512 of its
+    # output rows), x a column slice of a wider buffer (ldx > K), residual add
+    M, K, N = 64, 14336, 512
+    x, q, wp, s, _, b = make_case(M, K, N, K // 128, seed=64, bias=True)
+    wide = torch.zeros(M, K + 64, dtype=x.dtype)
+    wide[:, 32:32 + K] = x
+    res = torch.randn(M, N, generator=torch.Generator().manual_seed(65)).bfloat16()
+    y_ref = O.woq_linear(x, wp, s, bias=b, post_ops=("add",), post_bufs=[res])
+    wd = wide.to(DEV)
+    y = C.woq_linear(wd[:, 32:32 + K], *gpu(wp, s), None, b.to(DEV), post_ops=("add",),
+                     post_bufs=[res.to(DEV)])
+    check_close(y, y_ref)
+
+
 def test_llama_gate_up_silu_mul_m8():
     # gate half with the up half as the multiplier, N = 14336 per half
     run_case(8, 4096, 14336, 32, post=("silu", "mul"), nbuf=1, seed=77)

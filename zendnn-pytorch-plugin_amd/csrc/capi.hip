@@ -60,6 +60,41 @@ int convert_post_ops(const zt_post_ops *in, zt::PostOps *out, const char *op) {
   return ZT_OK;
 }
 
+size_t float_dt_bytes(int dt) { return dt == ZT_DT_F32 ? 4 : 2; }
+
+// Rows 33..64 of a decode-sized call run as blocks of 16 rows on the decode
+// kernels: each block streams the weights again, which still beats one
+// prefill-GEMM launch of so few row tiles (it cannot fill the GPU).  x, y
+// and the binary post-op buffers are offset to the block's first row.
+constexpr int64_t kWoqRowBlock = 16, kWoqRowBlockMax = 64;
+
+bool woq_use_row_blocks(const zt::WoqArgs &a) {
+  if (a.M <= 32 || a.M > kWoqRowBlockMax) return false;
+  zt::WoqArgs b = a;
+  b.M = kWoqRowBlock;
+  zt::DecodePlan p;
+  return zt::woq_select_kernel(b) == zt::kWoqDecode &&
+         zt::woq_decode_plan(b.M, b.N, b.K, &p) && zt::woq_decode_workspace(p, b.M, b.N) == 0;
+}
+
+hipError_t woq_row_blocks(const zt::WoqArgs &a, hipStream_t s) {
+  for (int64_t m0 = 0; m0 < a.M; m0 += kWoqRowBlock) {
+    zt::WoqArgs b = a;
+    b.M = std::min(kWoqRowBlock, a.M - m0);
+    b.x = static_cast<const char *>(a.x) + m0 * a.ldx * float_dt_bytes(a.x_dt);
+    b.y = static_cast<char *>(a.y) + m0 * a.ldy * float_dt_bytes(a.y_dt);
+    for (int i = 0; i < ZT_MAX_POST_OPS; ++i)
+      if (b.post.bufs[i])
+        b.post.bufs[i] = static_cast<const char *>(b.post.bufs[i]) +
+                         m0 * b.post.ld[i] * float_dt_bytes(b.post.dts[i]);
+    zt::DecodePlan p;
+    if (!zt::woq_decode_plan(b.M, b.N, b.K, &p)) return hipErrorInvalidValue;
+    const hipError_t err = zt::launch_woq_decode(b, p, nullptr, s);
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -223,6 +258,7 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   if (rc) return rc;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (woq_use_row_blocks(a)) return hip_status(woq_row_blocks(a, s), op);
   switch (zt::woq_select_kernel(a)) {
   case zt::kWoqDecode: {
     zt::DecodePlan p;

@@ -356,7 +356,8 @@ __global__ __launch_bounds__(decode_max_threads<CPW>()) void woq_decode_kernel(
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-// Weight-streaming decode kernel (M <= 16 and the activations fit in LDS).
+// Weight-streaming decode kernel (M <= 16 and the activations fit in LDS,
+// up to kStreamLdsMax with the partial slab).
 //
 // One workgroup per TPW 16-row tiles over all of K; its NW waves split K
 // into slices of CPW 128-wide chunks.  The workgroup first starts the copy
@@ -368,6 +369,7 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // The wave then walks its chunks: B operands come from LDS (lanes past M
 // read zeros), A operands are the fragments dequantised in registers.  K
 // partials meet in LDS and are added in wave order.
+constexpr size_t kStreamLdsMax = 160 * 1024;
 template <int NW>
 __host__ __device__ constexpr size_t stream_slab_bytes(int tpw) {
   return (size_t)NW * tpw * 16 * 17 * sizeof(float);
@@ -994,19 +996,23 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
 }
 
 // The weight-streaming kernel, when it applies: M <= 16 and x [M, K] in at
-// most 64 KB of LDS.  Returns false when the caller should use the planned
+// most kStreamLdsMax of LDS.  Returns false when the caller should use the planned
 // decode kernel instead.
 static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                               hipError_t *err) {
   const int C = (int)(a.K / 128);
   const int tiles = (int)((a.N + 15) / 16);
-  if (a.M > 16 || (size_t)a.M * stream_x_pitch((int)a.K) * 2 > 64 * 1024) return false;
+  if (a.M > 16) return false;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles
   int nw = 8, tpw = tiles >= 512 ? 2 : 1, cpw = 0;
   const char *e = std::getenv("ZT_WOQ_STREAM");  // "0" disables; "NW,CPW,TPW" forces
   if (e && e[0] == '0') return false;
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
+  // x [M, K] and the partial slab must fit one workgroup's LDS (160 KB on
+  // gfx950)
+  if (stream_slab_bytes<8>(2) + (size_t)a.M * stream_x_pitch((int)a.K) * 2 > kStreamLdsMax)
+    return false;
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
     for (int c : {2, 4, 8, 12, 16})
