@@ -136,6 +136,21 @@ def test_llama_decode_shapes_m16(N, K):
     run_case(16, K, N, K // 128, seed=N + K)
 
 
+@pytest.mark.parametrize("M,K", [(4, 3328), (16, 3328), (8, 3584)])
+def test_stream_kernel_x_copy_paths(M, K):
+    # 26 or 28 chunks of K: the stream kernel, x copied by loads when its
+    # rows are not whole 1 KB pieces (K % 512 != 0), by DMA otherwise
+    run_case(M, K, 96, K // 128, seed=M + K)
+
+
+@pytest.mark.parametrize("M", [5, 8, 9, 16])
+@pytest.mark.parametrize("post,nbuf", [((), 0), (("add",), 1)])
+def test_stream_kernel_phases_down_shape(M, post, nbuf):
+    # K = 14336 with M > 4: x does not fit LDS whole, so it is staged in 2
+    # (M <= 8) or 4 K-phases; 256 of the 4096 output rows keep the oracle fast
+    run_case(M, 14336, 256, 112, post=post, nbuf=nbuf, seed=M + 3 * nbuf, bias=True)
+
+
 # M = 33..64 runs as blocks of 16 rows on the decode kernels, with x, y and
 # the binary post-op buffers offset to each block's first row
 @pytest.mark.parametrize("M", [33, 40, 64])

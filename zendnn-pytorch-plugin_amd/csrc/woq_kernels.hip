@@ -376,8 +376,9 @@ __host__ __device__ constexpr size_t stream_slab_bytes(int tpw) {
 }
 __host__ __device__ inline int stream_x_pitch(int K) { return K + 8; }  // bf16
 
-template <int NW, int CPW, int TPW, int MODE>
-__global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_shift, int gmask) {
+template <int NW, int CPW, int TPW, int MODE, int P>
+__global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_shift, int gmask,
+                                                             int x_dma) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -385,29 +386,39 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
   const int KW = K / 8, C = K / 128;
   const int t0 = blockIdx.x * TPW;
-  const int c0 = wv * CPW;
   const int zmode = zp_mode_of(a.zp, a.zp_dt);
   const int s_bytes = MODE == kDecGenF32 ? 4 : 2;
   const auto w_rsrc = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
   const auto s_rsrc = make_rsrc(a.scales, (uint32_t)(a.G * N * s_bytes));
+  // Phases (P > 1, when x [M, K] does not fit LDS): K splits into P ranges
+  // of CP chunks; x holds one range at a time.  Wave w owns chunks
+  // p * CP + w * CPWP + j (j < CPWP) of phase p; with P == 1 its chunks are
+  // the contiguous slice w * CPW + c.
+  constexpr int CPWP = CPW / P;
+  const int CP = C / P;
+  auto chunk_of = [&](int c) {
+    if (P == 1) return wv * CPW + c;
+    const int p = c / CPWP, kcl = wv * CPWP + (c - p * CPWP);
+    return kcl < CP ? p * CP + kcl : C;  // C: past the phase, reads zeros
+  };
 
-  // 1. x [M, K] -> LDS (row pitch K + 8 bf16).  By DMA when every row
-  //    starts 16-byte aligned: instruction i moves 64 16-byte chunks of one
-  //    row (K % 128 == 0, so a row is whole 1 KB pieces).
-  const int XP = stream_x_pitch(K);
+  // 1. x [M, K] (or phase 0's range) -> LDS (row pitch XP bf16).  By DMA
+  //    when x_dma (stream_x_dma: every row 16-byte aligned and whole 1 KB
+  //    pieces; always for P > 1): instruction i moves 64 16-byte chunks of
+  //    one row.
+  const int XP = P == 1 ? stream_x_pitch(K) : stream_x_pitch(K / P);
   uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes<NW>(TPW));
-  const bool x_dma = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) == 0 &&
-                     (int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2 < (int64_t)kOobOffset;
-  if (x_dma) {
-    const auto x_rsrc = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
-    const int per_row = K / 512;  // 1 KB pieces per row
+  const auto x_rsrc = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
+  auto dma_x = [&](int p) {
+    const int per_row = (P == 1 ? K : K / P) / 512;  // 1 KB pieces per row
     for (int i = wv; i < M * per_row; i += NW) {
-      const int m = i / per_row, p = i - m * per_row;
+      const int m = i / per_row, q = i - m * per_row;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          x_rsrc, (lds_ptr_t)(xl + m * XP + p * 512), 16,
-          (uint32_t)(m * a.ldx * 2 + p * 1024 + lane * 16), 0, 0, 0);
+          x_rsrc, (lds_ptr_t)(xl + m * XP + q * 512), 16,
+          (uint32_t)(m * a.ldx * 2 + p * (K / P) * 2 + q * 1024 + lane * 16), 0, 0, 0);
     }
-  }
+  };
+  if (x_dma) dma_x(0);
 
   // 2. the slice's weights and scales, all in flight.  Rows past N are
   //    clamped (their results are never stored); chunks past C read zeros.
@@ -420,7 +431,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
-      const int kc = c0 + c;
+      const int kc = chunk_of(c);
       const int kcs = min(kc, C - 1);
       const uint32_t sidx = (uint32_t)((kcs >> cpg_shift) & gmask) * (uint32_t)N + (uint32_t)n;
       wr[t][c] = __builtin_bit_cast(
@@ -434,9 +445,9 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
 
-  // 3. copy x by loads when the DMA does not apply, and wait for it either
-  //    way (the barrier's fence waits for this wave's x DMA and the weight
-  //    loads issued after it; they are needed next anyway)
+  // 3. copy x by loads when the DMA does not apply (P == 1 only), and wait
+  //    for it either way (the barrier's fence waits for this wave's x DMA
+  //    and the weight loads issued after it; they are needed next anyway)
   if (!x_dma) {
     const uint16_t *xp = reinterpret_cast<const uint16_t *>(a.x);
     const int per_row = K / 8;
@@ -448,18 +459,25 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   }
   __syncthreads();
 
-  // 4. the slice's MFMAs
+  // 4. the slice's MFMAs; between phases every wave finishes with the
+  //    range in LDS before the next one is loaded over it
   f32x4_t acc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
-    const int kc = c0 + c;
+    if (P > 1 && c > 0 && c % CPWP == 0) {
+      __syncthreads();
+      dma_x(c / CPWP);
+      __syncthreads();
+    }
+    const int kc = chunk_of(c);
     if (kc < C) {
+      const int kcl = P == 1 ? kc : kc - (c / CPWP) * CP;  // chunk within the LDS range
       u32x4_t xb[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        xb[i] = lr < M ? *reinterpret_cast<const u32x4_t *>(xl + lr * XP + kc * 128 + 32 * lg + 8 * i)
+        xb[i] = lr < M ? *reinterpret_cast<const u32x4_t *>(xl + lr * XP + kcl * 128 + 32 * lg + 8 * i)
                        : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
@@ -981,23 +999,37 @@ static hipError_t launch_decode_t(const WoqArgs &a, const DecodePlan &p, hipStre
   return hipGetLastError();
 }
 
-template <int NW, int CPW, int TPW>
+// x goes to LDS by DMA when its rows (or each phase's part of them) are
+// whole 1 KB pieces, 16-byte aligned, within 32-bit offsets
+static bool stream_x_dma(const WoqArgs &a, int p) {
+  return (a.K / p) % 512 == 0 &&
+         ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) == 0 &&
+         (a.M - 1) * a.ldx * 2 + a.K * 2 < (int64_t)kOobOffset;
+}
+
+template <int NW, int CPW, int TPW, int P = 1>
 static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode) {
   const int tiles = (int)((a.N + 15) / 16);
-  const size_t lds = stream_slab_bytes<NW>(TPW) + (size_t)a.M * stream_x_pitch((int)a.K) * 2;
+  const int x_dma = stream_x_dma(a, P) ? 1 : 0;
+  if (P > 1 && !x_dma) return hipErrorInvalidValue;  // phases need the DMA (host-checked)
+  const size_t lds =
+      stream_slab_bytes<NW>(TPW) + (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2;
   dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
   if (mode == kDecFast)
-    woq_stream_kernel<NW, CPW, TPW, kDecFast><<<grid, block, lds, s>>>(a, shift, gmask);
+    woq_stream_kernel<NW, CPW, TPW, kDecFast, P><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+  else if (P > 1)
+    return hipErrorInvalidValue;  // phases are built for the fast mode only
   else if (mode == kDecGenBf16)
-    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16><<<grid, block, lds, s>>>(a, shift, gmask);
+    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
   else
-    woq_stream_kernel<NW, CPW, TPW, kDecGenF32><<<grid, block, lds, s>>>(a, shift, gmask);
+    woq_stream_kernel<NW, CPW, TPW, kDecGenF32, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
   return hipGetLastError();
 }
 
-// The weight-streaming kernel, when it applies: M <= 16 and x [M, K] in at
-// most kStreamLdsMax of LDS.  Returns false when the caller should use the planned
-// decode kernel instead.
+// The weight-streaming kernel, when it applies: M <= 16 and x [M, K] (or,
+// in the fast mode, a 2- or 4-phase range of it) in at most kStreamLdsMax
+// of LDS.  Returns false when the caller should use the planned decode
+// kernel instead.
 static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                               hipError_t *err) {
   const int C = (int)(a.K / 128);
@@ -1009,10 +1041,26 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   const char *e = std::getenv("ZT_WOQ_STREAM");  // "0" disables; "NW,CPW,TPW" forces
   if (e && e[0] == '0') return false;
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
-  // x [M, K] and the partial slab must fit one workgroup's LDS (160 KB on
-  // gfx950)
-  if (stream_slab_bytes<8>(2) + (size_t)a.M * stream_x_pitch((int)a.K) * 2 > kStreamLdsMax)
+  auto fits = [&](int p) {
+    return stream_slab_bytes<8>(2) + (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 <=
+           kStreamLdsMax;
+  };
+  if (!fits(1)) {
+    // phases: 8 waves, 16 chunks each (CPW / P per phase), ranges of whole
+    // 1 KB pieces per row, fast mode
+    if (e || mode != kDecFast || a.x_dt != ZT_DT_BF16) return false;
+    for (int p : {2, 4}) {
+      const int cp = C / p;
+      if (C % p || !stream_x_dma(a, p) || !fits(p) || (cp + 7) / 8 > 16 / p) continue;
+      if (std::getenv("ZT_WOQ_DEBUG"))
+        std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: NW=8 CPW=16 TPW=1 P=%d\n",
+                     (long long)a.M, (long long)a.N, (long long)a.K, p);
+      *err = p == 2 ? launch_stream_t<8, 16, 1, 2>(a, s, shift, gmask, mode)
+                    : launch_stream_t<8, 16, 1, 4>(a, s, shift, gmask, mode);
+      return true;
+    }
     return false;
+  }
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
     for (int c : {2, 4, 8, 12, 16})
