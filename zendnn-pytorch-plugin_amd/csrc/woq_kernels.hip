@@ -1036,19 +1036,23 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   const int tiles = (int)((a.N + 15) / 16);
   if (a.M > 16) return false;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
-  // each, two tiles per wave once there are two rounds of tiles
-  int nw = 8, tpw = tiles >= 512 ? 2 : 1, cpw = 0;
+  // each, two tiles per wave once there are two rounds of tiles, or more
+  // tiles than CUs when x takes most of the LDS (one workgroup per CU)
+  const bool big_x = (size_t)a.M * stream_x_pitch((int)a.K) * 2 > 64 * 1024;
+  int nw = 8, tpw = tiles >= 512 || (big_x && tiles > 256) ? 2 : 1, cpw = 0;
   const char *e = std::getenv("ZT_WOQ_STREAM");  // "0" disables; "NW,CPW,TPW" forces
   if (e && e[0] == '0') return false;
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
   auto fits = [&](int p) {
-    return stream_slab_bytes<8>(2) + (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 <=
+    return (size_t)nw * tpw * 16 * 17 * sizeof(float) +
+               (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 <=
            kStreamLdsMax;
   };
   if (!fits(1)) {
     // phases: 8 waves, 16 chunks each (CPW / P per phase), ranges of whole
     // 1 KB pieces per row, fast mode
     if (e || mode != kDecFast || a.x_dt != ZT_DT_BF16) return false;
+    nw = 8, tpw = 1;  // the phased kernels' shape
     for (int p : {2, 4}) {
       const int cp = C / p;
       if (C % p || !stream_x_dma(a, p) || !fits(p) || (cp + 7) / 8 > 16 / p) continue;
@@ -1075,6 +1079,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   ZT_STREAM_CASE(4, 16, 1) ZT_STREAM_CASE(4, 8, 2) ZT_STREAM_CASE(4, 4, 2) ZT_STREAM_CASE(4, 16, 2)
   ZT_STREAM_CASE(8, 4, 1) ZT_STREAM_CASE(8, 8, 1) ZT_STREAM_CASE(8, 12, 1) ZT_STREAM_CASE(8, 16, 1)
   ZT_STREAM_CASE(8, 4, 2) ZT_STREAM_CASE(8, 8, 2) ZT_STREAM_CASE(8, 16, 2) ZT_STREAM_CASE(2, 16, 1)
+  ZT_STREAM_CASE(16, 2, 1) ZT_STREAM_CASE(16, 2, 2) ZT_STREAM_CASE(16, 4, 1) ZT_STREAM_CASE(16, 8, 1)
 #undef ZT_STREAM_CASE
   return false;
 }
