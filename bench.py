@@ -370,7 +370,7 @@ def main():
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(c0["GBps"] / HBM_PEAK_GBS, 4),
                             "traffic": read_traffic(),
-                            "kernel": "woq_decode_kernel",
+                            "kernel": "woq_stream_kernel",
                             "kernel_avg_us": round(c0["s_per_call"] * 1e6, 3),
                             "algorithmic_bytes": c0["bytes_per_call"]}
     if not args.no_cpu_baseline and only in (None, "config0"):
