@@ -151,6 +151,26 @@ def test_stream_kernel_phases_down_shape(M, post, nbuf):
     run_case(M, 14336, 256, 112, post=post, nbuf=nbuf, seed=M + 3 * nbuf, bias=True)
 
 
+# 17..64 rows on the stream kernel: 2 or 4 token tiles per weight fragment,
+# x staged in 1, 2, 4 or 8 K-phases (M = 17: whole; 20..32: 2; 33..48: 4;
+# 49..64: 8 at K = 4096)
+@pytest.mark.parametrize("M", [17, 20, 24, 32, 33, 48, 64])
+@pytest.mark.parametrize("post,nbuf", [((), 0), (("mul", "add"), 2)])
+def test_stream_kernel_token_tiles(M, post, nbuf):
+    run_case(M, 4096, 160, 32, post=post, nbuf=nbuf, seed=M + 7 * nbuf, bias=True)
+
+
+def test_stream_kernel_token_tiles_strided_x():
+    M, K, N = 64, 4096, 96
+    x, q, wp, s, _, _ = make_case(M, K, N, K // 128, seed=640)
+    wide = torch.zeros(M, K + 256, dtype=x.dtype)
+    wide[:, 128:128 + K] = x
+    y_ref = O.woq_linear(x, wp, s)
+    wd = wide.to(DEV)
+    y = C.woq_linear(wd[:, 128:128 + K], *gpu(wp, s))
+    check_close(y, y_ref)
+
+
 # M = 33..64 runs as blocks of 16 rows on the decode kernels, with x, y and
 # the binary post-op buffers offset to each block's first row
 @pytest.mark.parametrize("M", [33, 40, 64])

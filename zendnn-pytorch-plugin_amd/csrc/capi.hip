@@ -62,14 +62,15 @@ int convert_post_ops(const zt_post_ops *in, zt::PostOps *out, const char *op) {
 
 size_t float_dt_bytes(int dt) { return dt == ZT_DT_F32 ? 4 : 2; }
 
-// Rows 33..64 of a decode-sized call run as blocks of 16 rows on the decode
-// kernels: each block streams the weights again, which still beats one
+// 17..64 rows of a decode-sized call: one stream-kernel launch over all
+// rows when x fits (in K phases), else blocks of 16 rows on the decode
+// kernels.  Each block streams the weights again, which still beats one
 // prefill-GEMM launch of so few row tiles (it cannot fill the GPU).  x, y
 // and the binary post-op buffers are offset to the block's first row.
 constexpr int64_t kWoqRowBlock = 16, kWoqRowBlockMax = 64;
 
 bool woq_use_row_blocks(const zt::WoqArgs &a) {
-  if (a.M <= 32 || a.M > kWoqRowBlockMax) return false;
+  if (a.M <= kWoqRowBlock || a.M > kWoqRowBlockMax) return false;
   zt::WoqArgs b = a;
   b.M = kWoqRowBlock;
   zt::DecodePlan p;
@@ -258,7 +259,13 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   if (rc) return rc;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (woq_use_row_blocks(a)) return hip_status(woq_row_blocks(a, s), op);
+  if (woq_use_row_blocks(a)) {
+    // one stream-kernel launch over all rows when x (in K phases) fits, else
+    // blocks of 16 rows
+    hipError_t err = hipSuccess;
+    if (zt::woq_try_stream(a, s, &err)) return hip_status(err, op);
+    return hip_status(woq_row_blocks(a, s), op);
+  }
   switch (zt::woq_select_kernel(a)) {
   case zt::kWoqDecode: {
     zt::DecodePlan p;

@@ -370,13 +370,13 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // read zeros), A operands are the fragments dequantised in registers.  K
 // partials meet in LDS and are added in wave order.
 constexpr size_t kStreamLdsMax = 160 * 1024;
-template <int NW>
-__host__ __device__ constexpr size_t stream_slab_bytes(int tpw) {
-  return (size_t)NW * tpw * 16 * 17 * sizeof(float);
+// per-wave fp32 partials: TPW row tiles x MT token tiles of 16 x 16 (+1 pad)
+__host__ __device__ constexpr size_t stream_slab_bytes(int nw, int tpw, int mt) {
+  return (size_t)nw * tpw * mt * 16 * 17 * sizeof(float);
 }
 __host__ __device__ inline int stream_x_pitch(int K) { return K + 8; }  // bf16
 
-template <int NW, int CPW, int TPW, int MODE, int P>
+template <int NW, int CPW, int TPW, int MODE, int P, int MT>
 __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_shift, int gmask,
                                                              int x_dma) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   //    pieces; always for P > 1): instruction i moves 64 16-byte chunks of
   //    one row.
   const int XP = P == 1 ? stream_x_pitch(K) : stream_x_pitch(K / P);
-  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes<NW>(TPW));
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes(NW, TPW, MT));
   const auto x_rsrc = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
   auto dma_x = [&](int p) {
     const int per_row = (P == 1 ? K : K / P) / 512;  // 1 KB pieces per row
@@ -460,10 +460,13 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   __syncthreads();
 
   // 4. the slice's MFMAs; between phases every wave finishes with the
-  //    range in LDS before the next one is loaded over it
-  f32x4_t acc[TPW];
+  //    range in LDS before the next one is loaded over it.  A chunk's
+  //    weight fragments are dequantised once and feed its MT token tiles.
+  f32x4_t acc[TPW][MT];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     if (P > 1 && c > 0 && c % CPWP == 0) {
@@ -474,40 +477,52 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     const int kc = chunk_of(c);
     if (kc < C) {
       const int kcl = P == 1 ? kc : kc - (c / CPWP) * CP;  // chunk within the LDS range
-      u32x4_t xb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        xb[i] = lr < M ? *reinterpret_cast<const u32x4_t *>(xl + lr * XP + kcl * 128 + 32 * lg + 8 * i)
-                       : u32x4_t{0u, 0u, 0u, 0u};
+      bf16x8_t wb[TPW][4];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const uint32_t sb = sr[t][c];
         const float sc = MODE == kDecGenF32 ? __uint_as_float(sb) : __uint_as_float(sb << 16);
 #pragma unroll
+        for (int i = 0; i < 4; ++i) wb[t][i] = dq_word<MODE>(wr[t][c][i], sc, zr[t][c], zmode);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = mt * 16 + lr;
+        u32x4_t xb[4];
+#pragma unroll
         for (int i = 0; i < 4; ++i)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              dq_word<MODE>(wr[t][c][i], sc, zr[t][c], zmode),
-              __builtin_bit_cast(bf16x8_t, xb[i]), acc[t], 0, 0, 0);
+          xb[i] = row < M ? *reinterpret_cast<const u32x4_t *>(xl + row * XP + kcl * 128 + 32 * lg + 8 * i)
+                          : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int t = 0; t < TPW; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                wb[t][i], __builtin_bit_cast(bf16x8_t, xb[i]), acc[t][mt], 0, 0, 0);
       }
     }
   }
 
-  // 5. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t], then
+  // 5. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t][mt], then
   //    each output adds the NW partials in wave order
   float *slab = reinterpret_cast<float *>(smem);
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][r];
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        slab[(((wv * TPW + t) * MT + mt) * 16 + 4 * lg + r) * 17 + lr] = acc[t][mt][r];
   __syncthreads();
   const int n0 = t0 * 16;
   for (int idx = tid; idx < TPW * 16 * M; idx += 64 * NW) {
     const int m = idx / (TPW * 16), nr = idx - m * (TPW * 16);
+    const int t = nr >> 4, r16 = nr & 15, mt = m >> 4;
     const int n = n0 + nr;
     if (n >= N) continue;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) v += slab[((w * TPW) * 16 + nr) * 17 + m];
+    for (int w = 0; w < NW; ++w) v += slab[(((w * TPW + t) * MT + mt) * 16 + r16) * 17 + (m & 15)];
     if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
     v = apply_post_ops(v, a.post, m, n);
     store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
@@ -1007,34 +1022,34 @@ static bool stream_x_dma(const WoqArgs &a, int p) {
          (a.M - 1) * a.ldx * 2 + a.K * 2 < (int64_t)kOobOffset;
 }
 
-template <int NW, int CPW, int TPW, int P = 1>
+template <int NW, int CPW, int TPW, int P = 1, int MT = 1>
 static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode) {
   const int tiles = (int)((a.N + 15) / 16);
   const int x_dma = stream_x_dma(a, P) ? 1 : 0;
   if (P > 1 && !x_dma) return hipErrorInvalidValue;  // phases need the DMA (host-checked)
   const size_t lds =
-      stream_slab_bytes<NW>(TPW) + (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2;
+      stream_slab_bytes(NW, TPW, MT) + (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2;
   dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
   if (mode == kDecFast)
-    woq_stream_kernel<NW, CPW, TPW, kDecFast, P><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
-  else if (P > 1)
-    return hipErrorInvalidValue;  // phases are built for the fast mode only
+    woq_stream_kernel<NW, CPW, TPW, kDecFast, P, MT><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+  else if (P > 1 || MT > 1)
+    return hipErrorInvalidValue;  // phases and token tiles are built for the fast mode only
   else if (mode == kDecGenBf16)
-    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
   else
-    woq_stream_kernel<NW, CPW, TPW, kDecGenF32, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+    woq_stream_kernel<NW, CPW, TPW, kDecGenF32, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
   return hipGetLastError();
 }
 
-// The weight-streaming kernel, when it applies: M <= 16 and x [M, K] (or,
-// in the fast mode, a 2- or 4-phase range of it) in at most kStreamLdsMax
-// of LDS.  Returns false when the caller should use the planned decode
-// kernel instead.
+// The weight-streaming kernel, when it applies: M <= 64 and x [M, K] (or,
+// in the fast mode, a 2-, 4- or 8-phase range of it) in at most
+// kStreamLdsMax of LDS.  Returns false when the caller should use another
+// kernel.
 static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                               hipError_t *err) {
   const int C = (int)(a.K / 128);
   const int tiles = (int)((a.N + 15) / 16);
-  if (a.M > 16) return false;
+  if (a.M > 64) return false;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles, or more
   // tiles than CUs when x takes most of the LDS (one workgroup per CU)
@@ -1043,25 +1058,32 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   const char *e = std::getenv("ZT_WOQ_STREAM");  // "0" disables; "NW,CPW,TPW" forces
   if (e && e[0] == '0') return false;
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
+  const int mt = (int)((a.M + 15) / 16) == 3 ? 4 : (int)((a.M + 15) / 16);
   auto fits = [&](int p) {
-    return (size_t)nw * tpw * 16 * 17 * sizeof(float) +
-               (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 <=
+    return stream_slab_bytes(nw, tpw, mt) + (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 <=
            kStreamLdsMax;
   };
-  if (!fits(1)) {
-    // phases: 8 waves, 16 chunks each (CPW / P per phase), ranges of whole
-    // 1 KB pieces per row, fast mode
+  if (mt > 1 || !fits(1)) {
+    // several token tiles or K phases: 8 waves, one tile each, fast mode,
+    // the fewest phases whose x range fits
     if (e || mode != kDecFast || a.x_dt != ZT_DT_BF16) return false;
-    nw = 8, tpw = 1;  // the phased kernels' shape
-    for (int p : {2, 4}) {
+    nw = 8, tpw = 1;
+    for (int p : {1, 2, 4, 8}) {
       const int cp = C / p;
-      if (C % p || !stream_x_dma(a, p) || !fits(p) || (cp + 7) / 8 > 16 / p) continue;
+      if (C % p || (p > 1 && !stream_x_dma(a, p)) || !fits(p)) continue;
+      const int cpw_need = p * ((cp + 7) / 8);  // chunks per wave over all phases
       if (std::getenv("ZT_WOQ_DEBUG"))
-        std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: NW=8 CPW=16 TPW=1 P=%d\n",
-                     (long long)a.M, (long long)a.N, (long long)a.K, p);
-      *err = p == 2 ? launch_stream_t<8, 16, 1, 2>(a, s, shift, gmask, mode)
-                    : launch_stream_t<8, 16, 1, 4>(a, s, shift, gmask, mode);
-      return true;
+        std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: MT=%d P=%d CPW>=%d\n",
+                     (long long)a.M, (long long)a.N, (long long)a.K, mt, p, cpw_need);
+#define ZT_STREAM_PCASE(CPW_, P_, MT_)                                          \
+  if (mt == MT_ && p == P_ && cpw_need <= CPW_ && CPW_ % P_ == 0) {            \
+    *err = launch_stream_t<8, CPW_, 1, P_, MT_>(a, s, shift, gmask, mode);      \
+    return true;                                                                \
+  }
+      ZT_STREAM_PCASE(16, 2, 1) ZT_STREAM_PCASE(16, 4, 1)
+      ZT_STREAM_PCASE(4, 1, 2) ZT_STREAM_PCASE(4, 2, 2) ZT_STREAM_PCASE(16, 4, 2)
+      ZT_STREAM_PCASE(4, 1, 4) ZT_STREAM_PCASE(4, 4, 4) ZT_STREAM_PCASE(8, 8, 4)
+#undef ZT_STREAM_PCASE
     }
     return false;
   }
@@ -1082,6 +1104,18 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   ZT_STREAM_CASE(16, 2, 1) ZT_STREAM_CASE(16, 2, 2) ZT_STREAM_CASE(16, 4, 1) ZT_STREAM_CASE(16, 8, 1)
 #undef ZT_STREAM_CASE
   return false;
+}
+
+// The stream kernel for a call of up to 64 rows whose shape the decode
+// kernels accept (capi.hip tries it before splitting 33..64 rows into
+// blocks of 16).
+bool woq_try_stream(const WoqArgs &a, hipStream_t s, hipError_t *err) {
+  const int64_t cpg = a.G == 1 ? 0 : (a.K / a.G) / 128;
+  int shift = 0;
+  while (cpg > 1 && (1 << shift) < cpg) ++shift;
+  const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  const int mode = a.s_dt == ZT_DT_F32 ? kDecGenF32 : (a.zp ? kDecGenBf16 : kDecFast);
+  return try_launch_stream(a, s, shift, gmask, mode, err);
 }
 
 hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *workspace,

@@ -51,6 +51,9 @@ hipError_t launch_woq_generic(const WoqArgs &a, hipStream_t s);
 hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p,
                              void *workspace, hipStream_t s);
 hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s);
+// The weight-streaming decode kernel for up to 64 rows, when it applies
+// (returns false otherwise; *err holds the launch status when it does).
+bool woq_try_stream(const WoqArgs &a, hipStream_t s, hipError_t *err);
 
 hipError_t launch_repack(const int8_t *w, int64_t N, int64_t K, int32_t *out,
                          hipStream_t s);
