@@ -100,3 +100,46 @@ def test_prefill_shape_accumulator_checksum():
     w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
     acc = C.s8s8s32_gemm(a.to(DEV), w.to(DEV)).cpu()
     assert torch.equal(acc, torch._int_mm(a, w.t().contiguous()))
+
+
+# 17..128 tokens run on the 32x32x32 skinny kernel over qx in fragment
+# order: ragged M inside the last 32-token tile, N not a multiple of the
+# 16-row weight tiles (an odd last tile pairs with zeros), K of one chunk
+# (waves with no chunks) up to 64.
+@pytest.mark.parametrize("M,K,N", [(17, 64, 50), (31, 320, 100), (32, 4096, 96),
+                                   (33, 1024, 4100), (64, 448, 48), (100, 4096, 1000),
+                                   (128, 192, 47)])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_dynamic_qlinear_fragment_kernel(M, K, N, x_dtype):
+    x, w, sw, b = make(M, K, N, seed=7 * M + K + N, x_dtype=x_dtype)
+    y_ref = O.dynamic_qlinear(x, w, sw, b)
+    y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV)).cpu()
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
+# every compiled (TPW, PF, NW) shape of the 32x32 kernel, forced; M = 1..16
+# forced onto it too
+@pytest.mark.parametrize("M,shape", [(20, "4,4,8"), (40, "4,2,8"), (64, "3,2,8"), (90, "2,2,8"),
+                                     (128, "4,2,8"), (128, "3,4,4"), (97, "4,4,4"),
+                                     (1, None), (9, None), (16, None)])
+def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, monkeypatch):
+    K, N = 1344, 232
+    if shape:
+        monkeypatch.setenv("ZT_S8_SKINNY32", shape)
+    monkeypatch.setenv("ZT_S8_FRAG", "1")
+    x, w, sw, b = make(M, K, N, seed=M + 5)
+    y_ref = O.dynamic_qlinear(x, w, sw, b)
+    y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV)).cpu()
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("post", [("relu",), ("add",), ("mul", "add"), ("gelu_tanh",)])
+def test_dynamic_qlinear_fragment_kernel_post_ops(post):
+    M, K, N = 48, 512, 136
+    x, w, sw, b = make(M, K, N, seed=3)
+    g = torch.Generator().manual_seed(11)
+    bufs = [torch.randn(M, N, generator=g).bfloat16() for p in post if p in ("add", "mul")]
+    y_ref = O.dynamic_qlinear(x, w, sw, b, post_ops=post, post_bufs=bufs)
+    y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV), post_ops=post,
+                          post_bufs=[t.to(DEV) for t in bufs]).cpu()
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)

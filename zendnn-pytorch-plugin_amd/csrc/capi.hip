@@ -287,10 +287,15 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   }
 }
 
+// qx region of the dynamic-qlinear workspace: whole 32-row tiles (the
+// fragment order of the skinny int8 kernel), rounded to 256 bytes
+static size_t dyn_qx_bytes(int64_t M, int64_t K) {
+  return ((size_t)((M + 31) / 32 * 32) * (size_t)K + 255) & ~(size_t)255;
+}
+
 size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K) {
   if (M <= 0 || K <= 0) return 0;
-  const size_t q = ((size_t)M * K + 255) & ~(size_t)255;
-  return q + (size_t)M * sizeof(float);
+  return dyn_qx_bytes(M, K) + (size_t)M * sizeof(float);
 }
 
 int zt_dynamic_quantize(const void *x, int32_t x_dtype, int64_t M, int64_t K,
@@ -301,7 +306,7 @@ int zt_dynamic_quantize(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   if (M < 0 || K < 1) return fail(ZT_EINVAL, "%s: need M >= 0, K >= 1", op);
   if (M == 0) return ZT_OK;
   if (!x || !qx || !sx) return fail(ZT_EINVAL, "%s: null pointer", op);
-  return hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx,
+  return hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, false,
                                             reinterpret_cast<hipStream_t>(stream)),
                     op);
 }
@@ -346,11 +351,11 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   int rc = convert_post_ops(post, &a.post, op);
   if (rc) return rc;
   int8_t *qx = reinterpret_cast<int8_t *>(workspace);
-  float *sx = reinterpret_cast<float *>(
-      reinterpret_cast<char *>(workspace) + (((size_t)M * K + 255) & ~(size_t)255));
+  float *sx = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + dyn_qx_bytes(M, K));
   a.qx = qx, a.sx = sx;
+  a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, s), op);
+  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s), op);
   if (rc) return rc;
   return hip_status(zt::launch_s8_gemm(a, s), op);
 }

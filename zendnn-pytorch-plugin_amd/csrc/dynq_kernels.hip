@@ -20,8 +20,18 @@ namespace zt {
 
 namespace {
 
+// Byte offset of qx[m][k] in the fragment order read by s8_skinny32_kernel
+// (K % 64 == 0): 32-token tiles, each a run of 64-k chunks, each chunk two
+// 1 KB B-operand fragments of v_mfma_i32_32x32x32_i8.  Fragment f holds the
+// 16-byte k blocks f (lanes 0-31) and f + 2 (lanes 32-63) of the chunk; lane
+// 32*h + (m % 32) holds block f + 2h of token m.
+__device__ __forceinline__ int64_t qx_frag_offset(int64_t m, int64_t k, int64_t K) {
+  return (((m >> 5) * (K >> 6) + (k >> 6)) * 2 + ((k >> 4) & 1)) * 1024 +
+         ((((k >> 5) & 1) * 32 + (m & 31)) * 16) + (k & 15);
+}
+
 __global__ __launch_bounds__(256) void dyn_quantize_kernel(
-    const void *x, int x_dt, int64_t K, int8_t *qx, float *sx) {
+    const void *x, int x_dt, int64_t K, int8_t *qx, float *sx, int frag) {
   __shared__ float wmax[4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t m = blockIdx.x;
@@ -41,15 +51,16 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(
   for (int64_t k = tid; k < K; k += 256) {
     float r = rintf(__fdiv_rn(load_elem(x, x_dt, base + k), s));
     r = fminf(fmaxf(r, -128.f), 127.f);
-    qx[base + k] = (int8_t)(int)r;
+    qx[frag ? qx_frag_offset(m, k, K) : base + k] = (int8_t)(int)r;
   }
 }
 
 // The same per-row quantisation for bf16 rows with K % 8 == 0, 16-byte
 // aligned: each thread holds up to VPT 8-element vectors of its row in
 // registers between the amax and the quantise pass and writes 8 bytes of qx
-// at a time.  Bit-identical to dyn_quantize_kernel.
-template <int VPT>
+// at a time (row-major, or in fragment order when FRAG).  Bit-identical to
+// dyn_quantize_kernel.
+template <int VPT, bool FRAG>
 __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *x, int64_t K,
                                                                  int8_t *qx, float *sx) {
   __shared__ float wmax[4];
@@ -95,7 +106,10 @@ __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *
       o[h] = q1(__uint_as_float(a0 << 16)) | (q1(__uint_as_float(a0 & 0xffff0000u)) << 8) |
              (q1(__uint_as_float(a1 << 16)) << 16) | (q1(__uint_as_float(a1 & 0xffff0000u)) << 24);
     }
-    out[j] = o;
+    if (FRAG)
+      *reinterpret_cast<u32x2_t *>(qx + qx_frag_offset(m, 8 * (int64_t)j, K)) = o;
+    else
+      out[j] = o;
   }
 }
 
@@ -612,6 +626,69 @@ constexpr size_t s8_skinny_lds() {
   return (size_t)4 * (16 * MT) * (16 * TPW + kSkPitchPad) * 4;
 }
 
+// Sum of the four K-partial slabs [4][ROWS][16*TPW + pad] int32 and the
+// dequantising epilogue, for the skinny kernels (ROWS tokens, TPW 16-row
+// weight tiles from n0, 64*NW threads).
+template <int ROWS, int TPW, int NW>
+__device__ __forceinline__ void skinny_epilogue(const DynArgs &a, const int32_t *slab, int n0,
+                                                int tid) {
+  const int M = (int)a.M, N = (int)a.N;
+  constexpr int P = 16 * TPW + kSkPitchPad;
+  // 4*TPW four-column groups divide the 64*NW threads: a thread keeps its
+  // columns, so their weight scales and bias are loaded once
+  constexpr int G4 = 4 * TPW;
+  if ((64 * NW) % G4 != 0) {  // groups do not divide the threads: general loop
+    for (int idx = tid; idx < ROWS * G4; idx += 64 * NW) {
+      const int m = idx / G4, cc = (idx % G4) * 4;
+      if (m >= M || n0 + cc >= N) continue;
+      i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + cc);
+#pragma unroll
+      for (int w = 1; w < 4; ++w)
+        v += *reinterpret_cast<const i32x4_t *>(slab + (w * ROWS + m) * P + cc);
+      dyn_epilogue4(a, m, n0 + cc, v);
+    }
+    return;
+  }
+  const int c4 = (tid % G4) * 4, n = n0 + c4;
+  if (n >= N) return;
+  const bool fast = a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0;
+  float sw[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+  if (fast) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sw[r] = load_elem(a.sw, a.sw_dt, n + r);
+      if (a.bias) b[r] = load_elem(a.bias, a.b_dt, n + r);
+    }
+  }
+  for (int m = tid / G4; m < M && m < ROWS; m += (64 * NW) / G4) {
+    i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + c4);
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      v += *reinterpret_cast<const i32x4_t *>(slab + (w * ROWS + m) * P + c4);
+    if (!fast) {
+      dyn_epilogue4(a, m, n, v);
+      continue;
+    }
+    const float sxm = a.sx[m];
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = (float)v[r] * sxm;
+      t = t * sw[r];
+      f[r] = a.bias ? t + b[r] : t;
+    }
+    if (a.y_dt == ZT_DT_BF16) {
+      u32x2_t pk;
+      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
+    } else {
+      *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
+          f32x4_t{f[0], f[1], f[2], f[3]};
+    }
+  }
+}
+
 template <int MT, int TPW, int PF, int NW>
 __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunks_per_wave) {
   extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
@@ -703,59 +780,151 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunk
       }
   }
   __syncthreads();
-  // 4*TPW four-column groups divide the 64*NW threads: a thread keeps its
-  // columns, so their weight scales and bias are loaded once
-  constexpr int G4 = 4 * TPW;
-  if ((64 * NW) % G4 != 0) {  // groups do not divide the threads: general loop
-    for (int idx = tid; idx < 16 * MT * G4; idx += 64 * NW) {
-      const int m = idx / G4, cc = (idx % G4) * 4;
-      if (m >= M || n0 + cc >= N) continue;
-      i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + cc);
+  skinny_epilogue<16 * MT, TPW, NW>(a, slab, n0, tid);
+}
+
+// The skinny GEMM on v_mfma_i32_32x32x32_i8 (twice the int8 rate of the
+// 16x16x64 shape on gfx950), for qx in fragment order (qx_frag_offset,
+// written by the quantise kernels of zt_dynamic_qlinear).  MT 32-token tiles,
+// TPW 16-row weight tiles per workgroup, NW waves splitting K into 64-wide
+// chunks, PF chunks of loads in flight per wave, as in s8_skinny_kernel.
+// Weights load as two 16-row x 64 B tiles; one v_permlane16_swap per dword
+// turns a pair into the two 32-row A operands of a chunk (k blocks {0, 2}
+// and {1, 3} of each row), which pair with qx fragments 0 and 1.  An odd
+// last tile pairs with zeros.  D[n][m] leaves each lane four runs of four
+// consecutive n of one token; the K partials meet in LDS as in the 16-token
+// kernel.
+template <int MT, int TPW, int PF, int NW>
+__global__ __launch_bounds__(64 * NW) void s8_skinny32_kernel(DynArgs a, int chunks_per_wave) {
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+  constexpr int NG = (TPW + 1) / 2;  // 32-row groups
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4, lh = lane >> 5;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int n0 = blockIdx.x * (16 * TPW);
+  const int tiles_m = (M + 31) >> 5;
+  const auto q_rs = make_rsrc(a.qx, (uint32_t)(tiles_m * 32 * K));
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+
+  uint32_t w_row[TPW], q_tile[MT];
 #pragma unroll
-      for (int w = 1; w < 4; ++w)
-        v += *reinterpret_cast<const i32x4_t *>(slab + (w * 16 * MT + m) * P + cc);
-      dyn_epilogue4(a, m, n0 + cc, v);
-    }
-    return;
+  for (int t = 0; t < TPW; ++t) {
+    const int n = n0 + t * 16 + lr;
+    w_row[t] = n < N ? (uint32_t)(n * K + 16 * lg) : kOobOffset;
   }
-  const int c4 = (tid % G4) * 4, n = n0 + c4;
-  if (n >= N) return;
-  const bool fast = a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0;
-  float sw[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
-  if (fast) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sw[r] = load_elem(a.sw, a.sw_dt, n + r);
-      if (a.bias) b[r] = load_elem(a.bias, a.b_dt, n + r);
+  for (int j = 0; j < MT; ++j) q_tile[j] = j < tiles_m ? (uint32_t)(j * 32 * K) : kOobOffset;
+  const int c_begin = wv * chunks_per_wave;
+  const int nch = max(0, min(chunks_per_wave, K / 64 - c_begin));
+
+  // K % 64 == 0 (host-checked).  A weight row past N, a token tile past M
+  // and a chunk past the wave's range start at kOobOffset and read zeros;
+  // two of them together wrap to a small in-range offset, whose data only
+  // reaches an output row or column that is never stored.  Tokens of the
+  // last tile past M read whatever the workspace holds, with the same
+  // effect.
+  i32x4_t wf[PF][TPW], qf[PF][MT][2];
+  auto load = [&](int slot, int c) {
+    const bool in = c < nch;
+    const uint32_t kw = in ? (uint32_t)((c_begin + c) * 64) : kOobOffset;
+    const uint32_t kq = in ? (uint32_t)((c_begin + c) * 2048) + 16u * lane : kOobOffset;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+      wf[slot][t] = __builtin_bit_cast(
+          i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, w_row[t] + kw, 0, 0));
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        qf[slot][j][f] = __builtin_bit_cast(
+            i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(q_rs, q_tile[j] + kq + 1024u * f, 0, 0));
+  };
+
+  i32x16_t acc[NG][MT];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[g][j][r] = 0;
+
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load(p, p);
+  for (int c = 0; c < nch; c += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        i32x4_t a0 = wf[p][2 * g], a1 = 2 * g + 1 < TPW ? wf[p][2 * g + 1] : i32x4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const auto sw = __builtin_amdgcn_permlane16_swap((uint32_t)a0[e], (uint32_t)a1[e],
+                                                          false, false);
+          a0[e] = (int32_t)sw[0];
+          a1[e] = (int32_t)sw[1];
+        }
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          acc[g][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[p][j][0], acc[g][j], 0, 0, 0);
+          acc[g][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[p][j][1], acc[g][j], 0, 0, 0);
+        }
+      }
+      load(p, c + p + PF);  // chunks past nch read as zero and are never used
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-  for (int m = tid / G4; m < M && m < 16 * MT; m += (64 * NW) / G4) {
-    i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + c4);
+
+  // K partials: slab[w][m][n_local]; D register r of lane l holds
+  // n_local = 32*g + 8*(r/4) + 4*(l/32) + r%4 of token 32*j + l%32
+  constexpr int ROWS = 32 * MT, P = 16 * TPW + kSkPitchPad;
+  int32_t *slab = reinterpret_cast<int32_t *>(s8_smem);
+  auto put = [&](int w, bool add) {
 #pragma unroll
-    for (int w = 1; w < 4; ++w)
-      v += *reinterpret_cast<const i32x4_t *>(slab + (w * 16 * MT + m) * P + c4);
-    if (!fast) {
-      dyn_epilogue4(a, m, n, v);
-      continue;
-    }
-    const float sxm = a.sx[m];
-    float f[4];
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float t = (float)v[r] * sxm;
-      t = t * sw[r];
-      f[r] = a.bias ? t + b[r] : t;
-    }
-    if (a.y_dt == ZT_DT_BF16) {
-      u32x2_t pk;
-      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
-      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
-    } else {
-      *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
-          f32x4_t{f[0], f[1], f[2], f[3]};
-    }
-  }
+      for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (2 * g + 1 >= TPW && q >= 2) continue;  // rows of the zero half
+          i32x4_t *d = reinterpret_cast<i32x4_t *>(
+              slab + (w * ROWS + 32 * j + (lane & 31)) * P + 32 * g + 8 * q + 4 * lh);
+          i32x4_t v = {acc[g][j][4 * q], acc[g][j][4 * q + 1], acc[g][j][4 * q + 2],
+                       acc[g][j][4 * q + 3]};
+          if (add) v += *d;
+          *d = v;
+        }
+  };
+  if (NW == 8 && wv >= 4) put(wv - 4, false);
+  if (NW == 8) __syncthreads();
+  if (wv < 4) put(wv, NW == 8);
+  __syncthreads();
+  skinny_epilogue<ROWS, TPW, NW>(a, slab, n0, tid);
+}
+
+template <int MT, int TPW, int PF, int NW>
+hipError_t launch_s8_skinny32_t(const DynArgs &a, hipStream_t s) {
+  const int total = (int)(a.K / 64);
+  int cpw = (total + NW - 1) / NW;
+  cpw = (cpw + PF - 1) / PF * PF;
+  const int blocks = (int)((a.N + 16 * TPW - 1) / (16 * TPW));
+  const size_t lds = (size_t)4 * (32 * MT) * (16 * TPW + kSkPitchPad) * 4;
+  s8_skinny32_kernel<MT, TPW, PF, NW><<<dim3((unsigned)blocks), dim3(64 * NW), lds, s>>>(a, cpw);
+  return hipGetLastError();
+}
+
+hipError_t launch_s8_skinny32(const DynArgs &a, hipStream_t s) {
+  const int mt = (int)((a.M + 31) / 32);
+  const char *e = std::getenv("ZT_S8_SKINNY32");  // "TPW,PF,NW"
+  int tpw = 0, pf = 0, nw = 0;
+  if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+#define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
+  if (mt <= MT_ && (!tpw || (tpw == TPW_ && pf == PF_ && nw == NW_)))          \
+    return launch_s8_skinny32_t<MT_, TPW_, PF_, NW_>(a, s);
+  ZT_SK(1, 4, 4, 8) ZT_SK(2, 4, 2, 8) ZT_SK(4, 3, 2, 8) ZT_SK(4, 2, 2, 8) ZT_SK(4, 4, 2, 8)
+  ZT_SK(4, 3, 4, 4) ZT_SK(4, 4, 4, 4)
+#undef ZT_SK
+  return hipErrorInvalidValue;
 }
 
 template <int MT, int TPW, int PF, int NW>
@@ -796,28 +965,44 @@ hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
-                               int8_t *qx, float *sx, hipStream_t s) {
+                               int8_t *qx, float *sx, bool frag, hipStream_t s) {
   if (M == 0) return hipSuccess;
+  if (frag && K % 64 != 0) return hipErrorInvalidValue;
   const bool vec = x_dt == ZT_DT_BF16 && K % 8 == 0 &&
                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(qx)) & 15u) == 0;
   const int64_t per = (K / 8 + 255) / 256;  // 8-element vectors per thread
   if (vec && per <= 8) {
     const uint16_t *xb = static_cast<const uint16_t *>(x);
-    if (per <= 2)
-      dyn_quantize_bf16_kernel<2><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx);
-    else if (per <= 4)
-      dyn_quantize_bf16_kernel<4><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx);
-    else
-      dyn_quantize_bf16_kernel<8><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx);
-    return hipGetLastError();
+#define ZT_QB(V_)                                                                      \
+  if (per <= V_) {                                                                     \
+    if (frag)                                                                          \
+      dyn_quantize_bf16_kernel<V_, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx); \
+    else                                                                               \
+      dyn_quantize_bf16_kernel<V_, false><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx); \
+    return hipGetLastError();                                                          \
+  }
+    ZT_QB(2) ZT_QB(4) ZT_QB(8)
+#undef ZT_QB
   }
   hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)M), dim3(256), 0, s, x,
-                     x_dt, K, qx, sx);
+                     x_dt, K, qx, sx, (int)frag);
   return hipGetLastError();
+}
+
+bool s8_frag_ok(const DynArgs &a) {
+  // 17..128 tokens: the 32x32 kernel's tiles are at least half full there
+  // (one 16-token tile is cheaper on the 16x16 kernel)
+  const char *e = std::getenv("ZT_S8_FRAG");  // "0": never, "1": from M = 1
+  const int64_t lo = e && e[0] == '1' ? 1 : 17;
+  if ((e && e[0] == '0') || a.M < lo || a.M > 128 || a.K % 64 != 0) return false;
+  const int64_t rows = (a.M + 31) / 32 * 32;
+  return rows * a.K < (int64_t)kOobOffset && a.N * a.K < (int64_t)kOobOffset &&
+         ((reinterpret_cast<uintptr_t>(a.qx) | reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0;
 }
 
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
+  if (a.qx_frag) return s8_frag_ok(a) ? launch_s8_skinny32(a, s) : hipErrorInvalidValue;
   const bool aligned = ((reinterpret_cast<uintptr_t>(a.qx) |
                          reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0;
   if (a.K % 16 != 0 || !aligned) {

@@ -73,12 +73,17 @@ struct DynArgs {
   PostOps post;
   void *y;
   int y_dt;  // ZT_DT_S32 writes the raw accumulators
-  const int8_t *qx;  // [M, K] quantised activations
+  const int8_t *qx;  // [M, K] quantised activations (row-major unless qx_frag)
   const float *sx;   // [M]
+  int qx_frag;       // qx in the 32-token fragment order of s8_skinny32_kernel
 };
 
+// frag: write qx in the fragment order (K % 64 == 0; the buffer holds
+// ceil(M / 32) * 32 rows)
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
-                               int8_t *qx, float *sx, hipStream_t s);
+                               int8_t *qx, float *sx, bool frag, hipStream_t s);
+// whether launch_s8_gemm takes qx in fragment order for this call (a.qx set)
+bool s8_frag_ok(const DynArgs &a);
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);
 
 // Grouped int4 MoE (moe_kernels.hip).  Device scratch of one call.
