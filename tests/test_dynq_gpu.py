@@ -50,7 +50,10 @@ def test_quantize_bit_exact(M, K, x_dtype):
                                    # large-M tiled kernel: ragged M, N and K % 128 != 0
                                    (257, 200, 144), (520, 4160, 272), (1024, 1000, 2064),
                                    # skinny weight-streaming kernel: ragged N, K % 64 != 0
-                                   (33, 100, 4112), (100, 4100, 272), (17, 50, 80)])
+                                   (33, 100, 4112), (100, 4100, 272), (17, 50, 80),
+                                   # more tiles than CUs (workgroups loop over tiles),
+                                   # ragged M and N, K % 64 != 0
+                                   (2100, 4100, 144), (4096, 2080, 208)])
 def test_s8_gemm_accumulators_bit_exact(M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)

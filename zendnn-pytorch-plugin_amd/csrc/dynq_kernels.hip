@@ -599,6 +599,172 @@ void s8_gemm_dma_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
   s8_tile_epilogue<BM, BN>(a, tile, sx_l, m0, n0, tid);
 }
 
+// Prefill int8 GEMM on v_mfma_i32_32x32x32_i8: BM x BN tiles, 4 waves of
+// (BM/2) x (BN/2), K in steps of 64 bytes moved straight into LDS by the
+// buffer unit, S stages deep, two workgroups per CU (at most 256 registers
+// and 80 KB of LDS each), so one workgroup's epilogue and barriers overlap
+// the other's MFMAs.
+//
+// LDS rows are 64 B; the 16-byte chunk c of row r sits at position
+// c ^ f(r), f(r) = ((r >> 2) ^ (r >> 1)) & 3, and one wave's 1 KB load fills
+// 16 whole rows.  f gives the 16 rows a fragment read touches 16 distinct
+// 16-byte bank groups over 256 bytes, and any 8 of them (rows of equal
+// parity) distinct groups over 128 bytes.
+// Step ks: wait for this wave's loads of step ks (those of the S - 2 later
+// steps stay in flight), barrier (a bare s_barrier: __syncthreads' release
+// fence would wait for every load in flight), start the loads of step
+// ks + S - 1 into the buffer step ks - 1 used, read the step's fragments
+// and run its MFMAs.  Loads past the last step read zeros into a buffer no
+// step reads, so the loop has no branches (a branch join makes the compiler
+// wait for LDS reads still in flight).
+//
+// The MFMA takes W as A and qx as B, so D is [n][m]: register r of lane l
+// holds n = 8*(r/4) + 4*(l/32) + r%4 and m = l%32, four runs of four
+// consecutive n per lane.  The epilogue stages one half of the tile (the
+// rows of the waves with wm == h) as fp32 [m][n] in LDS at a time.
+constexpr int kS32BK = 64;
+
+__host__ __device__ constexpr int s32_swz(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
+
+__host__ __device__ constexpr int vmcnt_wait_imm(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+template <int BM, int BN, int S>
+constexpr size_t s8_gemm32_lds() {
+  const size_t stages = (size_t)S * (BM + BN) * kS32BK;
+  const size_t half = (size_t)(BM / 2) * acc_pitch<BN>() * 4 + (size_t)(BM / 2) * 4;
+  return stages > half ? stages : half;
+}
+
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void s8_gemm32_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
+  constexpr int WTM = BM / 64, WTN = BN / 64;  // 32 x 32 tiles per wave
+  constexpr int STAGE = (BM + BN) * kS32BK;
+  constexpr int GROUPS = (BM + BN) / 16;        // 1 KB loads (16 rows) per stage
+  constexpr int LPW = GROUPS / 4;               // per wave
+  static_assert(GROUPS % 4 == 0 && S >= 2 && S <= 5 && (S - 2) * LPW <= 63, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const auto a_rs = make_rsrc(a.qx, (uint32_t)((int64_t)M * K));
+  const auto b_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+
+  // this lane's source in each of the wave's loads: row grp*16 + lane/4 of
+  // the [A | B] slab, logical chunk (lane % 4) ^ f(row)
+  const int lrow = lane >> 2;
+  const int lchunk = ((lane & 3) ^ s32_swz(lrow)) * 16;
+  uint32_t src[LPW];
+#pragma unroll
+  for (int q = 0; q < LPW; ++q) {
+    const int row = (wv * LPW + q) * 16 + lrow;
+    if (row < BM)
+      src[q] = m0 + row < M ? (uint32_t)((m0 + row) * K + lchunk) : kOobOffset;
+    else
+      src[q] = n0 + row - BM < N ? (uint32_t)((n0 + row - BM) * K + lchunk) : kOobOffset;
+  }
+  auto dma = [&](int step) {
+    const int k0 = step * kS32BK;
+    int8_t *stage = s8_smem + (step % S) * STAGE;
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+      // K % 16 == 0: a chunk lies wholly inside or past K
+      const uint32_t off = (src[q] == kOobOffset || k0 + lchunk >= K) ? kOobOffset : src[q] + k0;
+      lds_ptr_t dst = (lds_ptr_t)(stage + (wv * LPW + q) * 1024);
+      if ((wv * LPW + q) * 16 < BM)  // whole loads lie in A or in B
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, dst, 16, off, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, dst, 16, off, 0, 0, 0);
+    }
+  };
+
+  // fragments: row R (R % 32 == lane % 32), k block kb = 2*sub + lane/32
+  const int fsw = s32_swz(lane & 31);
+  const int a_base = (wm * (BM / 2) + (lane & 31)) * kS32BK;
+  const int b_base = (BM + wn * (BN / 2) + (lane & 31)) * kS32BK;
+  i32x16_t acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int nk = (K + kS32BK - 1) / kS32BK;
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p) dma(p);
+  for (int ks = 0; ks < nk; ++ks) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait_imm((S - 2) * LPW));
+    asm volatile("s_barrier" ::: "memory");
+    dma(ks + S - 1);
+    const int8_t *stage = s8_smem + (ks % S) * STAGE;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int pos = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
+      i32x4_t Af[WTM], Bf[WTN];
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+        Af[i] = *reinterpret_cast<const i32x4_t *>(stage + a_base + i * 32 * kS32BK + pos);
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        Bf[j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kS32BK + pos);
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Bf[j], Af[i], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // epilogue in two halves of BM/2 rows: the waves with wm == h stage
+  // their accumulators as [m][n], then all threads finish those rows
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_barrier" ::: "memory");
+  constexpr int AP = acc_pitch<BN>();
+  int32_t *tile = reinterpret_cast<int32_t *>(s8_smem);
+  float *sx_l = reinterpret_cast<float *>(tile + (BM / 2) * AP);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (wm == h) {
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<i32x4_t *>(
+                tile + (i * 32 + (lane & 31)) * AP + wn * (BN / 2) + j * 32 + 8 * q + 4 * (lane >> 5)) =
+                i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]};
+    }
+    s8_stage_row_scales<BM / 2>(a, sx_l, m0 + h * (BM / 2), tid);
+    __syncthreads();
+    s8_tile_epilogue<BM / 2, BN>(a, tile, sx_l, m0 + h * (BM / 2), n0, tid);
+    __syncthreads();
+  }
+}
+
+template <int BM, int BN, int S>
+hipError_t launch_s8_gemm32(const DynArgs &a, hipStream_t s) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  s8_gemm32_kernel<BM, BN, S><<<dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                                s8_gemm32_lds<BM, BN, S>(), s>>>(a, tiles_m, tiles_n, group_m);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int S>
 hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
@@ -1023,6 +1189,11 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
     const char *tile = std::getenv("ZT_S8_TILE");
     const bool big = tile ? tile[0] == '2' : t256 >= 128;
     const char *kind = std::getenv("ZT_S8_KIND");  // r: register staging, 2/3: DMA stages
+    if (!kind || kind[0] == 'n') {  // 32x32x32 kernel, S stages
+      const int st = kind && kind[1] ? kind[1] - '0' : 3;
+      if (st == 2) return big ? launch_s8_gemm32<256, 128, 2>(a, s) : launch_s8_gemm32<128, 128, 2>(a, s);
+      return big ? launch_s8_gemm32<256, 128, 3>(a, s) : launch_s8_gemm32<128, 128, 3>(a, s);
+    }
     if (kind && kind[0] == 'r')
       return big ? launch_s8_tiled<256, 128>(a, s) : launch_s8_tiled<128, 128>(a, s);
     if (kind && kind[0] == '3')
