@@ -98,6 +98,15 @@ def test_gemm_kernel_vs_oracle(M, K, N, G):
     run_case(M, K, N, G, kernel="gemm", seed=M + K, bias=True)
 
 
+# the 32x32 prefill kernel (bf16 scales, no zero points, N % 8 == 0):
+# 128 x 128 and 256 x 128 tiles, ragged M and N, group sizes 128 / 256 /
+# per-channel, more tiles than CUs
+@pytest.mark.parametrize("M,K,N,G", [(300, 1024, 200, 8), (520, 512, 264, 2),
+                                     (1100, 2048, 1032, 1), (2100, 768, 4104, 6)])
+def test_gemm32_kernel_vs_oracle(M, K, N, G):
+    run_case(M, K, N, G, kernel="gemm", seed=M + N, bias=True)
+
+
 @pytest.mark.parametrize("M,K,N,G", [(1, 32, 32, 1), (4, 64, 48, 1), (24, 128, 64, 2),
                                      (3, 72, 16, 9), (5, 256, 40, 2)])
 def test_generic_kernel_vs_oracle(M, K, N, G):

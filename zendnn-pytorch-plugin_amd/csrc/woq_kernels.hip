@@ -554,6 +554,42 @@ constexpr size_t woq_dma_lds() {
   return stages > tile ? stages : tile;
 }
 
+// Epilogue of ROWS x BN fp32 outputs staged in LDS (row pitch BN + 4) for
+// rows m0.. and columns n0..: bias, post-ops, then rows of four columns per
+// thread (8-byte bf16 stores where the row allows), 256 threads.
+template <int ROWS, int BN>
+__device__ __forceinline__ void woq_tile_epilogue(const WoqArgs &a, const float *tile, int m0,
+                                                  int n0, int tid) {
+  constexpr int TP = BN + 4;
+  const int M = (int)a.M, N = (int)a.N;
+  for (int idx = tid; idx < ROWS * (BN / 4); idx += 256) {
+    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c4;
+    if (m >= M || n >= N) continue;
+    const f32x4_t v4 = *reinterpret_cast<const f32x4_t *>(tile + row * TP + c4);
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = v4[r];
+      if (n + r < N) {
+        if (a.bias) v = v + load_elem(a.bias, a.b_dt, n + r);
+        v = apply_post_ops(v, a.post, m, n + r);
+      }
+      f[r] = v;
+    }
+    if (a.y_dt == ZT_DT_BF16 && n + 3 < N && (a.ldy & 3) == 0) {
+      u32x2_t pk;
+      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * a.ldy + n) = pk;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n + r, f[r]);
+    }
+  }
+}
+
 template <int BM, int BN, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void woq_gemm_dma_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg_shift,
@@ -688,32 +724,187 @@ void woq_gemm_dma_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int c
       for (int r = 0; r < 4; ++r)
         tile[(wm * (BM / 2) + i * 16 + 4 * lg + r) * TP + wn * (BN / 2) + j * 16 + lr] = acc[i][j][r];
   __syncthreads();
-  for (int idx = tid; idx < BM * (BN / 4); idx += 256) {
-    const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
-    const int m = m0 + row, n = n0 + c4;
-    if (m >= M || n >= N) continue;
-    const f32x4_t v4 = *reinterpret_cast<const f32x4_t *>(tile + row * TP + c4);
-    float f[4];
+  woq_tile_epilogue<BM, BN>(a, tile, m0, n0, tid);
+}
+
+// Prefill int4 GEMM on v_mfma_f32_32x32x16_bf16 (signed int4, bf16 scales):
+// BM x BN tiles, 4 waves of (BM/2) x (BN/2), K in steps of 64, two stages
+// moved straight into LDS by the buffer unit: the x slab [BM][64] bf16 (128 B
+// rows, 16-byte chunk c of row r at position c ^ ((r ^ (r >> 3)) & 7)), the
+// int4 slab [BN][64] (32 B rows, 16-byte half h of row r at h ^ ((r >> 3) &
+// 1)) and the step's scale row [BN] bf16.  Both swizzles give the 16 rows one
+// fragment read touches 16 distinct 16-byte bank groups.  Two workgroups per
+// CU (at most 256 registers and 80 KB of LDS each) overlap one another's
+// barriers and epilogues.
+//
+// k order: the MFMA pairs A and B by k position, so any permutation shared
+// by both operands leaves the sums unchanged (bit for bit: each MFMA adds
+// the same 16 products).  Sub-step s of a step takes, for lane half h, the
+// eight k of word 4h + s of each 32-byte weight row, which lets a lane read
+// its four weight words of the step in one 16-byte LDS read; its x fragment
+// is chunk 4h + s of the row.
+//
+// A = dequantised W (exactly bf16_rne of the reference's fp32 dequantised
+// weight), B = x, so D is [n][m]: register r of lane l holds
+// n = 8*(r/4) + 4*(l/32) + r%4 and m = l%32.  The epilogue stages one half of
+// the tile (the rows of the waves with wm == h) as fp32 [m][n] at a time.
+constexpr int kW32BK = 64;
+
+template <int BM, int BN>
+constexpr size_t woq_gemm32_stage() {
+  return (size_t)BM * 128 + (size_t)BN * 32 + 1024;
+}
+template <int BM, int BN>
+constexpr size_t woq_gemm32_lds() {
+  const size_t stages = 2 * woq_gemm32_stage<BM, BN>();
+  const size_t half = (size_t)(BM / 2) * (BN + 4) * 4;
+  return stages > half ? stages : half;
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void woq_gemm32_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg_shift,
+                       int gmask) {
+  constexpr int WTM = BM / 64, WTN = BN / 64;  // 32 x 32 tiles per wave
+  constexpr int STAGE = (int)woq_gemm32_stage<BM, BN>();
+  constexpr int XI = BM / 8;                    // 1 KB x loads (8 rows) per stage
+  constexpr int WI = BN / 32;                   // 1 KB weight loads (32 rows)
+  constexpr int LOADS = XI + WI + 1;            // + the scale row
+  constexpr int LPW = (LOADS + 3) / 4;
+  static_assert(BN <= 512 && BN % 64 == 0 && BM % 64 == 0, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+  const int hl = lane >> 5, l32 = lane & 31;
+
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int ldx2 = (int)a.ldx * 2, KB = K / 2;
+
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)M * ldx2));
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KB));
+  const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
+
+  // the wave's loads: index li = wv * LPW + q; x loads first, then the
+  // weight loads, then the scale row (lanes 0..BN/8-1, 16 bytes each)
+  auto dma = [&](int step) {
+    const int k0 = step * kW32BK;
+    const bool in = k0 < K;
+    unsigned char *stage = smem + (step & 1) * STAGE;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = v4[r];
-      if (n + r < N) {
-        if (a.bias) v = v + load_elem(a.bias, a.b_dt, n + r);
-        v = apply_post_ops(v, a.post, m, n + r);
+    for (int q = 0; q < LPW; ++q) {
+      const int li = wv * LPW + q;
+      if (li >= LOADS) break;
+      uint32_t off;
+      if (li < XI) {
+        const int row = li * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+        off = in && m0 + row < M ? (uint32_t)((m0 + row) * ldx2 + k0 * 2 + chunk * 16) : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(stage + li * 1024), 16, off, 0, 0, 0);
+      } else if (li < XI + WI) {
+        const int wi = li - XI;
+        const int row = wi * 32 + (lane >> 1);
+        const int half = (lane & 1) ^ ((row >> 3) & 1);
+        off = in && n0 + row < N ? (uint32_t)((n0 + row) * KB + k0 / 2 + half * 16) : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (lds_ptr_t)(stage + BM * 128 + wi * 1024), 16,
+                                                 off, 0, 0, 0);
+      } else {
+        // N % 8 == 0 (host-checked): a lane's 8 scales lie wholly inside or past N
+        const uint32_t grp = (uint32_t)(((k0 >> 7) >> cpg_shift) & gmask);
+        off = in && lane < BN / 8 && n0 + 8 * lane < N
+                  ? (grp * (uint32_t)N + (uint32_t)(n0 + 8 * lane)) * 2u
+                  : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rs, (lds_ptr_t)(stage + BM * 128 + BN * 32), 16,
+                                                 off, 0, 0, 0);
       }
-      f[r] = v;
     }
-    if (a.y_dt == ZT_DT_BF16 && n + 3 < N && (a.ldy & 3) == 0) {
-      u32x2_t pk;
-      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
-      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * a.ldy + n) = pk;
-    } else {
+  };
+
+  f32x16_t acc[WTM][WTN];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (n + r < N) store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n + r, f[r]);
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = K / kW32BK;
+  dma(0);
+  for (int ks = 0; ks < nk; ++ks) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of step ks
+    asm volatile("s_barrier" ::: "memory");
+    dma(ks + 1);  // past the last step: zeros into the buffer step ks - 1 used
+    const unsigned char *stage = smem + (ks & 1) * STAGE;
+    // weight words 4h..4h+3 of rows wn*BN/2 + 32j + l32, and their scales
+    u32x4_t wq[WTN];
+    float sc[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const int row = wn * (BN / 2) + j * 32 + l32;
+      wq[j] = *reinterpret_cast<const u32x4_t *>(stage + BM * 128 + row * 32 +
+                                                 ((hl ^ ((row >> 3) & 1)) * 16));
+      sc[j] = bf16_bits_to_f32(
+          *reinterpret_cast<const uint16_t *>(stage + BM * 128 + BN * 32 + row * 2));
+    }
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      const int chunk = 4 * hl + sub;
+      bf16x8_t xb[WTM];
+#pragma unroll
+      for (int i = 0; i < WTM; ++i) {
+        const int row = wm * (BM / 2) + i * 32 + l32;
+        xb[i] = *reinterpret_cast<const bf16x8_t *>(stage + row * 128 +
+                                                    ((chunk ^ ((row ^ (row >> 3)) & 7)) * 16));
+      }
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        const bf16x8_t wb = dq_word<kDecFast>(wq[j][sub], sc[j], 0.f, 0);
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb, xb[i], acc[i][j], 0, 0, 0);
+      }
     }
   }
+
+  // epilogue in two halves of BM/2 rows
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_barrier" ::: "memory");
+  constexpr int TP = BN + 4;
+  float *tile = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (wm == h) {
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4_t *>(tile + (i * 32 + l32) * TP + wn * (BN / 2) + j * 32 + 8 * q +
+                                         4 * hl) =
+                f32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+    woq_tile_epilogue<BM / 2, BN>(a, tile, m0 + h * (BM / 2), n0, tid);
+    __syncthreads();
+  }
+}
+
+template <int BM, int BN>
+static hipError_t launch_woq_gemm32_t(const WoqArgs &a, hipStream_t s, int shift, int gmask) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  woq_gemm32_kernel<BM, BN><<<dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                              woq_gemm32_lds<BM, BN>(), s>>>(a, tiles_m, tiles_n, group_m, shift, gmask);
+  return hipGetLastError();
 }
 
 template <int BM, int BN>
@@ -1172,6 +1363,14 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
       const int gmask = a.G == 1 ? 0 : 0x7fffffff;
       const int mode = a.s_dt == ZT_DT_F32 ? kDecGenF32 : (a.zp ? kDecGenBf16 : kDecFast);
       const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
+      // the 32x32 kernel: fast mode, K in 64-steps, scale rows of whole
+      // 16-byte pieces
+      if (mode == kDecFast && a.N % 8 == 0 && !(e && e[0] == 'd') &&
+          (int64_t)a.G * a.N * 2 < (int64_t)kOobOffset) {
+        const bool big32 = e ? e[0] != '1' : t256 >= 128;
+        return big32 ? launch_woq_gemm32_t<256, 128>(a, s, shift, gmask)
+                     : launch_woq_gemm32_t<128, 128>(a, s, shift, gmask);
+      }
       // 256 x 128 only for the fast mode: the general dequant spills there
       const bool big = mode == kDecFast && (e ? e[0] == '2' : t256 >= 128);
       return big ? launch_woq_dma_t<256, 128>(a, s, shift, gmask, mode)
