@@ -56,14 +56,21 @@ def check_close(y_gpu, y_ref, **tol):
 
 
 def run_case(M, K, N, G, kernel=None, seed=0, post=(), nbuf=0, **kw):
-    if kernel:
-        os.environ["ZT_WOQ_FORCE_KERNEL"] = kernel
+    """kernel: force one kernel for this call only (None: the library's choice)."""
     x, q, wp, s, z, b = make_case(M, K, N, G, seed, **kw)
     g = torch.Generator().manual_seed(seed + 1)
     bufs = [torch.randn(M, N, generator=g).to(x.dtype) for _ in range(nbuf)]
     y_ref = O.woq_linear(x, wp, s, zero_points=z, bias=b, post_ops=post, post_bufs=bufs)
     xd, wd, sd, zd, bd = gpu(x, wp, s, z, b)
-    y = C.woq_linear(xd, wd, sd, zd, bd, post_ops=post, post_bufs=gpu(*bufs))
+    saved = os.environ.pop("ZT_WOQ_FORCE_KERNEL", None)
+    if kernel:
+        os.environ["ZT_WOQ_FORCE_KERNEL"] = kernel
+    try:
+        y = C.woq_linear(xd, wd, sd, zd, bd, post_ops=post, post_bufs=gpu(*bufs))
+    finally:
+        os.environ.pop("ZT_WOQ_FORCE_KERNEL", None)
+        if saved is not None:
+            os.environ["ZT_WOQ_FORCE_KERNEL"] = saved
     check_close(y, y_ref)
     return y, y_ref
 
@@ -96,6 +103,37 @@ def test_post_ops_all_kernels(post, nbuf, kernel, M):
                                      (256, 1024, 256, 8), (2048, 256, 128, 2)])
 def test_gemm_kernel_vs_oracle(M, K, N, G):
     run_case(M, K, N, G, kernel="gemm", seed=M + K, bias=True)
+
+
+# the wide decode kernel (17..64 rows, bf16 scales, no zero points,
+# K % 512 == 0, N % 4 == 0): one or two 32-token tiles, K split over several
+# workgroups (partials + reduce) or not (epilogue in the kernel), ragged N,
+# group 128 / 256 / per-channel
+@pytest.mark.parametrize("M", [17, 24, 32, 33, 48, 64])
+@pytest.mark.parametrize("K,N,G", [(4096, 1000, 32), (2048, 200, 8), (1024, 2052, 1),
+                                   (14336, 384, 112)])
+def test_wide_kernel_vs_oracle(M, K, N, G):
+    run_case(M, K, N, G, kernel="wide", seed=M + K + N, bias=(M % 2 == 1))
+
+
+@pytest.mark.parametrize("splits", ["1", "2", "4"])
+@pytest.mark.parametrize("post,nbuf", [(("gelu_tanh",), 0), (("mul", "add"), 2),
+                                       (("silu", "mul"), 1)])
+def test_wide_kernel_post_ops_and_splits(splits, post, nbuf, monkeypatch):
+    monkeypatch.setenv("ZT_WOQ_WIDE", splits)
+    run_case(40, 2048, 264, 16, kernel="wide", post=post, nbuf=nbuf, seed=21, bias=True)
+
+
+def test_wide_kernel_strided_x():
+    M, K, N, G = 48, 4096, 512, 32
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=77)
+    xs = torch.randn(M, K + 64).bfloat16()
+    xs[:, :K] = x
+    y_ref = O.woq_linear(x, wp, s)
+    xd = xs.to(DEV)[:, :K]
+    assert xd.stride(0) == K + 64
+    y = C.woq_linear(xd, wp.to(DEV), s.to(DEV))
+    check_close(y, y_ref)
 
 
 # the 32x32 prefill kernel (bf16 scales, no zero points, N % 8 == 0):

@@ -208,16 +208,19 @@ int32_t zt_version(void) { return 100; }
 size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
                                     int64_t G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0 || K % G) return 0;
+  // the wide kernel's K-split partials (17..64 rows)
+  zt::WidePlan wp;
+  const size_t wide = zt::woq_wide_plan(M, N, K, G, &wp) ? zt::woq_wide_workspace(wp, M, N) : 0;
   zt::WoqArgs a{};
   a.x_dt = ZT_DT_BF16;
   a.M = M, a.K = K, a.N = N, a.G = G, a.ldx = K;
   // Assume aligned pointers: the workspace a call needs is never larger.
   a.x = reinterpret_cast<const void *>(256);
   a.w = reinterpret_cast<const uint32_t *>(256);
-  if (zt::woq_select_kernel(a) != zt::kWoqDecode) return 0;
+  if (zt::woq_select_kernel(a) != zt::kWoqDecode) return wide;
   zt::DecodePlan p;
-  if (!zt::woq_decode_plan(M, N, K, &p)) return 0;
-  return zt::woq_decode_workspace(p, M, N);
+  if (!zt::woq_decode_plan(M, N, K, &p)) return wide;
+  return std::max(wide, zt::woq_decode_workspace(p, M, N));
 }
 
 int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
@@ -259,6 +262,14 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   if (rc) return rc;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  zt::WidePlan wp;
+  if (zt::woq_wide_ok(a, &wp)) {
+    const size_t need = zt::woq_wide_workspace(wp, M, N);
+    if (need && (!workspace || workspace_bytes < need))
+      return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need,
+                  workspace ? workspace_bytes : (size_t)0);
+    return hip_status(zt::launch_woq_wide(a, wp, workspace, s), op);
+  }
   if (woq_use_row_blocks(a)) {
     // one stream-kernel launch over all rows when x (in K phases) fits, else
     // blocks of 16 rows

@@ -1297,6 +1297,270 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   return false;
 }
 
+// ------------------------------------------------ wide decode (17..64 rows)
+// Weight streaming for 17..64 tokens, where re-reading x per 16-row weight
+// tile (the stream kernel) moves up to 16 bytes of x per byte of int4.  A
+// workgroup owns 128 weight rows (4 waves x 32) over one K split and keeps
+// x [32*MT][512] of the current K phase in LDS, shared by its waves, so x
+// costs at most 4*M/128 bytes per weight byte.
+//
+// A wave loads its 32 rows as two 16-row x 64-byte tiles per 128-k chunk
+// (16 rows x 64 B per instruction, straight from HBM to registers, two
+// phases ahead) and turns each pair into the 32-row A operands of
+// v_mfma_f32_32x32x16_bf16 with one v_permlane16_swap per dword: lanes 0-31
+// then hold bytes [0, 16) and [16, 32) of rows 0-31, lanes 32-63 bytes
+// [32, 48) and [48, 64), so MFMA q of the chunk takes k block 8*(l/32) + q
+// (8 k each) in both operands.  B is x from LDS: 1 KB rows, 16-byte chunk c
+// of token row t at position c ^ (t & 15) (16 distinct bank groups for the
+// 16 rows one read pass touches).  Dequantisation is the decode kernels'
+// (bf16_rne of the exact fp32 product).
+//
+// D is [n][token]: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4
+// of the wave's 32 and token 32*j + l%32.  With one K split the workgroup
+// applies the epilogue; with several it writes fp32 partials
+// [split][M][N], which woq_splitk_reduce_kernel adds in split order.
+__host__ __device__ constexpr int vmcnt_imm_woq(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+constexpr int kWideKP = 512;    // k per phase
+constexpr int kWideRows = 128;  // weight rows per workgroup
+
+template <int MT>
+constexpr size_t woq_wide_lds() {
+  const size_t x = 2 * (size_t)(32 * MT) * 1024;
+  const size_t tile = (size_t)(32 * MT) * (kWideRows + 4) * 4;
+  return x > tile ? x : tile;
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int cpg_shift, int gmask,
+                                                       float *partial) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int XB = 32 * MT * 1024;  // one x phase buffer
+  constexpr int XL = 8 * MT;          // x rows (one load each) per wave per phase
+  constexpr int WAIT = vmcnt_imm_woq(12);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4, l32 = lane & 31, hl = lane >> 5;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
+  const int ldx2 = (int)a.ldx * 2;
+  const int n0 = blockIdx.x * kWideRows;
+  const int ph0 = blockIdx.y * pps;  // first phase of this K split
+
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * ldx2 + (int64_t)K * 2));
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
+
+  // the lane's two load rows and its A-operand row after the swap (rows
+  // past N read zeros / a clamped scale; their outputs are never stored)
+  const int r_lo = n0 + wv * 32 + lr, r_hi = r_lo + 16;
+  const bool ok_lo = r_lo < N, ok_hi = r_hi < N;
+  const uint32_t off_lo = (uint32_t)r_lo * (uint32_t)KW * 4u + 16u * lg;
+  const uint32_t off_hi = (uint32_t)r_hi * (uint32_t)KW * 4u + 16u * lg;
+  const uint32_t srow = (uint32_t)min(n0 + wv * 32 + l32, N - 1);
+
+  u32x4_t wq[3][4][2];
+  uint32_t sq[3][4];
+  // Phases past the split (or past K) load zeros so every phase issues the
+  // same number of loads.  The out-of-range bit is ORed into the offsets
+  // (valid offsets stay below it): a select on the wave-uniform condition
+  // would be compiled into branches around each load.
+  const uint32_t oob_lo = ok_lo ? 0u : kOobOffset, oob_hi = ok_hi ? 0u : kOobOffset;
+  auto load_w = [&](int set, int ph) {
+    const uint32_t oob = ph < ph0 + pps ? 0u : kOobOffset;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t kc = (uint32_t)(ph * 4 + c);
+      wq[set][c][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+          w_rs, (off_lo + kc * 64u) | oob_lo | oob, 0, 0));
+      wq[set][c][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+          w_rs, (off_hi + kc * 64u) | oob_hi | oob, 0, 0));
+      const uint32_t sidx = ((kc >> cpg_shift) & (uint32_t)gmask) * (uint32_t)N + srow;
+      sq[set][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, (sidx * 2u) | oob, 0, 0);
+    }
+  };
+  auto dma_x = [&](int ph) {
+    const uint32_t oob = ph < ph0 + pps ? 0u : kOobOffset;
+    unsigned char *buf = smem + (ph & 1) * XB;
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int t = wv + 4 * i;
+      const int c = lane ^ (t & 15);
+      const uint32_t off = (uint32_t)(t * ldx2 + ph * (kWideKP * 2) + c * 16) |
+                           (t < M ? 0u : kOobOffset) | oob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(buf + t * 1024), 16, off, 0, 0, 0);
+    }
+  };
+
+  f32x16_t acc[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+
+  auto compute = [&](int set, int ph) {
+    const unsigned char *buf = smem + (ph & 1) * XB;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4_t w0 = wq[set][c][0], w1 = wq[set][c][1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(w0[e], w1[e], false, false);
+        w0[e] = sw[0];
+        w1[e] = sw[1];
+      }
+      const float sc = __uint_as_float(sq[set][c] << 16);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const bf16x8_t wb = dq_word<kDecFast>(q < 4 ? w0[q] : w1[q - 4], sc, 0.f, 0);
+        const int cc = c * 16 + 8 * hl + q;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          const int t = 32 * j + l32;
+          const bf16x8_t xb =
+              *reinterpret_cast<const bf16x8_t *>(buf + t * 1024 + ((cc ^ (t & 15)) * 16));
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb, xb, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  };
+  // phase j: x(j) and W(j) landed once only the loads of W(j + 1) are
+  // outstanding (issued after x(j)); the barrier also means every wave is
+  // done with phase j - 1, whose x buffer the next DMA overwrites
+  auto phase = [&](int j, int set) {
+    __builtin_amdgcn_s_waitcnt(WAIT);
+    asm volatile("s_barrier" ::: "memory");
+    dma_x(ph0 + j + 1);
+    load_w((set + 2) % 3, ph0 + j + 2);
+    compute(set, ph0 + j);
+  };
+  dma_x(ph0);
+  load_w(0, ph0);
+  load_w(1, ph0 + 1);
+  for (int j = 0; j < pps; j += 3) {
+    phase(j, 0);
+    if (j + 1 < pps) phase(j + 1, 1);
+    if (j + 2 < pps) phase(j + 2, 2);
+  }
+
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_barrier" ::: "memory");
+  if (partial == nullptr) {
+    constexpr int TP = kWideRows + 4;
+    float *tile = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4_t *>(tile + (32 * j + l32) * TP + wv * 32 + 8 * q + 4 * hl) =
+            f32x4_t{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
+    __syncthreads();
+    woq_tile_epilogue<32 * MT, kWideRows>(a, tile, 0, n0, tid);
+    return;
+  }
+  float *pp = partial + (size_t)blockIdx.y * M * N;
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const int m = 32 * j + l32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + wv * 32 + 8 * q + 4 * hl;  // N % 4 == 0: n..n+3 all in or out
+      if (m < M && n < N)
+        *reinterpret_cast<f32x4_t *>(pp + (size_t)m * N + n) =
+            f32x4_t{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
+    }
+  }
+}
+
+// y = epilogue(sum over the splits of partial[split][m][n], in split order)
+__global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const float *partial,
+                                                                int splits) {
+  const int M = (int)a.M, N = (int)a.N;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * (N / 4)) return;
+  const int m = (int)(idx / (N / 4)), n = (int)(idx % (N / 4)) * 4;
+  f32x4_t v = *reinterpret_cast<const f32x4_t *>(partial + (size_t)m * N + n);
+  for (int s = 1; s < splits; ++s)
+    v += *reinterpret_cast<const f32x4_t *>(partial + ((size_t)s * M + m) * N + n);
+  float f[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float t = v[r];
+    if (a.bias) t = t + load_elem(a.bias, a.b_dt, n + r);
+    f[r] = apply_post_ops(t, a.post, m, n + r);
+  }
+  if (a.y_dt == ZT_DT_BF16 && (a.ldy & 3) == 0) {
+    u32x2_t pk;
+    pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+    pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+    *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * a.ldy + n) = pk;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n + r, f[r]);
+  }
+}
+
+bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
+  const char *e = std::getenv("ZT_WOQ_WIDE");  // "0" disables; "KS" forces the split count
+  if (e && e[0] == '0') return false;
+  if (M < 17 || M > 64 || N < 4 || N % 4 || K % kWideKP || G <= 0 || K % G) return false;
+  const int64_t gs = K / G, cpg = gs / 128;
+  if (G != 1 && (gs % 128 || (cpg & (cpg - 1)))) return false;
+  const int phases = (int)(K / kWideKP);
+  const int64_t blocks = (N + kWideRows - 1) / kWideRows;
+  int ks = 1;
+  // the most K splits (a divisor of the phase count) that keep the grid
+  // within about 1.25 rounds of 256 CUs
+  for (int d = 1; d <= phases; ++d)
+    if (phases % d == 0 && blocks * d <= 320) ks = d;
+  if (e) {
+    const int f = std::atoi(e);
+    if (f >= 1 && phases % f == 0) ks = f;
+  }
+  p->mt = M <= 32 ? 1 : 2;
+  p->splits = ks;
+  p->pps = phases / ks;
+  return true;
+}
+
+size_t woq_wide_workspace(const WidePlan &p, int64_t M, int64_t N) {
+  return p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+bool woq_wide_ok(const WoqArgs &a, WidePlan *p) {
+  const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");  // another forced kernel skips this one
+  if (f && std::strcmp(f, "wide")) return false;
+  if (!woq_wide_plan(a.M, a.N, a.K, a.G, p)) return false;
+  return a.x_dt == ZT_DT_BF16 && a.s_dt == ZT_DT_BF16 && !a.zp && a.ldx % 8 == 0 &&
+         aligned16(a.x) && aligned16(a.w) &&
+         (a.M - 1) * a.ldx * 2 + a.K * 2 < (int64_t)kOobOffset &&
+         a.N * (a.K / 2) < (int64_t)kOobOffset && a.G * a.N * 2 < (int64_t)kOobOffset;
+}
+
+hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace, hipStream_t s) {
+  const int64_t cpg = a.G == 1 ? 0 : (a.K / a.G) / 128;
+  int shift = 0;
+  while (cpg > 1 && (1 << shift) < cpg) ++shift;
+  const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  float *partial = p.splits > 1 ? static_cast<float *>(workspace) : nullptr;
+  if (p.splits > 1 && !partial) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.N + kWideRows - 1) / kWideRows), (unsigned)p.splits);
+  if (std::getenv("ZT_WOQ_DEBUG"))
+    std::fprintf(stderr, "[zt] woq wide M=%lld N=%lld K=%lld: MT=%d splits=%d phases/split=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, p.mt, p.splits, p.pps);
+  if (p.mt == 1)
+    woq_wide_kernel<1><<<grid, dim3(256), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial);
+  else
+    woq_wide_kernel<2><<<grid, dim3(256), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || p.splits == 1) return err;
+  const int64_t n4 = a.M * (a.N / 4);
+  woq_splitk_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(a, partial,
+                                                                                   p.splits);
+  return hipGetLastError();
+}
+
 // The stream kernel for a call of up to 64 rows whose shape the decode
 // kernels accept (capi.hip tries it before splitting 33..64 rows into
 // blocks of 16).

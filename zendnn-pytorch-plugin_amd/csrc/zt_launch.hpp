@@ -54,6 +54,18 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s);
 // The weight-streaming decode kernel for up to 64 rows, when it applies
 // (returns false otherwise; *err holds the launch status when it does).
 bool woq_try_stream(const WoqArgs &a, hipStream_t s, hipError_t *err);
+// 17..64 rows: the wide weight-streaming kernel (bf16 x and scales, no
+// zero points), K split over `splits` workgroups per row block whose fp32
+// partials take woq_wide_workspace bytes of workspace.
+struct WidePlan {
+  int mt;      // 32-token tiles (1 or 2)
+  int splits;  // K splits
+  int pps;     // 512-k phases per split
+};
+bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p);
+size_t woq_wide_workspace(const WidePlan &p, int64_t M, int64_t N);
+bool woq_wide_ok(const WoqArgs &a, WidePlan *p);
+hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace, hipStream_t s);
 
 hipError_t launch_repack(const int8_t *w, int64_t N, int64_t K, int32_t *out,
                          hipStream_t s);
