@@ -1300,9 +1300,12 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
 // ------------------------------------------------ wide decode (17..64 rows)
 // Weight streaming for 17..64 tokens, where re-reading x per 16-row weight
 // tile (the stream kernel) moves up to 16 bytes of x per byte of int4.  A
-// workgroup owns 128 weight rows (4 waves x 32) over one K split and keeps
-// x [32*MT][512] of the current K phase in LDS, shared by its waves, so x
-// costs at most 4*M/128 bytes per weight byte.
+// workgroup owns 128 weight rows over one K split and keeps x [32*MT][512]
+// of the current K phase in LDS, shared by its waves, so x costs at most
+// 4*M/128 bytes per weight byte.  Its 8 waves form 4 row groups of 32; the
+// two waves of a group take alternate chunk pairs of each phase (two waves
+// per SIMD, so one wave's dequantisation overlaps the other's MFMAs) and
+// add their halves in LDS at the end.
 //
 // A wave loads its 32 rows as two 16-row x 64-byte tiles per 128-k chunk
 // (16 rows x 64 B per instruction, straight from HBM to registers, two
@@ -1334,14 +1337,16 @@ constexpr size_t woq_wide_lds() {
 }
 
 template <int MT>
-__global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int cpg_shift, int gmask,
+__global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int cpg_shift, int gmask,
                                                        float *partial) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int XB = 32 * MT * 1024;  // one x phase buffer
-  constexpr int XL = 8 * MT;          // x rows (one load each) per wave per phase
-  constexpr int WAIT = vmcnt_imm_woq(12);
+  constexpr int XL = 4 * MT;          // x rows (one load each) per wave per phase
+  constexpr int WL = 6;  // weight + scale loads per wave per phase
+  constexpr int WAIT = vmcnt_imm_woq(WL);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rw = wv & 3, kh = wv >> 2;  // row group; chunk pair {2kh, 2kh+1} of each phase
   const int lr = lane & 15, lg = lane >> 4, l32 = lane & 31, hl = lane >> 5;
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
   const int ldx2 = (int)a.ldx * 2;
@@ -1354,24 +1359,23 @@ __global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int c
 
   // the lane's two load rows and its A-operand row after the swap (rows
   // past N read zeros / a clamped scale; their outputs are never stored)
-  const int r_lo = n0 + wv * 32 + lr, r_hi = r_lo + 16;
-  const bool ok_lo = r_lo < N, ok_hi = r_hi < N;
+  const int r_lo = n0 + rw * 32 + lr, r_hi = r_lo + 16;
   const uint32_t off_lo = (uint32_t)r_lo * (uint32_t)KW * 4u + 16u * lg;
   const uint32_t off_hi = (uint32_t)r_hi * (uint32_t)KW * 4u + 16u * lg;
-  const uint32_t srow = (uint32_t)min(n0 + wv * 32 + l32, N - 1);
+  const uint32_t srow = (uint32_t)min(n0 + rw * 32 + l32, N - 1);
 
-  u32x4_t wq[3][4][2];
-  uint32_t sq[3][4];
+  u32x4_t wq[3][2][2];
+  uint32_t sq[3][2];
   // Phases past the split (or past K) load zeros so every phase issues the
   // same number of loads.  The out-of-range bit is ORed into the offsets
   // (valid offsets stay below it): a select on the wave-uniform condition
   // would be compiled into branches around each load.
-  const uint32_t oob_lo = ok_lo ? 0u : kOobOffset, oob_hi = ok_hi ? 0u : kOobOffset;
+  const uint32_t oob_lo = r_lo < N ? 0u : kOobOffset, oob_hi = r_hi < N ? 0u : kOobOffset;
   auto load_w = [&](int set, int ph) {
     const uint32_t oob = ph < ph0 + pps ? 0u : kOobOffset;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t kc = (uint32_t)(ph * 4 + c);
+    for (int c = 0; c < 2; ++c) {
+      const uint32_t kc = (uint32_t)(ph * 4 + 2 * kh + c);
       wq[set][c][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
           w_rs, (off_lo + kc * 64u) | oob_lo | oob, 0, 0));
       wq[set][c][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
@@ -1385,7 +1389,7 @@ __global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int c
     unsigned char *buf = smem + (ph & 1) * XB;
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      const int t = wv + 4 * i;
+      const int t = wv + 8 * i;
       const int c = lane ^ (t & 15);
       const uint32_t off = (uint32_t)(t * ldx2 + ph * (kWideKP * 2) + c * 16) |
                            (t < M ? 0u : kOobOffset) | oob;
@@ -1402,7 +1406,7 @@ __global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int c
   auto compute = [&](int set, int ph) {
     const unsigned char *buf = smem + (ph & 1) * XB;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 2; ++c) {
       u32x4_t w0 = wq[set][c][0], w1 = wq[set][c][1];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -1414,7 +1418,7 @@ __global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int c
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const bf16x8_t wb = dq_word<kDecFast>(q < 4 ? w0[q] : w1[q - 4], sc, 0.f, 0);
-        const int cc = c * 16 + 8 * hl + q;
+        const int cc = (2 * kh + c) * 16 + 8 * hl + q;
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
           const int t = 32 * j + l32;
@@ -1444,28 +1448,43 @@ __global__ __launch_bounds__(256) void woq_wide_kernel(WoqArgs a, int pps, int c
     if (j + 2 < pps) phase(j + 2, 2);
   }
 
+  // the two chunk halves meet in LDS: waves kh = 1 store, kh = 0 add
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("s_barrier" ::: "memory");
+  f32x16_t *red = reinterpret_cast<f32x16_t *>(smem) + (rw * MT) * 64 + lane;
+  if (kh == 1) {
+#pragma unroll
+    for (int j = 0; j < MT; ++j) red[j * 64] = acc[j];
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[j] += red[j * 64];
+  }
+  __syncthreads();
   if (partial == nullptr) {
     constexpr int TP = kWideRows + 4;
     float *tile = reinterpret_cast<float *>(smem);
+    if (kh == 0) {
 #pragma unroll
-    for (int j = 0; j < MT; ++j)
+      for (int j = 0; j < MT; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<f32x4_t *>(tile + (32 * j + l32) * TP + wv * 32 + 8 * q + 4 * hl) =
-            f32x4_t{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4_t *>(tile + (32 * j + l32) * TP + rw * 32 + 8 * q + 4 * hl) =
+              f32x4_t{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
+    }
     __syncthreads();
-    woq_tile_epilogue<32 * MT, kWideRows>(a, tile, 0, n0, tid);
+    if (tid < 256) woq_tile_epilogue<32 * MT, kWideRows>(a, tile, 0, n0, tid);
     return;
   }
+  if (kh != 0) return;
   float *pp = partial + (size_t)blockIdx.y * M * N;
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
     const int m = 32 * j + l32;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = n0 + wv * 32 + 8 * q + 4 * hl;  // N % 4 == 0: n..n+3 all in or out
+      const int n = n0 + rw * 32 + 8 * q + 4 * hl;  // N % 4 == 0: n..n+3 all in or out
       if (m < M && n < N)
         *reinterpret_cast<f32x4_t *>(pp + (size_t)m * N + n) =
             f32x4_t{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
@@ -1505,6 +1524,11 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   const char *e = std::getenv("ZT_WOQ_WIDE");  // "0" disables; "KS" forces the split count
   if (e && e[0] == '0') return false;
   if (M < 17 || M > 64 || N < 4 || N % 4 || K % kWideKP || G <= 0 || K % G) return false;
+  // up to 32 rows of a matrix of at most 4096 x 4096 the stream kernel is
+  // faster (measured: the split-K reduce launch outweighs the x savings)
+  const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");
+  const bool forced = e || (f && !std::strcmp(f, "wide"));
+  if (M <= 32 && N * K <= (int64_t)4096 * 4096 && !forced) return false;
   const int64_t gs = K / G, cpg = gs / 128;
   if (G != 1 && (gs % 128 || (cpg & (cpg - 1)))) return false;
   const int phases = (int)(K / kWideKP);
@@ -1550,9 +1574,9 @@ hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace,
     std::fprintf(stderr, "[zt] woq wide M=%lld N=%lld K=%lld: MT=%d splits=%d phases/split=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, p.mt, p.splits, p.pps);
   if (p.mt == 1)
-    woq_wide_kernel<1><<<grid, dim3(256), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial);
+    woq_wide_kernel<1><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial);
   else
-    woq_wide_kernel<2><<<grid, dim3(256), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial);
+    woq_wide_kernel<2><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const int64_t n4 = a.M * (a.N / 4);
