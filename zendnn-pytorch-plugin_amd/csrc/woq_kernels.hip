@@ -446,8 +446,12 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   }
 
   // 3. copy x by loads when the DMA does not apply (P == 1 only), and wait
-  //    for it either way (the barrier's fence waits for this wave's x DMA
-  //    and the weight loads issued after it; they are needed next anyway)
+  //    for it.  With the DMA and the fast mode a wave issued exactly
+  //    2*TPW*CPW weight and scale loads after its x, so waiting until at
+  //    most that many are outstanding (then a bare barrier) leaves the
+  //    weights in flight: each chunk is dequantised as its own weights land
+  //    instead of after all of them (__syncthreads' fence waits for every
+  //    load).  Otherwise the barrier's fence waits for x and the weights.
   if (!x_dma) {
     const uint16_t *xp = reinterpret_cast<const uint16_t *>(a.x);
     const int per_row = K / 8;
@@ -457,7 +461,13 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
           *reinterpret_cast<const u32x4_t *>(xp + (int64_t)m * a.ldx + k8 * 8);
     }
   }
-  __syncthreads();
+  if (P == 1 && MODE == kDecFast && x_dma) {
+    constexpr int after = 2 * TPW * CPW > 63 ? 63 : 2 * TPW * CPW;
+    __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("s_barrier" ::: "memory");
+  } else {
+    __syncthreads();
+  }
 
   // 4. the slice's MFMAs; between phases every wave finishes with the
   //    range in LDS before the next one is loaded over it.  A chunk's
