@@ -1533,11 +1533,12 @@ __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const
 bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   const char *e = std::getenv("ZT_WOQ_WIDE");  // "0" disables; "KS" forces the split count
   if (e && e[0] == '0') return false;
-  if (M < 17 || M > 64 || N < 4 || N % 4 || K % kWideKP || G <= 0 || K % G) return false;
+  if (M < 1 || M > 64 || N < 4 || N % 4 || K % kWideKP || G <= 0 || K % G) return false;
   // up to 32 rows of a matrix of at most 4096 x 4096 the stream kernel is
   // faster (measured: the split-K reduce launch outweighs the x savings)
   const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");
   const bool forced = e || (f && !std::strcmp(f, "wide"));
+  if (M < 8 && !forced) return false;
   if (M <= 32 && N * K <= (int64_t)4096 * 4096 && !forced) return false;
   const int64_t gs = K / G, cpg = gs / 128;
   if (G != 1 && (gs % 128 || (cpg & (cpg - 1)))) return false;
@@ -1552,6 +1553,10 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
     const int f = std::atoi(e);
     if (f >= 1 && phases % f == 0) ks = f;
   }
+  // 8..16 rows: only without a K split (measured: gate_up 28672 x 4096 at
+  // M = 8 / 16 takes 22.4 / 23.4 us here against 26.8 / 29.5 on the stream
+  // kernel, while the split shapes lose the reduce launch)
+  if (M < 17 && ks > 1 && !forced) return false;
   p->mt = M <= 32 ? 1 : 2;
   p->splits = ks;
   p->pps = phases / ks;
