@@ -497,12 +497,14 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int row = mt * 16 + lr;
+        // token columns past M repeat row M-1: their sums are never
+        // stored, and an unconditional read keeps the loop free of exec
+        // branches and of the zero fills they need
+        const int row = min(mt * 16 + lr, M - 1);
         u32x4_t xb[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          xb[i] = row < M ? *reinterpret_cast<const u32x4_t *>(xl + row * XP + kcl * 128 + 32 * lg + 8 * i)
-                          : u32x4_t{0u, 0u, 0u, 0u};
+          xb[i] = *reinterpret_cast<const u32x4_t *>(xl + row * XP + kcl * 128 + 32 * lg + 8 * i);
 #pragma unroll
         for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -1281,7 +1283,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     *err = launch_stream_t<8, CPW_, 1, P_, MT_>(a, s, shift, gmask, mode);      \
     return true;                                                                \
   }
-      ZT_STREAM_PCASE(16, 2, 1) ZT_STREAM_PCASE(16, 4, 1)
+      ZT_STREAM_PCASE(14, 2, 1) ZT_STREAM_PCASE(16, 2, 1) ZT_STREAM_PCASE(16, 4, 1)
       ZT_STREAM_PCASE(4, 1, 2) ZT_STREAM_PCASE(4, 2, 2) ZT_STREAM_PCASE(16, 4, 2)
       ZT_STREAM_PCASE(4, 1, 4) ZT_STREAM_PCASE(4, 4, 4) ZT_STREAM_PCASE(8, 8, 4)
 #undef ZT_STREAM_PCASE
@@ -1290,7 +1292,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   }
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
-    for (int c : {2, 4, 8, 12, 16})
+    for (int c : {2, 4, 8, 12, 14, 16})
       if (c >= need) { cpw = c; break; }
   if (cpw < need) return false;
   if (std::getenv("ZT_WOQ_DEBUG"))
@@ -1300,7 +1302,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   if (nw == NW_ && cpw == CPW_ && tpw == TPW_) { *err = launch_stream_t<NW_, CPW_, TPW_>(a, s, shift, gmask, mode); return true; }
   ZT_STREAM_CASE(4, 2, 1) ZT_STREAM_CASE(4, 4, 1) ZT_STREAM_CASE(4, 8, 1) ZT_STREAM_CASE(4, 12, 1)
   ZT_STREAM_CASE(4, 16, 1) ZT_STREAM_CASE(4, 8, 2) ZT_STREAM_CASE(4, 4, 2) ZT_STREAM_CASE(4, 16, 2)
-  ZT_STREAM_CASE(8, 4, 1) ZT_STREAM_CASE(8, 8, 1) ZT_STREAM_CASE(8, 12, 1) ZT_STREAM_CASE(8, 16, 1)
+  ZT_STREAM_CASE(8, 4, 1) ZT_STREAM_CASE(8, 8, 1) ZT_STREAM_CASE(8, 12, 1) ZT_STREAM_CASE(8, 14, 1)
+  ZT_STREAM_CASE(8, 16, 1) ZT_STREAM_CASE(8, 14, 2)
   ZT_STREAM_CASE(8, 4, 2) ZT_STREAM_CASE(8, 8, 2) ZT_STREAM_CASE(8, 16, 2) ZT_STREAM_CASE(2, 16, 1)
   ZT_STREAM_CASE(16, 2, 1) ZT_STREAM_CASE(16, 2, 2) ZT_STREAM_CASE(16, 4, 1) ZT_STREAM_CASE(16, 8, 1)
 #undef ZT_STREAM_CASE
