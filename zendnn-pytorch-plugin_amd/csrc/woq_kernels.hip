@@ -375,6 +375,11 @@ __host__ __device__ constexpr size_t stream_slab_bytes(int nw, int tpw, int mt) 
   return (size_t)nw * tpw * mt * 16 * 17 * sizeof(float);
 }
 __host__ __device__ inline int stream_x_pitch(int K) { return K + 8; }  // bf16
+// fast mode: the bf16 scales of the workgroup's TPW*16 rows for all G groups,
+// [G][TPW*16], moved by 256-byte DMA instructions
+__host__ __device__ constexpr size_t stream_scale_bytes(int G, int tpw) {
+  return (size_t)((G * tpw + 7) / 8) * 256;
+}
 
 template <int NW, int CPW, int TPW, int MODE, int P, int MT>
 __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_shift, int gmask,
@@ -419,8 +424,24 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   };
   if (x_dma) dma_x(0);
+  // The fast mode's scales: one DMA instruction moves 64 dwords, i.e. the
+  // TPW*16 row scales of 8/TPW groups ([G][TPW*16] bf16 in LDS; N is even,
+  // host-checked, so every dword is aligned).  Issued before the weights,
+  // so the wait for x below covers them too.
+  const uint16_t *sl = reinterpret_cast<const uint16_t *>(
+      smem + stream_slab_bytes(NW, TPW, MT) + (size_t)M * XP * 2);
+  if (MODE == kDecFast) {
+    const int G = (int)a.G, gbytes = TPW * 32;
+    const int ns = (G * TPW + 7) / 8;
+    for (int i = wv; i < ns; i += NW) {
+      const int byte = i * 256 + lane * 4, g = byte / gbytes, b = byte - g * gbytes;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          s_rsrc, (lds_ptr_t)(sl + i * 128), 4,
+          g < G ? (uint32_t)((g * N + t0 * 16) * 2 + b) : kOobOffset, 0, 0, 0);
+    }
+  }
 
-  // 2. the slice's weights and scales, all in flight.  Rows past N are
+  // 2. the slice's weights and (other modes) scales, all in flight.  Rows past N are
   //    clamped (their results are never stored); chunks past C read zeros.
   u32x4_t wr[TPW][CPW];
   uint32_t sr[TPW][CPW];
@@ -439,7 +460,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
                        w_rsrc, kc < C ? row_off + (uint32_t)kc * 64u : kOobOffset, 0, 0));
       if (MODE == kDecGenF32)
         sr[t][c] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, sidx * 4u, 0, 0);
-      else
+      else if (MODE == kDecGenBf16)
         sr[t][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, sidx * 2u, 0, 0);
       zr[t][c] = (MODE != kDecFast && zmode) ? load_elem(a.zp, a.zp_dt, sidx) : 0.f;
     }
@@ -447,7 +468,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
 
   // 3. copy x by loads when the DMA does not apply (P == 1 only), and wait
   //    for it.  With the DMA and the fast mode a wave issued exactly
-  //    2*TPW*CPW weight and scale loads after its x, so waiting until at
+  //    TPW*CPW weight loads after its x and scale DMAs, so waiting until at
   //    most that many are outstanding (then a bare barrier) leaves the
   //    weights in flight: each chunk is dequantised as its own weights land
   //    instead of after all of them (__syncthreads' fence waits for every
@@ -462,7 +483,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
   if (P == 1 && MODE == kDecFast && x_dma) {
-    constexpr int after = 2 * TPW * CPW > 63 ? 63 : 2 * TPW * CPW;
+    constexpr int after = TPW * CPW > 63 ? 63 : TPW * CPW;
     __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (7 << 4) | (15 << 8));
     asm volatile("s_barrier" ::: "memory");
   } else {
@@ -490,7 +511,10 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
       bf16x8_t wb[TPW][4];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
-        const uint32_t sb = sr[t][c];
+        const uint32_t sb =
+            MODE == kDecFast
+                ? (uint32_t)sl[((min(kc, C - 1) >> cpg_shift) & gmask) * (TPW * 16) + t * 16 + lr]
+                : sr[t][c];
         const float sc = MODE == kDecGenF32 ? __uint_as_float(sb) : __uint_as_float(sb << 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) wb[t][i] = dq_word<MODE>(wr[t][c][i], sc, zr[t][c], zmode);
@@ -1231,7 +1255,8 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
   const int x_dma = stream_x_dma(a, P) ? 1 : 0;
   if (P > 1 && !x_dma) return hipErrorInvalidValue;  // phases need the DMA (host-checked)
   const size_t lds =
-      stream_slab_bytes(NW, TPW, MT) + (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2;
+      stream_slab_bytes(NW, TPW, MT) + (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2 +
+      (mode == kDecFast ? stream_scale_bytes((int)a.G, TPW) : 0);
   dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
   if (mode == kDecFast)
     woq_stream_kernel<NW, CPW, TPW, kDecFast, P, MT><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
@@ -1253,6 +1278,9 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   const int C = (int)(a.K / 128);
   const int tiles = (int)((a.N + 15) / 16);
   if (a.M > 64) return false;
+  // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
+  // N take the general bf16-scale mode (same weights, same results)
+  if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles, or more
   // tiles than CUs when x takes most of the LDS (one workgroup per CU)
@@ -1263,7 +1291,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
   const int mt = (int)((a.M + 15) / 16) == 3 ? 4 : (int)((a.M + 15) / 16);
   auto fits = [&](int p) {
-    return stream_slab_bytes(nw, tpw, mt) + (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 <=
+    return stream_slab_bytes(nw, tpw, mt) + (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 +
+               (mode == kDecFast ? stream_scale_bytes((int)a.G, tpw) : 0) <=
            kStreamLdsMax;
   };
   if (mt > 1 || !fits(1)) {
