@@ -1358,7 +1358,9 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
 // (8 k each) in both operands.  B is x from LDS: 1 KB rows, 16-byte chunk c
 // of token row t at position c ^ (t & 15) (16 distinct bank groups for the
 // 16 rows one read pass touches).  Dequantisation is the decode kernels'
-// (bf16_rne of the exact fp32 product).
+// (bf16_rne of the exact fp32 product).  The scales of a phase's four
+// chunks for the workgroup's 128 rows come with its x, one 256-byte DMA per
+// chunk into a double-buffered LDS block [4][128].
 //
 // D is [n][token]: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4
 // of the wave's 32 and token 32*j + l%32.  With one K split the workgroup
@@ -1373,7 +1375,8 @@ constexpr int kWideRows = 128;  // weight rows per workgroup
 
 template <int MT>
 constexpr size_t woq_wide_lds() {
-  const size_t x = 2 * (size_t)(32 * MT) * 1024;
+  // two x phase buffers, then two phase buffers of scales [4 chunks][128 rows]
+  const size_t x = 2 * (size_t)(32 * MT) * 1024 + 2 * 4 * kWideRows * 2;
   const size_t tile = (size_t)(32 * MT) * (kWideRows + 4) * 4;
   return x > tile ? x : tile;
 }
@@ -1384,7 +1387,7 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int XB = 32 * MT * 1024;  // one x phase buffer
   constexpr int XL = 4 * MT;          // x rows (one load each) per wave per phase
-  constexpr int WL = 6;  // weight + scale loads per wave per phase
+  constexpr int WL = 4;  // weight loads per wave per phase
   constexpr int WAIT = vmcnt_imm_woq(WL);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1399,15 +1402,13 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
   const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
   const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
 
-  // the lane's two load rows and its A-operand row after the swap (rows
-  // past N read zeros / a clamped scale; their outputs are never stored)
+  // the lane's two load rows (rows past N read zeros, scales past N zeros
+  // or another group's; their outputs are never stored)
   const int r_lo = n0 + rw * 32 + lr, r_hi = r_lo + 16;
   const uint32_t off_lo = (uint32_t)r_lo * (uint32_t)KW * 4u + 16u * lg;
   const uint32_t off_hi = (uint32_t)r_hi * (uint32_t)KW * 4u + 16u * lg;
-  const uint32_t srow = (uint32_t)min(n0 + rw * 32 + l32, N - 1);
 
   u32x4_t wq[3][2][2];
-  uint32_t sq[3][2];
   // Phases past the split (or past K) load zeros so every phase issues the
   // same number of loads.  The out-of-range bit is ORed into the offsets
   // (valid offsets stay below it): a select on the wave-uniform condition
@@ -1422,13 +1423,20 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
           w_rs, (off_lo + kc * 64u) | oob_lo | oob, 0, 0));
       wq[set][c][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
           w_rs, (off_hi + kc * 64u) | oob_hi | oob, 0, 0));
-      const uint32_t sidx = ((kc >> cpg_shift) & (uint32_t)gmask) * (uint32_t)N + srow;
-      sq[set][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, (sidx * 2u) | oob, 0, 0);
     }
   };
+  // x of a phase, and its scales: wave w < 4 moves the 128 row scales of
+  // chunk w's group (one 256-byte DMA; N % 4 == 0 keeps the dwords aligned)
+  unsigned char *sbuf0 = smem + 2 * XB;
   auto dma_x = [&](int ph) {
     const uint32_t oob = ph < ph0 + pps ? 0u : kOobOffset;
     unsigned char *buf = smem + (ph & 1) * XB;
+    if (wv < 4) {
+      const uint32_t g = ((uint32_t)(ph * 4 + wv) >> cpg_shift) & (uint32_t)gmask;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          s_rs, (lds_ptr_t)(sbuf0 + ((ph & 1) * 4 + wv) * (kWideRows * 2)), 4,
+          ((g * (uint32_t)N + (uint32_t)n0) * 2u + (uint32_t)lane * 4u) | oob, 0, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       const int t = wv + 8 * i;
@@ -1456,7 +1464,10 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
         w0[e] = sw[0];
         w1[e] = sw[1];
       }
-      const float sc = __uint_as_float(sq[set][c] << 16);
+      const float sc = __uint_as_float(
+          (uint32_t)reinterpret_cast<const uint16_t *>(
+              sbuf0 + ((ph & 1) * 4 + 2 * kh + c) * (kWideRows * 2))[rw * 32 + l32]
+          << 16);
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const bf16x8_t wb = dq_word<kDecFast>(q < 4 ? w0[q] : w1[q - 4], sc, 0.f, 0);
