@@ -183,6 +183,14 @@ def test_llama_decode_shapes_m16(N, K):
     run_case(16, K, N, K // 128, seed=N + K)
 
 
+@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("N,K", [(8192, 1024), (3072, 4096), (8192, 8192), (97, 1024)])
+def test_stream_kernel_small_m_shapes(M, N, K):
+    # M <= 4: 16 waves of 2-4 chunks below 512 row tiles, 4 waves of one
+    # tile each from 512 tiles on; odd N takes the general bf16-scale mode
+    run_case(M, K, N, K // 128, seed=M + N + K, bias=True)
+
+
 @pytest.mark.parametrize("M,K", [(4, 3328), (16, 3328), (8, 3584)])
 def test_stream_kernel_x_copy_paths(M, K):
     # 26 or 28 chunks of K: the stream kernel, x copied by loads when its

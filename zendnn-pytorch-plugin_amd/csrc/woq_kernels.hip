@@ -1319,10 +1319,17 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     }
     return false;
   }
+  // at M <= 4 (x a few KB) the shortest per-wave chains win: 16 waves of
+  // two to four chunks for up to two rounds of tiles, 4 waves of one tile
+  // each beyond (measured with the Llama-3 8B shapes at K = 4096)
+  if (!e && a.M <= 4 && C <= 64) {
+    nw = tiles < 512 ? 16 : 4;
+    tpw = 1;
+  }
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
     for (int c : {2, 4, 8, 12, 14, 16})
-      if (c >= need) { cpw = c; break; }
+      if (c >= need && (c != 14 || nw == 8)) { cpw = c; break; }
   if (cpw < need) return false;
   if (std::getenv("ZT_WOQ_DEBUG"))
     std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: NW=%d CPW=%d TPW=%d\n",
