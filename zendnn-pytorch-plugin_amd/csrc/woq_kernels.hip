@@ -361,15 +361,24 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 //
 // One workgroup per TPW 16-row tiles over all of K; its NW waves split K
 // into slices of CPW 128-wide chunks.  The workgroup first starts the copy
-// of x [M, K] into LDS by DMA (when the rows are 16-byte aligned), then a
-// wave issues every weight and scale load of its slice (TPW x CPW 16-byte
-// fragments per lane, all in flight at once: few waves with many loads each
-// keep HBM busier than many waves with few).  A wave's loads retire in
-// issue order, so x (from L2) lands while its weights are still in flight.
-// The wave then walks its chunks: B operands come from LDS (lanes past M
-// read zeros), A operands are the fragments dequantised in registers.  K
-// partials meet in LDS and are added in wave order.
+// of x [M, K] into LDS by DMA (when the rows are 16-byte aligned) and, in
+// the fast mode, of its rows' scales; then a wave issues the weight loads
+// of its slice's first chunks (TPW 16-byte fragments per lane per chunk):
+// all of them in the general modes, ZT_STREAM_DEPTH of them in the fast
+// mode, which issues chunk c + depth as it starts computing chunk c, so
+// the buffer unit takes the later loads while the wave dequantises instead
+// of holding the wave in a long issue phase first.  A wave's loads retire
+// in issue order, so x (from L2) lands while its weights are still in
+// flight.  The wave then walks its chunks: B operands come from LDS (token
+// columns past M repeat row M-1), A operands are the fragments dequantised
+// in registers.  K partials meet in LDS and are added in wave order.
 constexpr size_t kStreamLdsMax = 160 * 1024;
+// fast mode: chunks (per tile) of weights in flight per wave; the next one
+// is issued as each is computed (measured best of 2, 3, 4, 6, 8 and all at
+// once on the Llama-3 8B decode shapes)
+#ifndef ZT_STREAM_DEPTH
+#define ZT_STREAM_DEPTH 2
+#endif
 // per-wave fp32 partials: TPW row tiles x MT token tiles of 16 x 16 (+1 pad)
 __host__ __device__ constexpr size_t stream_slab_bytes(int nw, int tpw, int mt) {
   return (size_t)nw * tpw * mt * 16 * 17 * sizeof(float);
@@ -441,17 +450,16 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
 
-  // 2. the slice's weights and (other modes) scales, all in flight.  Rows past N are
+  // 2. the slice's weights and (other modes) scales.  Rows past N are
   //    clamped (their results are never stored); chunks past C read zeros.
   u32x4_t wr[TPW][CPW];
   uint32_t sr[TPW][CPW];
   float zr[TPW][CPW];
+  auto load_chunk = [&](int c) {
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int n = min((t0 + t) * 16 + lr, N - 1);
-    const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
+    for (int t = 0; t < TPW; ++t) {
+      const int n = min((t0 + t) * 16 + lr, N - 1);
+      const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
       const int kc = chunk_of(c);
       const int kcs = min(kc, C - 1);
       const uint32_t sidx = (uint32_t)((kcs >> cpg_shift) & gmask) * (uint32_t)N + (uint32_t)n;
@@ -464,7 +472,11 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
         sr[t][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, sidx * 2u, 0, 0);
       zr[t][c] = (MODE != kDecFast && zmode) ? load_elem(a.zp, a.zp_dt, sidx) : 0.f;
     }
-  }
+  };
+  // the first D chunks now, chunk c + D when chunk c is computed
+  constexpr int D = (MODE == kDecFast && CPW > ZT_STREAM_DEPTH) ? ZT_STREAM_DEPTH : CPW;
+#pragma unroll
+  for (int c = 0; c < D; ++c) load_chunk(c);
 
   // 3. copy x by loads when the DMA does not apply (P == 1 only), and wait
   //    for it.  With the DMA and the fast mode a wave issued exactly
@@ -483,7 +495,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
   if (P == 1 && MODE == kDecFast && x_dma) {
-    constexpr int after = TPW * CPW > 63 ? 63 : TPW * CPW;
+    constexpr int after = TPW * D > 63 ? 63 : TPW * D;
     __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (7 << 4) | (15 << 8));
     asm volatile("s_barrier" ::: "memory");
   } else {
@@ -505,6 +517,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
       dma_x(c / CPWP);
       __syncthreads();
     }
+    if (c + D < CPW) load_chunk(c + D);
     const int kc = chunk_of(c);
     if (kc < C) {
       const int kcl = P == 1 ? kc : kc - (c / CPWP) * CP;  // chunk within the LDS range
