@@ -357,7 +357,7 @@ __global__ __launch_bounds__(decode_max_threads<CPW>()) void woq_decode_kernel(
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 // Weight-streaming decode kernel (M <= 16 and the activations fit in LDS,
-// up to kStreamLdsMax with the partial slab).
+// up to kStreamLdsMax with the scales; the partial slabs reuse x's space).
 //
 // One workgroup per TPW 16-row tiles over all of K; its NW waves split K
 // into slices of CPW 128-wide chunks.  The workgroup first starts the copy
@@ -382,6 +382,12 @@ constexpr size_t kStreamLdsMax = 160 * 1024;
 // per-wave fp32 partials: TPW row tiles x MT token tiles of 16 x 16 (+1 pad)
 __host__ __device__ constexpr size_t stream_slab_bytes(int nw, int tpw, int mt) {
   return (size_t)nw * tpw * mt * 16 * 17 * sizeof(float);
+}
+// LDS: x [M][XP] (or one phase's range) at offset 0, overlaid after the
+// chunk loop by the partial slabs; the fast mode's scales after the larger
+// of the two
+__host__ __device__ constexpr size_t stream_scale_offset(size_t slab, size_t x) {
+  return slab > x ? slab : x;
 }
 __host__ __device__ inline int stream_x_pitch(int K) { return K + 8; }  // bf16
 // fast mode: the bf16 scales of the workgroup's TPW*16 rows for all G groups,
@@ -421,7 +427,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   //    pieces; always for P > 1): instruction i moves 64 16-byte chunks of
   //    one row.
   const int XP = P == 1 ? stream_x_pitch(K) : stream_x_pitch(K / P);
-  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + stream_slab_bytes(NW, TPW, MT));
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem);
   const auto x_rsrc = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
   auto dma_x = [&](int p) {
     const int per_row = (P == 1 ? K : K / P) / 512;  // 1 KB pieces per row
@@ -438,7 +444,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   // host-checked, so every dword is aligned).  Issued before the weights,
   // so the wait for x below covers them too.
   const uint16_t *sl = reinterpret_cast<const uint16_t *>(
-      smem + stream_slab_bytes(NW, TPW, MT) + (size_t)M * XP * 2);
+      smem + stream_scale_offset(stream_slab_bytes(NW, TPW, MT), (size_t)M * XP * 2));
   if (MODE == kDecFast) {
     const int G = (int)a.G, gbytes = TPW * 32;
     const int ns = (G * TPW + 7) / 8;
@@ -552,8 +558,10 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   }
 
-  // 5. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t][mt], then
-  //    each output adds the NW partials in wave order
+  // 5. partials D[row = 4g + r][token = lane % 16] -> slab[wave][t][mt]
+  //    (over x, once every wave is done with it), then each output adds the
+  //    NW partials in wave order
+  __syncthreads();
   float *slab = reinterpret_cast<float *>(smem);
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
@@ -1268,7 +1276,8 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
   const int x_dma = stream_x_dma(a, P) ? 1 : 0;
   if (P > 1 && !x_dma) return hipErrorInvalidValue;  // phases need the DMA (host-checked)
   const size_t lds =
-      stream_slab_bytes(NW, TPW, MT) + (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2 +
+      stream_scale_offset(stream_slab_bytes(NW, TPW, MT),
+                          (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2) +
       (mode == kDecFast ? stream_scale_bytes((int)a.G, TPW) : 0);
   dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
   if (mode == kDecFast)
@@ -1304,7 +1313,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
   const int mt = (int)((a.M + 15) / 16) == 3 ? 4 : (int)((a.M + 15) / 16);
   auto fits = [&](int p) {
-    return stream_slab_bytes(nw, tpw, mt) + (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2 +
+    return stream_scale_offset(stream_slab_bytes(nw, tpw, mt),
+                               (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2) +
                (mode == kDecFast ? stream_scale_bytes((int)a.G, tpw) : 0) <=
            kStreamLdsMax;
   };
@@ -1602,6 +1612,11 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");
   const bool forced = e || (f && !std::strcmp(f, "wide"));
   if (M < 8 && !forced) return false;
+  // while x [M, K] leaves room for two stream-kernel workgroups per CU the
+  // stream kernel is faster (measured: gate_up 28672 x 4096 at M = 8 / 9
+  // takes 18.5 / 18.8 us there against 22.2 / 22.8 us here; 25.1 / 22.9 at
+  // M = 10, where x no longer fits twice)
+  if (M * (K + 8) * 2 <= 76 * 1024 && !forced) return false;
   if (M <= 32 && N * K <= (int64_t)4096 * 4096 && !forced) return false;
   const int64_t gs = K / G, cpg = gs / 128;
   if (G != 1 && (gs % 128 || (cpg & (cpg - 1)))) return false;
@@ -1616,9 +1631,9 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
     const int f = std::atoi(e);
     if (f >= 1 && phases % f == 0) ks = f;
   }
-  // 8..16 rows: only without a K split (measured: gate_up 28672 x 4096 at
-  // M = 8 / 16 takes 22.4 / 23.4 us here against 26.8 / 29.5 on the stream
-  // kernel, while the split shapes lose the reduce launch)
+  // up to 16 rows: only without a K split (measured: gate_up 28672 x 4096
+  // at M = 12 / 16 takes 22.6 / 22.9 us here against 25.9 / 27.2 on the
+  // stream kernel, while the split shapes lose the reduce launch)
   if (M < 17 && ks > 1 && !forced) return false;
   p->mt = M <= 32 ? 1 : 2;
   p->splits = ks;
