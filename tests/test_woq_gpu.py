@@ -186,8 +186,8 @@ def test_llama_decode_shapes_m16(N, K):
 @pytest.mark.parametrize("M", [1, 3, 4])
 @pytest.mark.parametrize("N,K", [(8192, 1024), (3072, 4096), (8192, 8192), (97, 1024)])
 def test_stream_kernel_small_m_shapes(M, N, K):
-    # M <= 4: 16 waves of 2-4 chunks below 512 row tiles, 4 waves of one
-    # tile each from 512 tiles on; odd N takes the general bf16-scale mode
+    # M <= 4: one row tile per wave below and above 512 tiles, K of 8 to
+    # 64 chunks; odd N takes the general bf16-scale mode
     run_case(M, K, N, K // 128, seed=M + N + K, bias=True)
 
 

@@ -1342,13 +1342,11 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     }
     return false;
   }
-  // at M <= 4 (x a few KB) the shortest per-wave chains win: 16 waves of
-  // two to four chunks for up to two rounds of tiles, 4 waves of one tile
-  // each beyond (measured with the Llama-3 8B shapes at K = 4096)
-  if (!e && a.M <= 4 && C <= 64) {
-    nw = tiles < 512 ? 16 : 4;
-    tpw = 1;
-  }
+  // at M <= 4 one tile per wave at any tile count (measured in HIP-graph
+  // replays of the Llama-3 8B shapes: gate_up 28672 x 4096 at M = 1 takes
+  // 16.0-16.5 us so against 17.4 with two tiles; 16 waves of two chunks or
+  // 4 of eight are no faster once the weights are pipelined)
+  if (!e && a.M <= 4) tpw = 1;
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
     for (int c : {2, 4, 8, 12, 14, 16})
