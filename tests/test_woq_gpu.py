@@ -191,6 +191,13 @@ def test_stream_kernel_small_m_shapes(M, N, K):
     run_case(M, K, N, K // 128, seed=M + N + K, bias=True)
 
 
+@pytest.mark.parametrize("M,N", [(10, 12816), (16, 12800)])
+def test_stream_kernel_four_tiles(M, N):
+    # x [M, 4096] past 76 KB with at least 800 row tiles: four tiles per
+    # wave; N = 12816 leaves a last workgroup with one real tile
+    run_case(M, 4096, N, 32, post=("add",), nbuf=1, seed=M + N, bias=True)
+
+
 @pytest.mark.parametrize("M,K", [(4, 3328), (16, 3328), (8, 3584)])
 def test_stream_kernel_x_copy_paths(M, K):
     # 26 or 28 chunks of K: the stream kernel, x copied by loads when its

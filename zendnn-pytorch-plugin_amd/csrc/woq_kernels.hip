@@ -1347,6 +1347,12 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // 16.0-16.5 us so against 17.4 with two tiles; 16 waves of two chunks or
   // 4 of eight are no faster once the weights are pipelined)
   if (!e && a.M <= 4) tpw = 1;
+  // x too large for two workgroups per CU: four tiles per wave while that
+  // still leaves most of a round of workgroups (measured: 14336 x 4096 at
+  // M = 12 / 16 takes 13.1 / 13.3 us so against 14.0 / 15.1 with two; at
+  // M = 8, with two workgroups per CU, four tiles lose)
+  if (!e && (size_t)a.M * stream_x_pitch((int)a.K) * 2 > 76 * 1024 && tiles >= 800 && C <= 64)
+    tpw = 4;
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
     for (int c : {2, 4, 8, 12, 14, 16})
@@ -1360,7 +1366,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   ZT_STREAM_CASE(4, 2, 1) ZT_STREAM_CASE(4, 4, 1) ZT_STREAM_CASE(4, 8, 1) ZT_STREAM_CASE(4, 12, 1)
   ZT_STREAM_CASE(4, 16, 1) ZT_STREAM_CASE(4, 8, 2) ZT_STREAM_CASE(4, 4, 2) ZT_STREAM_CASE(4, 16, 2)
   ZT_STREAM_CASE(8, 4, 1) ZT_STREAM_CASE(8, 8, 1) ZT_STREAM_CASE(8, 12, 1) ZT_STREAM_CASE(8, 14, 1)
-  ZT_STREAM_CASE(8, 16, 1) ZT_STREAM_CASE(8, 14, 2)
+  ZT_STREAM_CASE(8, 16, 1) ZT_STREAM_CASE(8, 14, 2) ZT_STREAM_CASE(8, 2, 4) ZT_STREAM_CASE(8, 4, 4)
+  ZT_STREAM_CASE(8, 8, 4)
   ZT_STREAM_CASE(8, 4, 2) ZT_STREAM_CASE(8, 8, 2) ZT_STREAM_CASE(8, 16, 2) ZT_STREAM_CASE(2, 16, 1)
   ZT_STREAM_CASE(16, 2, 1) ZT_STREAM_CASE(16, 2, 2) ZT_STREAM_CASE(16, 4, 1) ZT_STREAM_CASE(16, 8, 1)
 #undef ZT_STREAM_CASE
