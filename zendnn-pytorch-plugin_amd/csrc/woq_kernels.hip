@@ -1587,9 +1587,19 @@ __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)M * (N / 4)) return;
   const int m = (int)(idx / (N / 4)), n = (int)(idx % (N / 4)) * 4;
-  f32x4_t v = *reinterpret_cast<const f32x4_t *>(partial + (size_t)m * N + n);
-  for (int s = 1; s < splits; ++s)
-    v += *reinterpret_cast<const f32x4_t *>(partial + ((size_t)s * M + m) * N + n);
+  // four splits' loads in flight at a time, added in split order
+  const size_t stride = (size_t)M * N;
+  const float *p0 = partial + (size_t)m * N + n;
+  f32x4_t v = *reinterpret_cast<const f32x4_t *>(p0);
+  int s = 1;
+  for (; s + 4 <= splits; s += 4) {
+    f32x4_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = *reinterpret_cast<const f32x4_t *>(p0 + (s + i) * stride);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v += q[i];
+  }
+  for (; s < splits; ++s) v += *reinterpret_cast<const f32x4_t *>(p0 + s * stride);
   float f[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
