@@ -105,6 +105,32 @@ size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
                                     int64_t G);
 
 /*
+ * Merged gate_up int4 linear with the SiLU-and-mul epilogue.  No counterpart
+ * in the reference: it is the merged-weight form of the extension
+ * zentorch_woq_linear_silu_mul, for callers that hold the gate and up
+ * projections as one [2I, K] weight (vLLM's merged gate_up + SiluAndMul).
+ *   g = x . dequant(W[0:I])^T + bias[0:I]
+ *   u = x . dequant(W[I:2I])^T + bias[I:2I]
+ *   y[m][j] = silu(g[m][j]) * round_y(u[m][j]),   I = N/2
+ * round_y rounds u to y_dtype first, so y equals the two-op composition
+ * u = zt_woq_linear(x, W[I:2I]) then zt_woq_linear(x, W[0:I]) with the
+ * post-ops {SILU, MUL u}.  Arguments as zt_woq_linear without post-ops;
+ * N even, y [M, ldy] with N/2 columns.  Up to 16 rows of bf16 x with bf16
+ * scales and I % 16 == 0 run as one launch without workspace; other calls
+ * run the full linear into fp32 in the workspace, then the epilogue
+ * (zt_woq_linear_gate_up_workspace_size bytes).
+ */
+int zt_woq_linear_gate_up(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                          int64_t ldx, const int32_t *w_packed, int64_t N,
+                          const void *scales, int32_t scales_dtype, int64_t G,
+                          const void *zp, int32_t zp_dtype, const void *bias,
+                          int32_t bias_dtype, void *y, int32_t y_dtype, int64_t ldy,
+                          void *workspace, size_t workspace_bytes, zt_stream_t stream);
+
+size_t zt_woq_linear_gate_up_workspace_size(int64_t M, int64_t K, int64_t N,
+                                            int64_t G);
+
+/*
  * Dynamic int8 linear: per-token symmetric s8 quantisation of x inside the
  * op, int8 x int8 -> int32 GEMM, y = acc * sx[m] * sw[n] + bias[n].
  *

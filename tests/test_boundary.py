@@ -75,6 +75,12 @@ def test_c_abi_validates_without_gpu():
                       1, None, 2048, 256, None, None, 0, None)
     assert rc == 2 and b"1024 experts" in L.zt_last_error_string()
     assert L.zt_woq_moe_workspace_size(256, 4096, 2, 8, 14336) >= 512 * (14336 + 4096) * 2
+    # merged gate_up: an odd N is refused before any device work; the
+    # two-step path's workspace holds the fp32 [M, N] result
+    rc = L.zt_woq_linear_gate_up(None, 1, 4, 128, 128, None, 17, None, 1, 1, None, -1, None,
+                                 -1, None, 1, 8, None, 0, None)
+    assert rc == 1 and b"even" in L.zt_last_error_string()
+    assert L.zt_woq_linear_gate_up_workspace_size(20, 4096, 1024, 32) >= 20 * 1024 * 4
     # the WOQ kernels reduce K inside a workgroup: no device workspace
     assert L.zt_woq_linear_workspace_size(16, 14336, 4096, 112) == 0
     assert L.zt_woq_linear_workspace_size(2048, 4096, 4096, 32) == 0
@@ -126,6 +132,8 @@ def test_meta_shapes():
     buf = torch.empty(2, 3, 6144, dtype=torch.bfloat16, **m)
     assert ops.zentorch_woq_linear_mul_add(x, w, s, None, buf, buf).shape == (2, 3, 6144)
     assert ops.zentorch_woq_linear_silu_mul(x, w, s, None, buf).shape == (2, 3, 6144)
+    # merged gate_up [K/8, 2I] -> [*, I]
+    assert ops.zentorch_woq_linear_gate_up_silu_mul(x, w, s, None).shape == (2, 3, 3072)
     xw = torch.empty(128, 4096, dtype=torch.float32, **m)
     wq = torch.empty(11008, 4096, dtype=torch.int8, **m)
     y = ops.zentorch_dynamic_qlinear(xw, wq, torch.empty(11008, **m))

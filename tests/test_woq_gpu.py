@@ -198,6 +198,55 @@ def test_stream_kernel_four_tiles(M, N):
     run_case(M, 4096, N, 32, post=("add",), nbuf=1, seed=M + N, bias=True)
 
 
+def run_gate_up(M, K, I, G, seed, zp=None, x_dtype=torch.bfloat16, bias=True):
+    """Merged gate_up against the two-op composition on the oracle: the up
+    half through woq_linear, the gate half with the post-ops silu, mul."""
+    x, q, wp, s, z, b = make_case(M, K, 2 * I, G, seed, zp=zp, bias=bias, x_dtype=x_dtype)
+    half = lambda t, lo: None if t is None else (t[lo:lo + I] if t.dim() == 1 else
+                                                 t[:, lo:lo + I].contiguous())
+    up = O.woq_linear(x, wp[I:].contiguous(), half(s, I), zero_points=half(z, I),
+                      bias=half(b, I))
+    y_ref = O.woq_linear(x, wp[:I].contiguous(), half(s, 0), zero_points=half(z, 0),
+                         bias=half(b, 0), post_ops=("silu", "mul"), post_bufs=[up])
+    xd, wd, sd, zd, bd = gpu(x, wp, s, z, b)
+    y = C.woq_linear_gate_up(xd, wd, sd, zd, bd)
+    check_close(y, y_ref)
+
+
+# one launch: bf16, up to 16 rows, I % 16 == 0 (one gate/up tile pair per
+# wave, or two once x fills a CU's LDS and there are 800 tiles)
+@pytest.mark.parametrize("M", [1, 4, 9, 16])
+@pytest.mark.parametrize("K,I,G", [(1024, 64, 8), (4096, 256, 32), (2048, 1040, 1)])
+def test_gate_up_one_launch(M, K, I, G):
+    run_gate_up(M, K, I, G, seed=M + K + I)
+
+
+def test_gate_up_two_tile_pairs():
+    run_gate_up(16, 4096, 6400, 32, seed=5)
+
+
+# two steps (fp32 linear into the workspace, then silu * up): more rows,
+# fp32 activations, zero points, I % 16 != 0
+@pytest.mark.parametrize("M,K,I,G,zp,x_dtype", [
+    (20, 1024, 64, 8, None, torch.bfloat16),
+    (300, 512, 96, 4, None, torch.bfloat16),
+    (4, 1024, 64, 8, None, torch.float32),
+    (8, 512, 64, 4, "int", torch.bfloat16),
+    (3, 256, 40, 2, None, torch.bfloat16)])
+def test_gate_up_two_steps(M, K, I, G, zp, x_dtype):
+    run_gate_up(M, K, I, G, seed=M + I, zp=zp, x_dtype=x_dtype)
+
+
+def test_gate_up_torch_op():
+    import zentorch  # noqa: F401
+    M, K, I, G = 4, 1024, 128, 8
+    x, q, wp, s, z, b = make_case(M, K, 2 * I, G, seed=9, bias=True)
+    y = torch.ops.zentorch.zentorch_woq_linear_gate_up_silu_mul(
+        x.to(DEV), wp.to(DEV).t(), s.to(DEV), None, b.to(DEV))
+    y2 = C.woq_linear_gate_up(*gpu(x, wp, s), None, b.to(DEV))
+    assert y.shape == (M, I) and torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("M,K", [(4, 3328), (16, 3328), (8, 3584)])
 def test_stream_kernel_x_copy_paths(M, K):
     # 26 or 28 chunks of K: the stream kernel, x copied by loads when its

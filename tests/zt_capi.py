@@ -39,6 +39,12 @@ def lib():
         L.zt_woq_linear.restype = ctypes.c_int
         L.zt_woq_linear_workspace_size.argtypes = [_i64, _i64, _i64, _i64]
         L.zt_woq_linear_workspace_size.restype = _sz
+        L.zt_woq_linear_gate_up.argtypes = [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i32,
+                                            _i64, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
+                                            _vp, _sz, _vp]
+        L.zt_woq_linear_gate_up.restype = ctypes.c_int
+        L.zt_woq_linear_gate_up_workspace_size.argtypes = [_i64, _i64, _i64, _i64]
+        L.zt_woq_linear_gate_up_workspace_size.restype = _sz
         L.zt_dynamic_qlinear.argtypes = [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _i32, _vp,
                                          _i32, ctypes.POINTER(PostOps), _vp, _i32, _vp,
                                          _sz, _vp]
@@ -109,6 +115,27 @@ def woq_linear(x, w_nk, scales, zp=None, bias=None, post_ops=(), post_bufs=(),
     if sync:
         torch.cuda.synchronize()
     del keep
+    return y
+
+
+def woq_linear_gate_up(x, w_nk, scales, zp=None, bias=None, sync=True):
+    """Merged gate_up: w_nk int32 [2I,K/8] (gate rows, then up rows); y [M, I]."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    N = w_nk.shape[0]
+    G = scales.shape[0]
+    y = torch.empty(M, N // 2, dtype=x.dtype, device=x.device)
+    ws_bytes = lib().zt_woq_linear_gate_up_workspace_size(M, K, N, G)
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    rc = lib().zt_woq_linear_gate_up(
+        _p(x2), DT[x2.dtype], M, K, x2.stride(0), _p(w_nk), N, _p(scales), DT[scales.dtype], G,
+        _p(zp), DT[zp.dtype] if zp is not None else -1, _p(bias),
+        DT[bias.dtype] if bias is not None else -1, _p(y), DT[y.dtype], N // 2,
+        _p(ws), ws_bytes, _stream())
+    _check(rc)
+    if sync:
+        torch.cuda.synchronize()
     return y
 
 

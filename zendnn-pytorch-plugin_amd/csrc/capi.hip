@@ -223,14 +223,13 @@ size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
   return std::max(wide, zt::woq_decode_workspace(p, M, N));
 }
 
-int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
-                  int64_t ldx, const int32_t *w_packed, int64_t N,
-                  const void *scales, int32_t scales_dtype, int64_t G,
-                  const void *zp, int32_t zp_dtype, const void *bias,
-                  int32_t bias_dtype, const zt_post_ops *post, void *y,
-                  int32_t y_dtype, int64_t ldy, void *workspace,
-                  size_t workspace_bytes, zt_stream_t stream) {
-  static const char *op = "zt_woq_linear";
+// Argument checks shared by zt_woq_linear and zt_woq_linear_gate_up (ZT_OK
+// or the error code, with the message set); y_cols is the output width.
+static int check_woq_args(const char *op, const void *x, int32_t x_dtype, int64_t M,
+                          int64_t K, int64_t ldx, const int32_t *w_packed, int64_t N,
+                          const void *scales, int32_t scales_dtype, int64_t G, const void *zp,
+                          int32_t zp_dtype, const void *bias, int32_t bias_dtype, void *y,
+                          int32_t y_dtype, int64_t ldy, int64_t y_cols) {
   if (M < 0 || N < 0 || K < 8 || K % 8)
     return fail(ZT_EINVAL, "%s: need M,N >= 0 and K >= 8 with K %% 8 == 0 "
                 "(M=%lld N=%lld K=%lld)", op, (long long)M, (long long)N,
@@ -245,11 +244,25 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
     return fail(ZT_EINVAL, "%s: zero points must be bf16, fp32, int8, uint8 or int32", op);
   if (bias && !is_float_dt(bias_dtype))
     return fail(ZT_EINVAL, "%s: bias must be bf16 or fp32", op);
-  if (ldx < K || ldy < N)
+  if (ldx < K || ldy < y_cols)
     return fail(ZT_EINVAL, "%s: leading dimensions too small", op);
-  if (M == 0 || N == 0) return ZT_OK;
-  if (!x || !w_packed || !scales || !y)
+  if (M > 0 && N > 0 && (!x || !w_packed || !scales || !y))
     return fail(ZT_EINVAL, "%s: null tensor pointer", op);
+  return ZT_OK;
+}
+
+int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                  int64_t ldx, const int32_t *w_packed, int64_t N,
+                  const void *scales, int32_t scales_dtype, int64_t G,
+                  const void *zp, int32_t zp_dtype, const void *bias,
+                  int32_t bias_dtype, const zt_post_ops *post, void *y,
+                  int32_t y_dtype, int64_t ldy, void *workspace,
+                  size_t workspace_bytes, zt_stream_t stream) {
+  static const char *op = "zt_woq_linear";
+  int rc0 = check_woq_args(op, x, x_dtype, M, K, ldx, w_packed, N, scales, scales_dtype, G, zp,
+                           zp_dtype, bias, bias_dtype, y, y_dtype, ldy, N);
+  if (rc0) return rc0;
+  if (M == 0 || N == 0) return ZT_OK;
 
   zt::WoqArgs a{};
   a.x = x, a.x_dt = x_dtype, a.M = M, a.K = K, a.ldx = ldx;
@@ -296,6 +309,53 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   default:
     return hip_status(zt::launch_woq_generic(a, s), op);
   }
+}
+
+size_t zt_woq_linear_gate_up_workspace_size(int64_t M, int64_t K, int64_t N,
+                                            int64_t G) {
+  if (M <= 0 || N <= 0 || K <= 0 || G <= 0 || K % G) return 0;
+  const size_t h = ((size_t)M * (size_t)N * sizeof(float) + 255) / 256 * 256;
+  return h + zt_woq_linear_workspace_size(M, K, N, G);
+}
+
+int zt_woq_linear_gate_up(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                          int64_t ldx, const int32_t *w_packed, int64_t N,
+                          const void *scales, int32_t scales_dtype, int64_t G,
+                          const void *zp, int32_t zp_dtype, const void *bias,
+                          int32_t bias_dtype, void *y, int32_t y_dtype, int64_t ldy,
+                          void *workspace, size_t workspace_bytes, zt_stream_t stream) {
+  static const char *op = "zt_woq_linear_gate_up";
+  if (N % 2)
+    return fail(ZT_EINVAL, "%s: N=%lld must be even (gate rows, then up rows)", op,
+                (long long)N);
+  int rc0 = check_woq_args(op, x, x_dtype, M, K, ldx, w_packed, N, scales, scales_dtype, G, zp,
+                           zp_dtype, bias, bias_dtype, y, y_dtype, ldy, N / 2);
+  if (rc0) return rc0;
+  if (M == 0 || N == 0) return ZT_OK;
+  zt::WoqArgs a{};
+  a.x = x, a.x_dt = x_dtype, a.M = M, a.K = K, a.ldx = ldx;
+  a.w = reinterpret_cast<const uint32_t *>(w_packed), a.N = N;
+  a.scales = scales, a.s_dt = scales_dtype, a.G = G;
+  a.zp = zp, a.zp_dt = zp ? zp_dtype : ZT_DT_NONE;
+  a.bias = bias, a.b_dt = bias ? bias_dtype : ZT_DT_NONE;
+  a.y = y, a.y_dt = y_dtype, a.ldy = ldy;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipSuccess;
+  if (zt::woq_try_stream_gate_up(a, s, &err)) return hip_status(err, op);
+  // two steps: the full [M, N] linear in fp32 into the workspace, then
+  // silu(gate) * up over its halves
+  const size_t h = ((size_t)M * (size_t)N * sizeof(float) + 255) / 256 * 256;
+  if (!workspace || workspace_bytes < h)
+    return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op,
+                zt_woq_linear_gate_up_workspace_size(M, K, N, G),
+                workspace ? workspace_bytes : (size_t)0);
+  float *hbuf = static_cast<float *>(workspace);
+  int rc = zt_woq_linear(x, x_dtype, M, K, ldx, w_packed, N, scales, scales_dtype, G, zp,
+                         zp_dtype, bias, bias_dtype, nullptr, hbuf, ZT_DT_F32, N,
+                         static_cast<unsigned char *>(workspace) + h, workspace_bytes - h,
+                         stream);
+  if (rc) return rc;
+  return hip_status(zt::launch_silu_mul_halves(hbuf, N, M, N / 2, y, y_dtype, ldy, s), op);
 }
 
 // qx region of the dynamic-qlinear workspace: whole 32-row tiles (the

@@ -7,7 +7,8 @@
 // (src/cpu/cpp/WOQ_Linear.cpp:435-480, DynamicQLinear.cpp:184-189) so graphs,
 // the compile pass and callers such as vLLM's torchao patch bind unchanged.
 // zentorch_woq_linear_silu_mul is an extension (no reference op; the
-// reference's closest is zentorch_mm_silu_mul, Matmul.cpp:440-441).
+// reference's closest is zentorch_mm_silu_mul, Matmul.cpp:440-441), and so is
+// its merged-weight form zentorch_woq_linear_gate_up_silu_mul.
 //
 // There is no CPU kernel: a CPU tensor reaching these ops is an error, not a
 // fallback.
@@ -101,7 +102,7 @@ at::Tensor woq_linear_impl(const at::Tensor &input, const at::Tensor &weight,
                            const c10::optional<at::Tensor> &bias,
                            const std::vector<int32_t> &post_ids,
                            const std::vector<at::Tensor> &binary_inputs,
-                           const std::string &op_name) {
+                           const std::string &op_name, bool gate_up = false) {
   const char *op = op_name.c_str();
   check_device(input, input, op, "input");
   check_device(weight, input, op, "weight");
@@ -149,8 +150,26 @@ at::Tensor woq_linear_impl(const at::Tensor &input, const at::Tensor &weight,
                 " elements, got ", bias->numel());
     b = bias->contiguous();
   }
-  at::Tensor result = at::empty(out_sizes(input, N), input.options());
+  if (gate_up)
+    TORCH_CHECK(N % 2 == 0, op, ": the merged gate_up weight needs an even N (gate rows, "
+                "then up rows), got ", N);
+  at::Tensor result = at::empty(out_sizes(input, gate_up ? N / 2 : N), input.options());
   if (result.numel() == 0) return result;
+  if (gate_up) {
+    const size_t ws = zt_woq_linear_gate_up_workspace_size(M, K, N, G);
+    void *wsp = woq_workspace(input, ws);
+    const int rc = zt_woq_linear_gate_up(
+        x2.data_ptr(), zt_dtype_of(x2), M, K, K,
+        reinterpret_cast<const int32_t *>(w_nk.data_ptr()), N, s.data_ptr(),
+        zt_dtype_of(s), G, zp.defined() ? zp.data_ptr() : nullptr,
+        zp.defined() ? zt_dtype_of(zp) : ZT_DT_NONE,
+        b.defined() ? b.data_ptr() : nullptr,
+        b.defined() ? zt_dtype_of(b) : ZT_DT_NONE, result.data_ptr(),
+        zt_dtype_of(result), N / 2, wsp, ws,
+        reinterpret_cast<zt_stream_t>(current_stream()));
+    TORCH_CHECK(rc == ZT_OK, op, ": ", zt_last_error_string());
+    return result;
+  }
 
   zt_post_ops post{};
   post.count = (int32_t)post_ids.size();
@@ -268,6 +287,15 @@ at::Tensor woq_linear_silu_mul(const at::Tensor &input, const at::Tensor &weight
   return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias,
                          {ZT_PO_SILU, ZT_PO_MUL}, {mul_input},
                          std::string(zentorch_op_name));
+}
+
+at::Tensor woq_linear_gate_up_silu_mul(const at::Tensor &input, const at::Tensor &weight,
+                                       const at::Tensor &weight_scales,
+                                       const c10::optional<at::Tensor> &weight_zero_points,
+                                       const c10::optional<at::Tensor> &bias,
+                                       c10::string_view zentorch_op_name) {
+  return woq_linear_impl(input, weight, weight_scales, weight_zero_points, bias, {}, {},
+                         std::string(zentorch_op_name), /*gate_up=*/true);
 }
 
 at::Tensor woq_repack_weight(const at::Tensor &unpacked_weight) {
@@ -519,6 +547,11 @@ TORCH_LIBRARY(zentorch, m) {
         "Tensor mul_input, Tensor? bias=None, *, str "
         "zentorch_op_name='zentorch::zentorch_woq_linear_silu_mul') -> Tensor",
         {at::Tag::needs_fixed_stride_order});
+  // Extension: the merged gate_up weight [K/8, 2I] (gate columns, then up
+  // columns) with silu(gate) * up as its epilogue; output [*, I].
+  m.def("zentorch_woq_linear_gate_up_silu_mul(Tensor input, Tensor weight,"
+        "Tensor weight_scales, Tensor? weight_zero_points, Tensor? bias=None, *, str "
+        "zentorch_op_name='zentorch::zentorch_woq_linear_gate_up_silu_mul') -> Tensor");
   m.def("zentorch_woq_repack_weight(Tensor unpacked_weight) -> Tensor");
   m.def("zentorch_woq_repack_from_int4pack(Tensor "
         "packed_weight) -> Tensor");
@@ -547,6 +580,7 @@ TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
   m.impl("zentorch_woq_linear_mul_add", woq_linear_mul_add);
   m.impl("zentorch_woq_linear_add_add", woq_linear_add_add);
   m.impl("zentorch_woq_linear_silu_mul", woq_linear_silu_mul);
+  m.impl("zentorch_woq_linear_gate_up_silu_mul", woq_linear_gate_up_silu_mul);
   m.impl("zentorch_woq_repack_weight", woq_repack_weight);
   m.impl("zentorch_woq_repack_from_int4pack", woq_repack_from_int4pack);
   m.impl("zentorch_dynamic_qlinear", dynamic_qlinear);

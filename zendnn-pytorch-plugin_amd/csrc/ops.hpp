@@ -55,6 +55,11 @@ at::Tensor woq_linear_add_add(const at::Tensor &input, const at::Tensor &weight,
                               const at::Tensor &add_input_2,
                               const c10::optional<at::Tensor> &bias,
                               c10::string_view zentorch_op_name);
+at::Tensor woq_linear_gate_up_silu_mul(const at::Tensor &input, const at::Tensor &weight,
+                                       const at::Tensor &weight_scales,
+                                       const c10::optional<at::Tensor> &weight_zero_points,
+                                       const c10::optional<at::Tensor> &bias,
+                                       c10::string_view zentorch_op_name);
 at::Tensor woq_linear_silu_mul(const at::Tensor &input, const at::Tensor &weight,
                                const at::Tensor &weight_scales,
                                const c10::optional<at::Tensor> &weight_zero_points,

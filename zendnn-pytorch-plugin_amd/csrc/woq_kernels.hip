@@ -396,9 +396,15 @@ __host__ __device__ constexpr size_t stream_scale_bytes(int G, int tpw) {
   return (size_t)((G * tpw + 7) / 8) * 256;
 }
 
+// gu > 0 (merged gate_up, fast mode, TPW even, P == MT == 1): weight rows
+// [0, gu) are the gate and [gu, 2 gu) the up projection; tile 2i of the
+// workgroup is gate tile blockIdx.x * TPW/2 + i and tile 2i + 1 the up tile
+// of the same columns, and the workgroup writes silu(gate) * up for its
+// TPW/2 * 16 output columns (up rounded to the output dtype first, as the
+// two-op composition does).
 template <int NW, int CPW, int TPW, int MODE, int P, int MT>
 __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_shift, int gmask,
-                                                             int x_dma) {
+                                                             int x_dma, int gu) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -406,6 +412,10 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
   const int KW = K / 8, C = K / 128;
   const int t0 = blockIdx.x * TPW;
+  // first weight row of the workgroup's tile t
+  auto rowbase = [&](int t) {
+    return gu ? (t & 1) * gu + (blockIdx.x * (TPW / 2) + (t >> 1)) * 16 : (t0 + t) * 16;
+  };
   const int zmode = zp_mode_of(a.zp, a.zp_dt);
   const int s_bytes = MODE == kDecGenF32 ? 4 : 2;
   const auto w_rsrc = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
@@ -450,9 +460,10 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     const int ns = (G * TPW + 7) / 8;
     for (int i = wv; i < ns; i += NW) {
       const int byte = i * 256 + lane * 4, g = byte / gbytes, b = byte - g * gbytes;
+      const int q = b >> 1;  // row within the group's TPW*16 (even: both rows in one tile)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           s_rsrc, (lds_ptr_t)(sl + i * 128), 4,
-          g < G ? (uint32_t)((g * N + t0 * 16) * 2 + b) : kOobOffset, 0, 0, 0);
+          g < G ? (uint32_t)((g * N + rowbase(q >> 4) + (q & 15)) * 2) : kOobOffset, 0, 0, 0);
     }
   }
 
@@ -464,7 +475,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   auto load_chunk = [&](int c) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int n = min((t0 + t) * 16 + lr, N - 1);
+      const int n = min(rowbase(t) + lr, N - 1);
       const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
       const int kc = chunk_of(c);
       const int kcs = min(kc, C - 1);
@@ -571,6 +582,29 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
       for (int r = 0; r < 4; ++r)
         slab[(((wv * TPW + t) * MT + mt) * 16 + 4 * lg + r) * 17 + lr] = acc[t][mt][r];
   __syncthreads();
+  if (gu) {
+    constexpr int GT = TPW / 2;  // gate tiles of the workgroup
+    const int j0 = blockIdx.x * GT * 16;
+    for (int idx = tid; idx < GT * 16 * M; idx += 64 * NW) {
+      const int m = idx / (GT * 16), jr = idx - m * (GT * 16);
+      const int i = jr >> 4, r16 = jr & 15;
+      const int j = j0 + jr;
+      if (j >= gu) continue;
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        g += slab[((w * TPW + 2 * i) * MT * 16 + r16) * 17 + m];
+        u += slab[((w * TPW + 2 * i + 1) * MT * 16 + r16) * 17 + m];
+      }
+      if (a.bias) {
+        g = g + load_elem(a.bias, a.b_dt, j);
+        u = u + load_elem(a.bias, a.b_dt, gu + j);
+      }
+      if (a.y_dt == ZT_DT_BF16) u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+      store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + j, unary_op(ZT_PO_SILU, g) * u);
+    }
+    return;
+  }
   const int n0 = t0 * 16;
   for (int idx = tid; idx < TPW * 16 * M; idx += 64 * NW) {
     const int m = idx / (TPW * 16), nr = idx - m * (TPW * 16);
@@ -1281,13 +1315,13 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
       (mode == kDecFast ? stream_scale_bytes((int)a.G, TPW) : 0);
   dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
   if (mode == kDecFast)
-    woq_stream_kernel<NW, CPW, TPW, kDecFast, P, MT><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+    woq_stream_kernel<NW, CPW, TPW, kDecFast, P, MT><<<grid, block, lds, s>>>(a, shift, gmask, x_dma, 0);
   else if (P > 1 || MT > 1)
     return hipErrorInvalidValue;  // phases and token tiles are built for the fast mode only
   else if (mode == kDecGenBf16)
-    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+    woq_stream_kernel<NW, CPW, TPW, kDecGenBf16, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma, 0);
   else
-    woq_stream_kernel<NW, CPW, TPW, kDecGenF32, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma);
+    woq_stream_kernel<NW, CPW, TPW, kDecGenF32, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, x_dma, 0);
   return hipGetLastError();
 }
 
@@ -1703,6 +1737,72 @@ bool woq_try_stream(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   const int gmask = a.G == 1 ? 0 : 0x7fffffff;
   const int mode = a.s_dt == ZT_DT_F32 ? kDecGenF32 : (a.zp ? kDecGenBf16 : kDecFast);
   return try_launch_stream(a, s, shift, gmask, mode, err);
+}
+
+// The merged gate_up launch of the stream kernel (fast mode, M <= 16, x
+// whole in LDS).  Returns false when the caller should take the two-step
+// path (the full linear into fp32, then launch_silu_mul_halves).
+bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
+  const int64_t I = a.N / 2, gs = a.K / a.G, cpg = gs / 128;
+  if (a.x_dt != ZT_DT_BF16 || a.s_dt != ZT_DT_BF16 || a.zp || a.M < 1 || a.M > 16 ||
+      a.N % 32 != 0 || a.K % 128 != 0 || (a.G != 1 && (gs % 128 || (cpg & (cpg - 1)))) ||
+      a.ldx % 8 != 0 || !aligned16(a.x) || !aligned16(a.w) ||
+      a.N * (a.K / 2) >= (int64_t)kOobOffset || a.G * a.N * 2 >= (int64_t)kOobOffset)
+    return false;
+  int shift = 0;
+  while (cpg > 1 && (1 << shift) < cpg) ++shift;
+  const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  const int C = (int)(a.K / 128), tiles = (int)(a.N / 16);
+  const size_t x_bytes = (size_t)a.M * stream_x_pitch((int)a.K) * 2;
+  // as the plain stream kernel: four tiles (two pairs) per wave once x
+  // takes a CU's LDS and there are enough tiles, else one pair
+  const int tpw = x_bytes > 76 * 1024 && tiles >= 800 ? 4 : 2;
+  const size_t lds = stream_scale_offset(stream_slab_bytes(8, tpw, 1), x_bytes) +
+                     stream_scale_bytes((int)a.G, tpw);
+  if (lds > kStreamLdsMax) return false;
+  const int need = (C + 7) / 8;
+  int cpw = 0;
+  for (int c : {2, 4, 8, 12, 14, 16})
+    if (c >= need) { cpw = c; break; }
+  if (cpw < need) return false;
+  const int x_dma = stream_x_dma(a, 1) ? 1 : 0;
+  const dim3 grid((unsigned)((I / 16 + tpw / 2 - 1) / (tpw / 2))), block(512);
+  if (std::getenv("ZT_WOQ_DEBUG"))
+    std::fprintf(stderr, "[zt] woq gate_up stream M=%lld N=%lld K=%lld: CPW=%d TPW=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, cpw, tpw);
+#define ZT_GU_CASE(CPW_, TPW_)                                                              \
+  if (cpw == CPW_ && tpw == TPW_) {                                                        \
+    woq_stream_kernel<8, CPW_, TPW_, kDecFast, 1, 1><<<grid, block, lds, s>>>(a, shift, gmask, \
+                                                                            x_dma, (int)I); \
+    *err = hipGetLastError();                                                              \
+    return true;                                                                           \
+  }
+  ZT_GU_CASE(4, 2) ZT_GU_CASE(8, 2) ZT_GU_CASE(14, 2) ZT_GU_CASE(16, 2)
+  ZT_GU_CASE(2, 4) ZT_GU_CASE(4, 4) ZT_GU_CASE(8, 4)
+#undef ZT_GU_CASE
+  return false;
+}
+
+// y[m][j] = silu(h[m][j]) * round_y(h[m][I + j]) for the fp32 [M, ld_h]
+// result h of the full gate_up linear (the two-step merged path)
+__global__ __launch_bounds__(256) void silu_mul_halves_kernel(const float *h, int64_t ld_h,
+                                                              int64_t M, int64_t I, void *y,
+                                                              int y_dt, int64_t ldy) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * I) return;
+  const int64_t m = idx / I, j = idx - m * I;
+  float u = h[m * ld_h + I + j];
+  if (y_dt == ZT_DT_BF16) u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+  store_elem(y, y_dt, m * ldy + j, unary_op(ZT_PO_SILU, h[m * ld_h + j]) * u);
+}
+
+hipError_t launch_silu_mul_halves(const float *h, int64_t ld_h, int64_t M, int64_t I, void *y,
+                                  int y_dt, int64_t ldy, hipStream_t s) {
+  if (M == 0 || I == 0) return hipSuccess;
+  const int64_t n = M * I;
+  silu_mul_halves_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(h, ld_h, M, I, y,
+                                                                                y_dt, ldy);
+  return hipGetLastError();
 }
 
 hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *workspace,

@@ -54,6 +54,10 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s);
 // The weight-streaming decode kernel for up to 64 rows, when it applies
 // (returns false otherwise; *err holds the launch status when it does).
 bool woq_try_stream(const WoqArgs &a, hipStream_t s, hipError_t *err);
+// merged gate_up (weight rows [0, N/2) gate, [N/2, N) up): y = silu(gate) * up
+bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err);
+hipError_t launch_silu_mul_halves(const float *h, int64_t ld_h, int64_t M, int64_t I, void *y,
+                                  int y_dt, int64_t ldy, hipStream_t s);
 // 17..64 rows: the wide weight-streaming kernel (bf16 x and scales, no
 // zero points), K split over `splits` workgroups per row block whose fp32
 // partials take woq_wide_workspace bytes of workspace.

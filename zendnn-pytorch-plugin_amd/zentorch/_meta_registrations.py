@@ -63,6 +63,15 @@ def meta_zentorch_woq_linear_silu_mul(input, weight, weight_scales, weight_zero_
     return _woq_out(input, weight)
 
 
+@register_meta("zentorch_woq_linear_gate_up_silu_mul")
+def meta_zentorch_woq_linear_gate_up_silu_mul(input, weight, weight_scales, weight_zero_points,
+                                              bias=None, zentorch_op_name=""):
+    # merged gate_up weight [K/8, 2I] -> output [*, I]
+    out = list(input.size())
+    out[-1] = weight.size(1) // 2
+    return input.new_empty(out)
+
+
 @register_meta("zentorch_dynamic_qlinear")
 def meta_zentorch_dynamic_qlinear(input, weight, weight_scales, bias=None,
                                   zentorch_op_name="zentorch::zentorch_dynamic_qlinear"):
