@@ -75,6 +75,8 @@ class WoqLinear:
             self.extra = torch.randn(M, N, generator=g).bfloat16().to(dev)
 
     def bytes(self):
+        if self.post == "gate_up":  # output [M, N/2]
+            return woq_bytes(self.M, self.N, self.K, self.G) - self.M * self.N
         return woq_bytes(self.M, self.N, self.K, self.G, n_bin=1 if self.extra is not None else 0)
 
     def __call__(self, i=0):
@@ -82,6 +84,8 @@ class WoqLinear:
         w, s = self.w[i % len(self.w)], self.s[i % len(self.s)]
         if self.post == "silu_mul":
             return ops.zentorch_woq_linear_silu_mul(self.x, w, s, None, self.extra)
+        if self.post == "gate_up":
+            return ops.zentorch_woq_linear_gate_up_silu_mul(self.x, w, s, None)
         if self.post == "add":
             return ops.zentorch_woq_linear_add(self.x, w, s, None, self.extra)
         return ops.zentorch_woq_linear(self.x, w, s, None)
@@ -186,20 +190,13 @@ def read_traffic():
 
 
 LLAMA = [("qkv", 6144, 4096, None), ("o", 4096, 4096, None),
-         ("gate_up", 14336, 4096, "silu_mul"), ("down", 4096, 14336, "add")]
+         ("gate_up", 28672, 4096, "gate_up"), ("down", 4096, 14336, "add")]
 
 
 def bench_decode_layer(M, args, gen):
-    # gate_up is modelled as its gate half [14336 x 4096] with the up half's
-    # product as the silu_mul multiplier, so the weight bytes per layer equal
-    # the fused [28672 x 4096] gate_up's half; both halves are timed by running
-    # the gate_up linear twice (once per half), as a merged-weight kernel would
-    # stream both halves.
-    layer = []
-    for name, N, K, post in LLAMA:
-        reps = 2 if name == "gate_up" else 1
-        for _ in range(reps):
-            layer.append(WoqLinear(M, N, K, post=post, copies=1, gen=gen))
+    # gate_up is the merged [28672 x 4096] weight with silu(gate) * up as its
+    # epilogue (zentorch_woq_linear_gate_up_silu_mul); down adds the residual.
+    layer = [WoqLinear(M, N, K, post=post, copies=1, gen=gen) for _, N, K, post in LLAMA]
     per_layer = sum(l.N * l.K // 2 + l.G * l.N * 2 for l in layer)
     ncopy = max(1, -(-ROTATE_BYTES // per_layer))
     layers = [layer] + [[WoqLinear(M, l.N, l.K, post=l.post, copies=1, gen=gen) for l in layer]
@@ -233,7 +230,7 @@ def bench_woq_prefill(args, gen):
     M = 2048
     lins = []
     for name, N, K, post in LLAMA:
-        lins.append(WoqLinear(M, N if name != "gate_up" else 2 * N, K, post=None, gen=gen))
+        lins.append(WoqLinear(M, N, K, post=None, gen=gen))
     calls = [lambda l=l: l() for l in lins]
     reps = max(1, args.steps // len(calls) + 1)
     t = graph_time(calls, reps, args.warmup)
