@@ -76,6 +76,13 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_woq_linear_silu_mul(
     AtenTensorHandle *weight_zero_points, AtenTensorHandle mul_input,
     AtenTensorHandle *B, const char *zentorch_op_name, AtenTensorHandle *ret0);
 
+/* No reference counterpart: shim of the zentorch_woq_linear_gate_up_silu_mul
+ * extension (merged gate_up weight, output silu(gate) * up). */
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_woq_linear_gate_up_silu_mul(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
+    AtenTensorHandle *weight_zero_points, AtenTensorHandle *B,
+    const char *zentorch_op_name, AtenTensorHandle *ret0);
+
 /* shim_cpu_zentorch.hpp:195-197 */
 AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear(
     AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,

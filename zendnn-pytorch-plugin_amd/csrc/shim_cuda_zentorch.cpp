@@ -85,6 +85,18 @@ AOTITorchError aoti_torch_cuda_zentorch_woq_linear_silu_mul(
   });
 }
 
+AOTITorchError aoti_torch_cuda_zentorch_woq_linear_gate_up_silu_mul(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
+    AtenTensorHandle *weight_zero_points, AtenTensorHandle *B, const char *zentorch_op_name,
+    AtenTensorHandle *ret0) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    auto r = zentorch_hip::woq_linear_gate_up_silu_mul(
+        ZT_T(X), ZT_T(W), ZT_T(weight_scales), ZT_OPT(weight_zero_points), ZT_OPT(B),
+        zentorch_op_name);
+    *ret0 = new_tensor_handle(std::move(r));
+  });
+}
+
 AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear(
     AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
     AtenTensorHandle *B, const char *zentorch_op_name, AtenTensorHandle *ret0) {
