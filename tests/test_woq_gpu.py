@@ -191,6 +191,15 @@ def test_stream_kernel_small_m_shapes(M, N, K):
     run_case(M, K, N, K // 128, seed=M + N + K, bias=True)
 
 
+# the general modes on the stream kernel (zero points, fp32 scales), with
+# their weight, scale and zero-point loads pipelined like the fast mode's
+@pytest.mark.parametrize("M", [1, 8, 16])
+@pytest.mark.parametrize("zp,s_dtype", [("int", torch.bfloat16), ("float", torch.bfloat16),
+                                        (None, torch.float32)])
+def test_stream_kernel_general_modes(M, zp, s_dtype):
+    run_case(M, 4096, 272, 32, zp=zp, s_dtype=s_dtype, seed=M + 31, bias=True)
+
+
 @pytest.mark.parametrize("M,N", [(10, 12816), (16, 12800)])
 def test_stream_kernel_four_tiles(M, N):
     # x [M, 4096] past 76 KB with at least 800 row tiles: four tiles per

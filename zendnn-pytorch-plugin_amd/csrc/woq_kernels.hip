@@ -363,9 +363,9 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // into slices of CPW 128-wide chunks.  The workgroup first starts the copy
 // of x [M, K] into LDS by DMA (when the rows are 16-byte aligned) and, in
 // the fast mode, of its rows' scales; then a wave issues the weight loads
-// of its slice's first chunks (TPW 16-byte fragments per lane per chunk):
-// all of them in the general modes, ZT_STREAM_DEPTH of them in the fast
-// mode, which issues chunk c + depth as it starts computing chunk c, so
+// of its slice's first chunks (TPW 16-byte fragments per lane per chunk,
+// with their scales and zero points in the general modes): ZT_STREAM_DEPTH
+// of them, issuing chunk c + depth as it starts computing chunk c, so
 // the buffer unit takes the later loads while the wave dequantises instead
 // of holding the wave in a long issue phase first.  A wave's loads retire
 // in issue order, so x (from L2) lands while its weights are still in
@@ -373,9 +373,9 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // columns past M repeat row M-1), A operands are the fragments dequantised
 // in registers.  K partials meet in LDS and are added in wave order.
 constexpr size_t kStreamLdsMax = 160 * 1024;
-// fast mode: chunks (per tile) of weights in flight per wave; the next one
-// is issued as each is computed (measured best of 2, 3, 4, 6, 8 and all at
-// once on the Llama-3 8B decode shapes)
+// chunks (per tile) of weights in flight per wave; the next one is issued
+// as each is computed (measured best of 2, 3, 4, 6, 8 and all at once on the
+// Llama-3 8B decode shapes)
 #ifndef ZT_STREAM_DEPTH
 #define ZT_STREAM_DEPTH 2
 #endif
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
     }
   };
   // the first D chunks now, chunk c + D when chunk c is computed
-  constexpr int D = (MODE == kDecFast && CPW > ZT_STREAM_DEPTH) ? ZT_STREAM_DEPTH : CPW;
+  constexpr int D = CPW > ZT_STREAM_DEPTH ? ZT_STREAM_DEPTH : CPW;
 #pragma unroll
   for (int c = 0; c < D; ++c) load_chunk(c);
 
@@ -583,7 +583,7 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
         slab[(((wv * TPW + t) * MT + mt) * 16 + 4 * lg + r) * 17 + lr] = acc[t][mt][r];
   __syncthreads();
   if (gu) {
-    constexpr int GT = TPW / 2;  // gate tiles of the workgroup
+    constexpr int GT = TPW / 2 > 0 ? TPW / 2 : 1;  // gate tiles (TPW is even here)
     const int j0 = blockIdx.x * GT * 16;
     for (int idx = tid; idx < GT * 16 * M; idx += 64 * NW) {
       const int m = idx / (GT * 16), jr = idx - m * (GT * 16);
