@@ -263,6 +263,12 @@ def test_stream_kernel_x_copy_paths(M, K):
     run_case(M, K, 96, K // 128, seed=M + K)
 
 
+@pytest.mark.parametrize("M", [9, 16])
+def test_stream_kernel_phases_k8192(M):
+    # K = 8192 with M > 9: two K phases of 32 chunks, 4 per wave
+    run_case(M, 8192, 208, 64, seed=M + 8192, bias=True)
+
+
 @pytest.mark.parametrize("M", [5, 8, 9, 16])
 @pytest.mark.parametrize("post,nbuf", [((), 0), (("add",), 1)])
 def test_stream_kernel_phases_down_shape(M, post, nbuf):

@@ -1369,7 +1369,9 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     *err = launch_stream_t<8, CPW_, 1, P_, MT_>(a, s, shift, gmask, mode);      \
     return true;                                                                \
   }
-      ZT_STREAM_PCASE(14, 2, 1) ZT_STREAM_PCASE(16, 2, 1) ZT_STREAM_PCASE(16, 4, 1)
+      // smallest CPW first, so that every wave has chunks in each phase
+      ZT_STREAM_PCASE(8, 2, 1) ZT_STREAM_PCASE(14, 2, 1) ZT_STREAM_PCASE(16, 2, 1)
+      ZT_STREAM_PCASE(16, 4, 1)
       ZT_STREAM_PCASE(4, 1, 2) ZT_STREAM_PCASE(4, 2, 2) ZT_STREAM_PCASE(16, 4, 2)
       ZT_STREAM_PCASE(4, 1, 4) ZT_STREAM_PCASE(4, 4, 4) ZT_STREAM_PCASE(8, 8, 4)
 #undef ZT_STREAM_PCASE
