@@ -421,15 +421,16 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   const auto w_rsrc = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
   const auto s_rsrc = make_rsrc(a.scales, (uint32_t)(a.G * N * s_bytes));
   // Phases (P > 1, when x [M, K] does not fit LDS): K splits into P ranges
-  // of CP chunks; x holds one range at a time.  Wave w owns chunks
-  // p * CP + w * CPWP + j (j < CPWP) of phase p; with P == 1 its chunks are
-  // the contiguous slice w * CPW + c.
+  // of CP chunks; x holds one range at a time.  Wave w owns the contiguous
+  // chunks [w*CP/NW, (w+1)*CP/NW) of each phase (with P == 1 of all C), so
+  // the waves' shares differ by at most one chunk; slots past the share
+  // are C, which loads zeros and computes nothing.
   constexpr int CPWP = CPW / P;
   const int CP = C / P;
+  const int lo = wv * CP / NW, len = (wv + 1) * CP / NW - lo;
   auto chunk_of = [&](int c) {
-    if (P == 1) return wv * CPW + c;
-    const int p = c / CPWP, kcl = wv * CPWP + (c - p * CPWP);
-    return kcl < CP ? p * CP + kcl : C;  // C: past the phase, reads zeros
+    const int p = P == 1 ? 0 : c / CPWP, j = c - p * CPWP;
+    return j < len ? p * CP + lo + j : C;
   };
 
   // 1. x [M, K] (or phase 0's range) -> LDS (row pitch XP bf16).  By DMA
