@@ -246,6 +246,22 @@ def test_gate_up_two_steps(M, K, I, G, zp, x_dtype):
     run_gate_up(M, K, I, G, seed=M + I, zp=zp, x_dtype=x_dtype)
 
 
+# one launch on the wide kernel (17-64 rows, no K split, N % 128 == 0):
+# forced with one K split at small shapes, and the Llama-3 8B gate_up shape
+# that takes it by default
+@pytest.mark.parametrize("M,K,I,G,bias", [
+    (17, 1024, 64, 8, True), (40, 2048, 192, 16, True), (64, 4096, 256, 32, False),
+    (33, 512, 128, 1, True), (12, 1024, 64, 8, True)])
+def test_gate_up_wide(M, K, I, G, bias, monkeypatch):
+    monkeypatch.setenv("ZT_WOQ_WIDE", "1")
+    run_gate_up(M, K, I, G, seed=M + K + I, bias=bias)
+
+
+@pytest.mark.parametrize("M", [17, 64])
+def test_gate_up_wide_llama(M):
+    run_gate_up(M, 4096, 14336, 32, seed=M)
+
+
 def test_gate_up_torch_op():
     import zentorch  # noqa: F401
     M, K, I, G = 4, 1024, 128, 8

@@ -342,6 +342,7 @@ int zt_woq_linear_gate_up(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
   if (zt::woq_try_stream_gate_up(a, s, &err)) return hip_status(err, op);
+  if (zt::woq_try_wide_gate_up(a, s, &err)) return hip_status(err, op);
   // two steps: the full [M, N] linear in fp32 into the workspace, then
   // silu(gate) * up over its halves
   const size_t h = ((size_t)M * (size_t)N * sizeof(float) + 255) / 256 * 256;

@@ -1455,7 +1455,7 @@ constexpr size_t woq_wide_lds() {
 
 template <int MT>
 __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int cpg_shift, int gmask,
-                                                       float *partial) {
+                                                       float *partial, int gu) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int XB = 32 * MT * 1024;  // one x phase buffer
   constexpr int XL = 4 * MT;          // x rows (one load each) per wave per phase
@@ -1469,6 +1469,10 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
   const int ldx2 = (int)a.ldx * 2;
   const int n0 = blockIdx.x * kWideRows;
   const int ph0 = blockIdx.y * pps;  // first phase of this K split
+  // merged gate_up (gu = N/2, a multiple of 64): local rows [0, 64) are gate
+  // rows j0.., local rows [64, 128) the up rows gu + j0..
+  const int j0 = blockIdx.x * (kWideRows / 2);
+  auto row_of = [&](int r) { return gu ? (r < 64 ? j0 + r : gu + j0 + r - 64) : n0 + r; };
 
   const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * ldx2 + (int64_t)K * 2));
   const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
@@ -1476,7 +1480,7 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
 
   // the lane's two load rows (rows past N read zeros, scales past N zeros
   // or another group's; their outputs are never stored)
-  const int r_lo = n0 + rw * 32 + lr, r_hi = r_lo + 16;
+  const int r_lo = row_of(rw * 32 + lr), r_hi = row_of(rw * 32 + lr + 16);
   const uint32_t off_lo = (uint32_t)r_lo * (uint32_t)KW * 4u + 16u * lg;
   const uint32_t off_hi = (uint32_t)r_hi * (uint32_t)KW * 4u + 16u * lg;
 
@@ -1507,7 +1511,7 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
       const uint32_t g = ((uint32_t)(ph * 4 + wv) >> cpg_shift) & (uint32_t)gmask;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           s_rs, (lds_ptr_t)(sbuf0 + ((ph & 1) * 4 + wv) * (kWideRows * 2)), 4,
-          ((g * (uint32_t)N + (uint32_t)n0) * 2u + (uint32_t)lane * 4u) | oob, 0, 0, 0);
+          ((g * (uint32_t)N + (uint32_t)row_of(2 * lane)) * 2u) | oob, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
@@ -1599,7 +1603,30 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
               f32x4_t{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
     }
     __syncthreads();
-    if (tid < 256) woq_tile_epilogue<32 * MT, kWideRows>(a, tile, 0, n0, tid);
+    if (tid >= 256) return;
+    if (gu) {
+      // y[m][j] = silu(gate + bias[j]) * (up + bias[gu + j]), the up value
+      // rounded to y's bf16 first (the unfused op's bf16 up output)
+      for (int idx = tid; idx < 32 * MT * 16; idx += 256) {
+        const int m = idx >> 4, c4 = (idx & 15) * 4;
+        if (m >= M) continue;
+        const f32x4_t g4 = *reinterpret_cast<const f32x4_t *>(tile + m * TP + c4);
+        const f32x4_t u4 = *reinterpret_cast<const f32x4_t *>(tile + m * TP + 64 + c4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = j0 + c4 + r;
+          float g = g4[r], u = u4[r];
+          if (a.bias) {
+            g = g + load_elem(a.bias, a.b_dt, j);
+            u = u + load_elem(a.bias, a.b_dt, gu + j);
+          }
+          if (a.y_dt == ZT_DT_BF16) u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+          store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + j, unary_op(ZT_PO_SILU, g) * u);
+        }
+      }
+      return;
+    }
+    woq_tile_epilogue<32 * MT, kWideRows>(a, tile, 0, n0, tid);
     return;
   }
   if (kh != 0) return;
@@ -1719,15 +1746,39 @@ hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace,
     std::fprintf(stderr, "[zt] woq wide M=%lld N=%lld K=%lld: MT=%d splits=%d phases/split=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, p.mt, p.splits, p.pps);
   if (p.mt == 1)
-    woq_wide_kernel<1><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial);
+    woq_wide_kernel<1><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial, 0);
   else
-    woq_wide_kernel<2><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial);
+    woq_wide_kernel<2><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial, 0);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const int64_t n4 = a.M * (a.N / 4);
   woq_splitk_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(a, partial,
                                                                                    p.splits);
   return hipGetLastError();
+}
+
+// Merged gate_up on the wide kernel: one launch writes silu(gate) * up,
+// workgroup b computing gate rows [64b, 64b + 64) and the matching up rows.
+// Taken when the wide kernel would run the full [M, N] linear without a K
+// split and N/2 is a multiple of 64; otherwise returns false.
+bool woq_try_wide_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
+  WidePlan p;
+  if (a.N % (2 * 64) || a.post.count != 0 || !woq_wide_ok(a, &p) || p.splits != 1) return false;
+  const int64_t cpg = a.G == 1 ? 0 : (a.K / a.G) / 128;
+  int shift = 0;
+  while (cpg > 1 && (1 << shift) < cpg) ++shift;
+  const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  const int gu = (int)(a.N / 2);
+  const dim3 grid((unsigned)(a.N / kWideRows), 1u);
+  if (std::getenv("ZT_WOQ_DEBUG"))
+    std::fprintf(stderr, "[zt] woq wide gate_up M=%lld N=%lld K=%lld: MT=%d\n", (long long)a.M,
+                 (long long)a.N, (long long)a.K, p.mt);
+  if (p.mt == 1)
+    woq_wide_kernel<1><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, nullptr, gu);
+  else
+    woq_wide_kernel<2><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, nullptr, gu);
+  *err = hipGetLastError();
+  return true;
 }
 
 // The stream kernel for a call of up to 64 rows whose shape the decode

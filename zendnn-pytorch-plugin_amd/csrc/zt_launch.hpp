@@ -70,6 +70,8 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p);
 size_t woq_wide_workspace(const WidePlan &p, int64_t M, int64_t N);
 bool woq_wide_ok(const WoqArgs &a, WidePlan *p);
 hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace, hipStream_t s);
+// merged gate_up on the wide kernel (no K split, N % 128 == 0)
+bool woq_try_wide_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err);
 
 hipError_t launch_repack(const int8_t *w, int64_t N, int64_t K, int32_t *out,
                          hipStream_t s);
