@@ -137,21 +137,62 @@ def graph_time(calls, reps, warmup):
     return t0.elapsed_time(t1) / 1e3 / reps
 
 
+def capture(calls):
+    """A HIP graph of `calls` (run once first on the capture stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    return g
+
+
 def copies_for(bytes_per_copy):
     return max(1, min(64, -(-ROTATE_BYTES // bytes_per_copy)))
 
 
 def bench_config0(args, gen):
+    """Exactly args.steps calls in one timed graph replay.
+
+    Call i of the timed graph uses weight copy i % 64 (64 copies = 557 MB,
+    more than the 256 MB Infinity Cache).  Before the timed replay: W eager
+    warm-up calls, one untimed replay of the same graph (its first launch),
+    then a replay of a graph over the other copies, so the timed calls read
+    their weights from HBM even when fewer than 64 steps are timed.  The
+    timed replay is bracketed by device synchronisation and by HIP events on
+    the replay stream (the graph's single kernel per call makes the per-call
+    time the kernel's launch-to-launch duration)."""
     M, N, K = 4, 4096, 4096
-    per = N * K // 2 + (K // 128) * N * 2
-    lin = WoqLinear(M, N, K, copies=copies_for(per), gen=gen)
-    calls = [lambda i=i: lin(i) for i in range(len(lin.w))]
-    reps = max(1, args.steps // len(calls))
-    t_step = graph_time(calls, reps, args.warmup) / len(calls)
+    ncopy = 64
+    lin = WoqLinear(M, N, K, copies=ncopy, gen=gen)
+    steps = max(1, args.steps)
+    for i in range(args.warmup):
+        lin(ncopy - 1 - i % ncopy)
+    timed = capture([lambda i=i: lin(i % ncopy) for i in range(steps)])
+    others = [i for i in range(steps, ncopy)]
+    flush = capture([lambda i=i: lin(i) for i in others]) if others else None
+    timed.replay()
+    if flush is not None:
+        flush.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    timed.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    t_step = t0.elapsed_time(t1) / 1e3 / steps
     b = lin.bytes()
     return {"M": M, "N": N, "K": K, "G": K // 128, "bytes_per_call": b,
             "s_per_call": t_step, "GBps": b / t_step / 1e9,
-            "copies": len(lin.w), "calls_timed": reps * len(calls)}
+            "copies": ncopy, "calls_timed": steps}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "woq_decode_config0_traffic.txt")
@@ -193,6 +234,12 @@ LLAMA = [("qkv", 6144, 4096, None), ("o", 4096, 4096, None),
          ("gate_up", 28672, 4096, "gate_up"), ("down", 4096, 14336, "add")]
 
 
+# Secondary workloads: each is timed over SECONDARY_REPS replays of one graph
+# (after `warmup` replays) and reports the calls it timed; --steps applies to
+# the headline workload only.
+SECONDARY_REPS = 10
+
+
 def bench_decode_layer(M, args, gen):
     # gate_up is the merged [28672 x 4096] weight with silu(gate) * up as its
     # epilogue (zentorch_woq_linear_gate_up_silu_mul); down adds the residual.
@@ -202,12 +249,12 @@ def bench_decode_layer(M, args, gen):
     layers = [layer] + [[WoqLinear(M, l.N, l.K, post=l.post, copies=1, gen=gen) for l in layer]
                         for _ in range(ncopy - 1)]
     calls = [lambda l=l: l() for lay in layers for l in lay]
-    reps = max(1, args.steps // len(calls) + 1)
-    t_pass = graph_time(calls, reps, args.warmup)
+    t_pass = graph_time(calls, SECONDARY_REPS, args.warmup)
     b = sum(l.bytes() for lay in layers for l in lay)
     t_layer = t_pass / len(layers)
     return {"M": M, "layer_bytes": b // len(layers), "s_per_layer": t_layer,
-            "GBps": b / t_pass / 1e9, "layer_copies": len(layers)}
+            "GBps": b / t_pass / 1e9, "frac_hbm": b / t_pass / 1e9 / HBM_PEAK_GBS,
+            "layer_copies": len(layers), "calls_timed": SECONDARY_REPS * len(calls)}
 
 
 def bench_dyn(M, shapes, args, gen):
@@ -217,13 +264,14 @@ def bench_dyn(M, shapes, args, gen):
         lins.append(DynLinear(M, N, K, copies=1 if M >= 1024 else copies_for(per) // len(shapes) or 1,
                               gen=gen))
     calls = [lambda l=l, i=i: l(i) for l in lins for i in range(len(l.w))]
-    reps = max(1, args.steps // len(calls) + 1)
-    t = graph_time(calls, reps, args.warmup)
+    t = graph_time(calls, SECONDARY_REPS, args.warmup)
     ops = sum(2 * l.M * l.N * l.K * len(l.w) for l in lins)
     b = sum(l.bytes() * len(l.w) for l in lins)
-    return {"M": M, "shapes": shapes, "s_per_pass": t, "TOPS": ops / t / 1e12,
-            "frac_int8_peak": ops / t / 1e12 / INT8_PEAK_TOPS, "GBps": b / t / 1e9,
-            "frac_hbm": b / t / 1e9 / HBM_PEAK_GBS}
+    return {"M": M, "shapes": shapes, "s_per_pass": t, "s_per_call": t / len(calls),
+            "TOPS": ops / t / 1e12, "frac_int8_peak": ops / t / 1e12 / INT8_PEAK_TOPS,
+            "GBps": b / t / 1e9, "frac_hbm": b / t / 1e9 / HBM_PEAK_GBS,
+            "ops_per_pass": ops, "bytes_per_pass": b,
+            "calls_timed": SECONDARY_REPS * len(calls)}
 
 
 def bench_woq_prefill(args, gen):
@@ -232,11 +280,11 @@ def bench_woq_prefill(args, gen):
     for name, N, K, post in LLAMA:
         lins.append(WoqLinear(M, N, K, post=None, gen=gen))
     calls = [lambda l=l: l() for l in lins]
-    reps = max(1, args.steps // len(calls) + 1)
-    t = graph_time(calls, reps, args.warmup)
+    t = graph_time(calls, SECONDARY_REPS, args.warmup)
     flops = sum(2 * l.M * l.N * l.K for l in lins)
     return {"M": M, "s_per_layer": t, "TFLOPS": flops / t / 1e12,
-            "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS}
+            "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS, "flops_per_layer": flops,
+            "calls_timed": SECONDARY_REPS * len(calls)}
 
 
 def bench_moe(args, gen):
@@ -264,52 +312,143 @@ def bench_moe(args, gen):
     out = torch.empty_like(x)
     call = lambda: ops.zentorch_fused_moe(out, x, w13, w2, None, None, wts, ids, False,
                                           "silu", s13, s2)
-    reps = max(2, args.steps // 64)
-    t = graph_time([call], reps, args.warmup)
+    t = graph_time([call], SECONDARY_REPS, args.warmup)
     wbytes = E * (2 * I * H // 2 + H * I // 2) + E * (H // 128 * 2 * I + I // 128 * H) * 2
     byts = wbytes + T * H * 2 * 2
     flops = 2 * T * k * (2 * I * H + H * I)
     return {"T": T, "H": H, "I": I, "E": E, "topk": k, "s_per_layer": t,
             "GBps": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / HBM_PEAK_GBS,
             "TFLOPS": flops / t / 1e12, "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS,
-            "weight_bytes": wbytes}
+            "weight_bytes": wbytes, "bytes_per_layer": byts, "calls_timed": SECONDARY_REPS}
 
 
-def cpu_baseline(budget_s=12.0):
-    """CPU oracle (port of the reference semantics) on config 0's shape."""
+# ------------------------------------------------------------ CPU baseline
+# The reference's CPU path (zentorch on ZenDNNL) cannot be built offline, so
+# the baseline is the oracle (oracle/zt_oracle.c, the port of the
+# reference's semantics, OpenMP) plus stock-torch CPU equivalents of the two
+# ops.  It runs in a child process (no GPU use there) started with
+# OMP_PROC_BIND=close and OMP_PLACES=cores, so the OpenMP threads are pinned
+# one per physical core from the start.
+CPU_THREAD_CAP = 16  # the CPU share of one GPU on the benchmark boxes
+
+
+def cpu_topology():
+    """(model name, physical cores of the largest socket, all physical
+    cores) over the CPUs this process may run on."""
+    import subprocess
+    allowed = os.sched_getaffinity(0)
+    model, cores = "unknown CPU", {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for ln in out.splitlines():
+            if ln.startswith("Model name:"):
+                model = ln.split(":", 1)[1].strip()
+        out = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], capture_output=True,
+                             text=True).stdout
+        for ln in out.splitlines():
+            if ln.startswith("#"):
+                continue
+            cpu, core, sock = (int(v) for v in ln.split(",")[:3])
+            if cpu in allowed:
+                cores.setdefault(sock, set()).add(core)
+    except (OSError, ValueError):
+        pass
+    if not cores:
+        return model, len(allowed), len(allowed)
+    per_socket = max(len(c) for c in cores.values())
+    return model, per_socket, sum(len(c) for c in cores.values())
+
+
+def _median_time(fn, budget_s, max_calls=20):
+    for _ in range(3):  # the first calls may reorder or cache weights
+        fn()
+    times, t0 = [], time.perf_counter()
+    while len(times) < max_calls and (time.perf_counter() - t0 < budget_s or len(times) < 5):
+        a = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - a) / 1e9)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline_child(threads):
+    """Runs in the pinned child: config 0 (M=4, N=K=4096, G=32) and config 1
+    (M=128, N=11008, K=4096) on `threads` threads.  Prints one JSON line."""
     from oracle import oracle as O
+    torch.set_num_threads(threads)
+    res = {"threads": threads}
     g = torch.Generator().manual_seed(0)
     M, N, K = 4, 4096, 4096
     x = torch.randn(M, K, generator=g).bfloat16()
     q = torch.randint(-8, 8, (N, K), generator=g, dtype=torch.int8)
-    wp = O.woq_repack_weight(q)
     s = (torch.rand(K // 128, N, generator=g) * 0.015 + 0.005).bfloat16()
-    threads = O.max_threads()
-    for _ in range(3):
-        O.woq_linear(x, wp, s)
-    n, t0 = 0, time.perf_counter()
-    times = []
-    while time.perf_counter() - t0 < budget_s and n < 200:
-        a = time.perf_counter_ns()
-        O.woq_linear(x, wp, s)
-        times.append((time.perf_counter_ns() - a) / 1e9)
-        n += 1
-    times.sort()
-    med = times[len(times) // 2]
-    model = "unknown CPU"
+    wp = O.woq_repack_weight(q)
+    b0 = woq_bytes(M, N, K, K // 128)
+    t, n = _median_time(lambda: O.woq_linear(x, wp, s, nthreads=threads), 6.0)
+    res["oracle_config0"] = {"s": t, "calls": n, "GBps": b0 / t / 1e9}
+    # stock torch: tinygemm int4pack with u4 = q + 8 and zero point 0 in the
+    # float-zero-point convention w = (u - 8) * s + 0
     try:
-        with open("/proc/cpuinfo") as f:
-            for ln in f:
-                if ln.startswith("model name"):
-                    model = ln.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": woq_bytes(M, N, K, K // 128) / med / 1e9, "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle/zt_oracle.c zto_woq_linear on config 0 (M=4,N=K=4096,G=32), "
-                      f"median of {n} calls after 3 warm-up, {threads} OpenMP threads, "
-                      f"same algorithmic-bytes formula, host CPU: {model}"}
+        u = (q.int() + 8).to(torch.int32)
+        packed = torch.ops.aten._convert_weight_to_int4pack_for_cpu(u, 1)
+        sz = torch.stack([s.t().contiguous(), torch.zeros_like(s.t())], dim=-1)
+        sz = sz.transpose(0, 1).contiguous()  # [G, N, 2]
+        fn = lambda: torch.ops.aten._weight_int4pack_mm_for_cpu(x, packed, 128, sz)
+        t, n = _median_time(fn, 6.0)
+        res["torch_int4pack_config0"] = {"s": t, "calls": n, "GBps": b0 / t / 1e9}
+    except Exception as e:  # noqa: BLE001 - an unavailable stock kernel is reported, not fatal
+        res["torch_int4pack_config0"] = {"error": str(e)[:200]}
+    M, N, K = 128, 11008, 4096
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.rand(N, generator=g) * 0.009 + 0.001
+    bias = (torch.randn(N, generator=g) * 0.1).bfloat16()
+    ops1 = 2 * M * N * K
+    t, n = _median_time(lambda: O.dynamic_qlinear(x, w, sw, bias, nthreads=threads), 6.0, 10)
+    res["oracle_config1"] = {"s": t, "calls": n, "TOPS": ops1 / t / 1e12,
+                             "GBps": dyn_bytes(M, N, K) / t / 1e9}
+    wt = w.t().contiguous()
+
+    def int_mm_path():
+        xf = x.float()
+        sx = xf.abs().amax(dim=1, keepdim=True).clamp(min=1e-12) / 127.0
+        qx = torch.clamp(torch.round(xf / sx), -128, 127).to(torch.int8)
+        acc = torch._int_mm(qx, wt)
+        return (acc.float() * sx * sw + bias.float()).bfloat16()
+
+    t, n = _median_time(int_mm_path, 6.0, 10)
+    res["torch_int_mm_config1"] = {"s": t, "calls": n, "TOPS": ops1 / t / 1e12,
+                                   "GBps": dyn_bytes(M, N, K) / t / 1e9}
+    print(json.dumps(res), flush=True)
+
+
+def cpu_baseline():
+    import subprocess
+    model, per_socket, all_cores = cpu_topology()
+    p_sock = max(1, min(per_socket, CPU_THREAD_CAP))
+    p_all = max(1, min(all_cores, CPU_THREAD_CAP))
+    env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
+    runs = {}
+    for label, p in (("one_socket", p_sock), ("all_cores", p_all)):
+        if label == "all_cores" and p == p_sock:
+            runs[label] = "same thread count as one_socket (capped at the GPU's CPU share)"
+            continue
+        out = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-baseline-child",
+                              str(p)], env=env, capture_output=True, text=True, timeout=300)
+        line = [l for l in out.stdout.splitlines() if l.startswith("{")]
+        runs[label] = json.loads(line[-1]) if line else {"error": out.stderr[-400:]}
+    main = runs["one_socket"]
+    c0 = main.get("oracle_config0", {})
+    return {"value": round(c0["GBps"], 3) if "GBps" in c0 else None, "unit": "GB/s",
+            "cores": p_sock, "kind": "port",
+            "sample": f"oracle/zt_oracle.c zto_woq_linear on config 0 (M=4, N=K=4096, G=32), "
+                      f"median of {c0.get('calls')} calls after 3 warm-up, {p_sock} OpenMP threads "
+                      f"pinned one per physical core (OMP_PROC_BIND=close, OMP_PLACES=cores); "
+                      f"host CPU: {model}, {per_socket} physical cores per socket, "
+                      f"{all_cores} in this process's CPU set, threads capped at "
+                      f"{CPU_THREAD_CAP}; zentorch's own CPU path unavailable (needs ZenDNNL, "
+                      f"not buildable offline)",
+            "cpu_model": model, "runs": runs}
 
 
 def main():
@@ -320,7 +459,11 @@ def main():
     ap.add_argument("--only", default=None,
                     help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | moe | traffic")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-baseline-child", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_baseline_child:
+        cpu_baseline_child(args.cpu_baseline_child)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
         sys.exit(2)
@@ -369,11 +512,69 @@ def main():
                             "traffic": read_traffic(),
                             "kernel": "woq_stream_kernel",
                             "kernel_avg_us": round(c0["s_per_call"] * 1e6, 3),
+                            "rocprof_kernel_avg_us": read_profile_avg(CONFIG0_TRACE_FILE),
                             "algorithmic_bytes": c0["bytes_per_call"]}
+    line["rooflines"] = secondary_rooflines(res)
     if not args.no_cpu_baseline and only in (None, "config0"):
         line["cpu_baseline"] = cpu_baseline()
     line["workloads"] = res
     print(json.dumps(line), flush=True)
+
+
+def secondary_rooflines(res):
+    """Roofline entries of the other BASELINE configs: achieved = algorithmic
+    work per call / per-call time from HIP events around graph replays (the
+    op's kernels back to back; `kernels` names them)."""
+    out = []
+    d = res.get("dyn_qlinear_m128")
+    if d:
+        out.append({"workload": "config 1: zentorch_dynamic_qlinear M=128 N=11008 K=4096",
+                    "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(d["frac_hbm"], 4),
+                    "achieved_tops": round(d["TOPS"], 2), "frac_int8_peak": round(d["frac_int8_peak"], 4),
+                    "kernels": "dyn_quantize_bf16_kernel + s8_skinny32_kernel",
+                    "op_avg_us": round(d["s_per_call"] * 1e6, 3)})
+    d = res.get("prefill_int8_m2048")
+    if d:
+        out.append({"workload": "config 3 int8: dynamic qlinear over the Llama-3-8B layer, M=2048",
+                    "bound": "mfma", "achieved": round(d["TOPS"], 2), "peak": INT8_PEAK_TOPS,
+                    "unit": "TOP/s", "frac": round(d["frac_int8_peak"], 4),
+                    "kernels": "dyn_quantize_bf16_kernel + s8_gemm32_kernel",
+                    "layer_avg_us": round(d["s_per_pass"] * 1e6, 3)})
+    d = res.get("prefill_int4_m2048")
+    if d:
+        out.append({"workload": "config 3 int4: WOQ linear over the Llama-3-8B layer, M=2048",
+                    "bound": "mfma", "achieved": round(d["TFLOPS"], 2), "peak": BF16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(d["frac_bf16_peak"], 4),
+                    "kernels": "woq_gemm32_kernel", "layer_avg_us": round(d["s_per_layer"] * 1e6, 3)})
+    for d in res.get("decode_layer", []):
+        out.append({"workload": f"config 2: Llama-3-8B decode layer, M={d['M']}",
+                    "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(d["frac_hbm"], 4),
+                    "layer_avg_us": round(d["s_per_layer"] * 1e6, 3)})
+    d = res.get("moe_mixtral_t256")
+    if d:
+        out.append({"workload": "config 4: Mixtral int4 MoE FFN, 256 tokens, top-2",
+                    "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(d["frac_hbm"], 4),
+                    "kernels": "moe_route + woq_moe_gemm x2 + moe_combine",
+                    "layer_avg_us": round(d["s_per_layer"] * 1e6, 3)})
+    return out
+
+
+CONFIG0_TRACE_FILE = os.path.join(ROOT, "profiles", "woq_decode_config0_kernel_trace.txt")
+
+
+def read_profile_avg(path):
+    """'profile_avg_us: <float>' from a committed rocprof summary, or None."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("profile_avg_us:"):
+                    return float(ln.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 if __name__ == "__main__":

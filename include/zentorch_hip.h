@@ -221,6 +221,22 @@ size_t zt_woq_moe_workspace_size(int64_t T, int64_t H, int64_t topk, int64_t E,
 /* Message of the calling thread's last failed call ("" if none). */
 const char *zt_last_error_string(void);
 
+/*
+ * Kernel-selection overrides, for tests and tuning.  No counterpart in the
+ * reference (its EnvReader, src/cpu/cpp/EnvReader.hpp, reads ZenDNN's own
+ * variables on every call).  Each knob is named after the environment
+ * variable that sets it when the library is loaded (ZT_WOQ_FORCE_KERNEL,
+ * ZT_WOQ_DECODE_PLAN, ZT_WOQ_STREAM, ZT_WOQ_WIDE, ZT_WOQ_GEMM, ZT_WOQ_DEBUG,
+ * ZT_S8_SKINNY32, ZT_S8_SKINNY, ZT_S8_FRAG, ZT_S8_FORCE, ZT_S8_TILE,
+ * ZT_S8_KIND, ZT_MOE_BN); the environment is not read again.  value NULL or
+ * "" unsets the knob.  Returns ZT_EINVAL for an unknown name.  Launches
+ * already enqueued are not affected.
+ */
+int zt_set_tuning(const char *name, const char *value);
+
+/* Current value of a knob (NULL if unset or unknown). */
+const char *zt_get_tuning(const char *name);
+
 /* Library ABI version (major*10000 + minor*100 + patch). */
 int32_t zt_version(void);
 

@@ -22,3 +22,29 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+class _Knobs:
+    """Test fixture: set library tuning knobs, restored when the test ends."""
+
+    def __init__(self):
+        self._saved = {}
+
+    def set(self, name, value):
+        import zt_capi as C
+        if name not in self._saved:
+            self._saved[name] = C.get_tuning(name)
+        C.set_tuning(name, value)
+
+    def restore(self):
+        import zt_capi as C
+        for k, v in self._saved.items():
+            C.set_tuning(k, v)
+        self._saved.clear()
+
+
+@pytest.fixture
+def knobs():
+    k = _Knobs()
+    yield k
+    k.restore()

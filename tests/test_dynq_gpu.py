@@ -125,11 +125,11 @@ def test_dynamic_qlinear_fragment_kernel(M, K, N, x_dtype):
 @pytest.mark.parametrize("M,shape", [(20, "4,4,8"), (40, "4,2,8"), (64, "3,2,8"), (90, "2,2,8"),
                                      (128, "4,2,8"), (128, "3,4,4"), (97, "4,4,4"),
                                      (1, None), (9, None), (16, None)])
-def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, monkeypatch):
+def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, knobs):
     K, N = 1344, 232
     if shape:
-        monkeypatch.setenv("ZT_S8_SKINNY32", shape)
-    monkeypatch.setenv("ZT_S8_FRAG", "1")
+        knobs.set("ZT_S8_SKINNY32", shape)
+    knobs.set("ZT_S8_FRAG", "1")
     x, w, sw, b = make(M, K, N, seed=M + 5)
     y_ref = O.dynamic_qlinear(x, w, sw, b)
     y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV)).cpu()

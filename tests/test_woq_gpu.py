@@ -24,8 +24,6 @@ TOL = dict(rtol=1e-2, atol=1e-2)
 @pytest.fixture(autouse=True)
 def _announce(request):
     print(f"\n[case] {request.node.name}", flush=True)
-    yield
-    os.environ.pop("ZT_WOQ_FORCE_KERNEL", None)
 
 
 def make_case(M, K, N, G, seed, zp=None, bias=False, s_dtype=torch.bfloat16,
@@ -62,15 +60,8 @@ def run_case(M, K, N, G, kernel=None, seed=0, post=(), nbuf=0, **kw):
     bufs = [torch.randn(M, N, generator=g).to(x.dtype) for _ in range(nbuf)]
     y_ref = O.woq_linear(x, wp, s, zero_points=z, bias=b, post_ops=post, post_bufs=bufs)
     xd, wd, sd, zd, bd = gpu(x, wp, s, z, b)
-    saved = os.environ.pop("ZT_WOQ_FORCE_KERNEL", None)
-    if kernel:
-        os.environ["ZT_WOQ_FORCE_KERNEL"] = kernel
-    try:
+    with C.tuning(ZT_WOQ_FORCE_KERNEL=kernel):
         y = C.woq_linear(xd, wd, sd, zd, bd, post_ops=post, post_bufs=gpu(*bufs))
-    finally:
-        os.environ.pop("ZT_WOQ_FORCE_KERNEL", None)
-        if saved is not None:
-            os.environ["ZT_WOQ_FORCE_KERNEL"] = saved
     check_close(y, y_ref)
     return y, y_ref
 
@@ -119,8 +110,8 @@ def test_wide_kernel_vs_oracle(M, K, N, G):
 @pytest.mark.parametrize("splits", ["1", "2", "4"])
 @pytest.mark.parametrize("post,nbuf", [(("gelu_tanh",), 0), (("mul", "add"), 2),
                                        (("silu", "mul"), 1)])
-def test_wide_kernel_post_ops_and_splits(splits, post, nbuf, monkeypatch):
-    monkeypatch.setenv("ZT_WOQ_WIDE", splits)
+def test_wide_kernel_post_ops_and_splits(splits, post, nbuf, knobs):
+    knobs.set("ZT_WOQ_WIDE", splits)
     run_case(40, 2048, 264, 16, kernel="wide", post=post, nbuf=nbuf, seed=21, bias=True)
 
 
@@ -248,13 +239,22 @@ def test_gate_up_two_steps(M, K, I, G, zp, x_dtype):
 
 # one launch on the wide kernel (17-64 rows, no K split, N % 128 == 0):
 # forced with one K split at small shapes, and the Llama-3 8B gate_up shape
-# that takes it by default
+# that takes it by default.  The 12-row case has x [12, 8192] (196 KB),
+# more than the stream kernel's LDS holds, so the stream gate_up refuses it
+# and the wide kernel runs it below 17 rows.
 @pytest.mark.parametrize("M,K,I,G,bias", [
     (17, 1024, 64, 8, True), (40, 2048, 192, 16, True), (64, 4096, 256, 32, False),
-    (33, 512, 128, 1, True), (12, 1024, 64, 8, True)])
-def test_gate_up_wide(M, K, I, G, bias, monkeypatch):
-    monkeypatch.setenv("ZT_WOQ_WIDE", "1")
+    (33, 512, 128, 1, True), (12, 8192, 64, 64, True)])
+def test_gate_up_wide(M, K, I, G, bias, knobs):
+    knobs.set("ZT_WOQ_WIDE", "1")
     run_gate_up(M, K, I, G, seed=M + K + I, bias=bias)
+
+
+@pytest.mark.parametrize("M", [9, 12, 16])
+def test_wide_kernel_below_17_rows(M, knobs):
+    # the plain linear on the wide kernel at 9-16 rows (one K split)
+    knobs.set("ZT_WOQ_WIDE", "1")
+    run_case(M, 8192, 384, 64, kernel="wide", seed=M + 3, bias=True)
 
 
 @pytest.mark.parametrize("M", [17, 64])

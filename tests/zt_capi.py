@@ -1,6 +1,7 @@
 """ctypes binding of libzentorch_hip.so's C-ABI (include/zentorch_hip.h) for
 the tests: GPU tensors go in as raw device pointers with sizes and the
 current torch stream, exactly as a non-torch caller would pass them."""
+import contextlib
 import ctypes
 import os
 
@@ -59,6 +60,10 @@ def lib():
         L.zt_woq_moe_workspace_size.argtypes = [_i64, _i64, _i64, _i64, _i64]
         L.zt_woq_moe_workspace_size.restype = _sz
         L.zt_last_error_string.restype = ctypes.c_char_p
+        L.zt_set_tuning.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
+        L.zt_set_tuning.restype = ctypes.c_int
+        L.zt_get_tuning.argtypes = [ctypes.c_char_p]
+        L.zt_get_tuning.restype = ctypes.c_char_p
         L.zt_version.restype = ctypes.c_int32
         _lib = L
     return _lib
@@ -75,6 +80,30 @@ def _stream():
 def _check(rc):
     if rc != 0:
         raise RuntimeError(f"C-ABI error {rc}: {lib().zt_last_error_string().decode()}")
+
+
+def set_tuning(name, value):
+    """Set a kernel-selection knob of the library (None unsets it)."""
+    v = None if value is None else str(value).encode()
+    _check(lib().zt_set_tuning(name.encode(), v))
+
+
+def get_tuning(name):
+    v = lib().zt_get_tuning(name.encode())
+    return None if v is None else v.decode()
+
+
+@contextlib.contextmanager
+def tuning(**knobs):
+    """Set knobs for the duration of a with-block, then restore them."""
+    saved = {k: get_tuning(k) for k in knobs}
+    try:
+        for k, v in knobs.items():
+            set_tuning(k, v)
+        yield
+    finally:
+        for k, v in saved.items():
+            set_tuning(k, v)
 
 
 def make_post(post_ops, bufs, N):

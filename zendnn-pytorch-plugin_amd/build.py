@@ -56,11 +56,13 @@ def _torch_flags():
     libdir = os.path.join(os.path.dirname(torch.__file__), "lib")
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     cflags = ["-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
-              f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-I" + INCLUDE, "-I" + CSRC]
+              f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-I" + INCLUDE, "-I" + CSRC,
+              "-I" + os.path.join(ROCM, "include")]
     cflags += ["-I" + i for i in incs]
     ldflags = ["-L" + libdir, "-Wl,-rpath," + libdir, "-lc10", "-lc10_hip",
                "-ltorch_cpu", "-ltorch_hip", "-ltorch", "-L" + PKG, "-lzentorch_hip",
-               "-Wl,-rpath,$ORIGIN", "-L" + os.path.join(ROCM, "lib"), "-lamdhip64"]
+               "-Wl,-rpath,$ORIGIN", "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
+               "-lrocprofiler-sdk-roctx"]
     return cflags, ldflags
 
 

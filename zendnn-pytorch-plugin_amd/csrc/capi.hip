@@ -1,13 +1,19 @@
 // extern "C" entry points of libzentorch_hip.so (declared in
 // include/zentorch_hip.h): argument validation, kernel choice, launch.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <memory>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include <algorithm>
 
 #include "zt_launch.hpp"
+#include "zt_tuning.hpp"
 
 namespace {
 
@@ -98,9 +104,63 @@ hipError_t woq_row_blocks(const zt::WoqArgs &a, hipStream_t s) {
 
 }  // namespace
 
+// ------------------------------------------------------------ tuning knobs
+namespace zt {
+namespace {
+
+constexpr const char *kKnobNames[kKnobCount] = {
+    "ZT_WOQ_FORCE_KERNEL", "ZT_WOQ_DECODE_PLAN", "ZT_WOQ_STREAM", "ZT_WOQ_WIDE",
+    "ZT_WOQ_GEMM",         "ZT_WOQ_DEBUG",       "ZT_S8_SKINNY32", "ZT_S8_SKINNY",
+    "ZT_S8_FRAG",          "ZT_S8_FORCE",        "ZT_S8_TILE",     "ZT_S8_KIND",
+    "ZT_MOE_BN"};
+
+// Values are interned copies that are never freed: a reader may hold an old
+// pointer while another thread replaces the value.
+std::atomic<const char *> g_knobs[kKnobCount];
+
+const char *intern(const char *v) {
+  if (!v || !*v) return nullptr;
+  static std::mutex mu;
+  static std::vector<std::unique_ptr<std::string>> pool;
+  std::lock_guard<std::mutex> g(mu);
+  pool.emplace_back(new std::string(v));
+  return pool.back()->c_str();
+}
+
+// Reads the environment once, when the library is loaded.
+struct KnobsFromEnv {
+  KnobsFromEnv() {
+    for (int i = 0; i < kKnobCount; ++i)
+      g_knobs[i].store(intern(std::getenv(kKnobNames[i])), std::memory_order_release);
+  }
+} g_knobs_from_env;
+
+}  // namespace
+
+const char *knob(Knob k) { return g_knobs[k].load(std::memory_order_acquire); }
+
+}  // namespace zt
+
 extern "C" {
 
 const char *zt_last_error_string(void) { return g_last_error.c_str(); }
+
+int zt_set_tuning(const char *name, const char *value) {
+  if (!name) return fail(ZT_EINVAL, "zt_set_tuning: null name");
+  for (int i = 0; i < zt::kKnobCount; ++i)
+    if (!std::strcmp(name, zt::kKnobNames[i])) {
+      zt::g_knobs[i].store(zt::intern(value), std::memory_order_release);
+      return ZT_OK;
+    }
+  return fail(ZT_EINVAL, "zt_set_tuning: unknown knob '%s'", name);
+}
+
+const char *zt_get_tuning(const char *name) {
+  if (!name) return nullptr;
+  for (int i = 0; i < zt::kKnobCount; ++i)
+    if (!std::strcmp(name, zt::kKnobNames[i])) return zt::knob(static_cast<zt::Knob>(i));
+  return nullptr;
+}
 
 }  // extern "C"
 

@@ -15,6 +15,7 @@
 #include <cstdlib>
 
 #include "zt_launch.hpp"
+#include "zt_tuning.hpp"
 
 namespace zt {
 
@@ -1081,7 +1082,7 @@ hipError_t launch_s8_skinny32_t(const DynArgs &a, hipStream_t s) {
 
 hipError_t launch_s8_skinny32(const DynArgs &a, hipStream_t s) {
   const int mt = (int)((a.M + 31) / 32);
-  const char *e = std::getenv("ZT_S8_SKINNY32");  // "TPW,PF,NW"
+  const char *e = knob(kKnobS8Skinny32);  // "TPW,PF,NW"
   int tpw = 0, pf = 0, nw = 0;
   if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
 #define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
@@ -1106,7 +1107,7 @@ hipError_t launch_s8_skinny_t(const DynArgs &a, hipStream_t s) {
 
 hipError_t launch_s8_skinny(const DynArgs &a, hipStream_t s) {
   const int mt = (int)((a.M + 15) / 16);
-  const char *e = std::getenv("ZT_S8_SKINNY");  // "TPW,PF,NW"
+  const char *e = knob(kKnobS8Skinny);  // "TPW,PF,NW"
   int tpw = 0, pf = 0, nw = 0;
   if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
 #define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
@@ -1158,7 +1159,7 @@ hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
 bool s8_frag_ok(const DynArgs &a) {
   // 17..128 tokens: the 32x32 kernel's tiles are at least half full there
   // (one 16-token tile is cheaper on the 16x16 kernel)
-  const char *e = std::getenv("ZT_S8_FRAG");  // "0": never, "1": from M = 1
+  const char *e = knob(kKnobS8Frag);  // "0": never, "1": from M = 1
   const int64_t lo = e && e[0] == '1' ? 1 : 17;
   if ((e && e[0] == '0') || a.M < lo || a.M > 128 || a.K % 64 != 0) return false;
   const int64_t rows = (a.M + 31) / 32 * 32;
@@ -1178,7 +1179,7 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
   }
   // the fast kernels address qx and W with 32-bit byte offsets
   const bool fits32 = a.M * a.K < (int64_t)kOobOffset && a.N * a.K < (int64_t)kOobOffset;
-  const char *force = std::getenv("ZT_S8_FORCE");  // t: tiled, s: skinny, o: old
+  const char *force = knob(kKnobS8Force);  // t: tiled, s: skinny, o: old
   const bool tiled = force ? force[0] == 't' : a.M >= 256;
   const bool skinny = force ? force[0] == 's' : a.M <= 128;
   if (skinny && fits32 && a.K % 64 == 0) return launch_s8_skinny(a, s);
@@ -1186,9 +1187,9 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
     // 256x128 tiles once there are half a round of them (measured on the
     // Llama prefill shapes: 2-stage DMA 256x128 is fastest from M = 2048 up)
     const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
-    const char *tile = std::getenv("ZT_S8_TILE");
+    const char *tile = knob(kKnobS8Tile);
     const bool big = tile ? tile[0] == '2' : t256 >= 128;
-    const char *kind = std::getenv("ZT_S8_KIND");  // r: register staging, 2/3: DMA stages
+    const char *kind = knob(kKnobS8Kind);  // r: register staging, 2/3: DMA stages
     if (!kind || kind[0] == 'n') {  // 32x32x32 kernel, S stages
       const int st = kind && kind[1] ? kind[1] - '0' : 3;
       if (st == 2) return big ? launch_s8_gemm32<256, 128, 2>(a, s) : launch_s8_gemm32<128, 128, 2>(a, s);

@@ -24,6 +24,7 @@
 
 #include "woq_dequant.hpp"
 #include "zt_launch.hpp"
+#include "zt_tuning.hpp"
 
 namespace zt {
 
@@ -435,7 +436,7 @@ hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s) {
 // (each 128 or 256) overrides them for tuning
 void moe_tile_widths(int &bn1, int &bn2) {
   bn1 = 128, bn2 = 128;
-  if (const char *v = std::getenv("ZT_MOE_BN")) {
+  if (const char *v = knob(kKnobMoeBn)) {
     int a = 0, b = 0;
     if (std::sscanf(v, "%d,%d", &a, &b) == 2 && (a == 128 || a == 256) &&
         (b == 128 || b == 256))

@@ -17,8 +17,9 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
-#include <map>
-#include <mutex>
+#include <rocprofiler-sdk-roctx/roctx.h>
+
+#include <algorithm>
 #include <utility>
 #include <vector>
 
@@ -54,33 +55,13 @@ hipStream_t current_stream() {
   return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
 }
 
-// Per-(device, stream) workspace (the dynamic path's quantised activations
-// and row scales).  Calls on one stream are ordered, so they can share it;
-// a larger request replaces the buffer (the old one is freed through the
-// caching allocator, stream-ordered).
-struct WorkspaceCache {
-  std::mutex mu;
-  std::map<std::pair<int, hipStream_t>, at::Tensor> bufs;
-};
-
-WorkspaceCache &woq_cache() {
-  static WorkspaceCache c;
-  return c;
-}
-
-void *woq_workspace(const at::Tensor &like, size_t bytes) {
-  if (bytes == 0) return nullptr;
-  auto &c = woq_cache();
-  std::lock_guard<std::mutex> g(c.mu);
-  const auto key = std::make_pair((int)like.get_device(), current_stream());
-  auto it = c.bufs.find(key);
-  if (it == c.bufs.end() || (size_t)it->second.numel() < bytes) {
-    at::Tensor t = at::zeros({(int64_t)bytes},
-                             like.options().dtype(at::kByte));
-    c.bufs[key] = t;
-    return t.data_ptr();
-  }
-  return it->second.data_ptr();
+// Device workspace of one call, from torch's stream-ordered caching
+// allocator.  It is released when the call returns; the allocator hands the
+// block to later work on the same stream only, and inside a HIP graph
+// capture it comes from the graph's private pool, so a captured call keeps
+// its own workspace on every replay.
+at::Tensor call_workspace(const at::Tensor &like, size_t bytes) {
+  return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
 }
 
 std::vector<int64_t> out_sizes(const at::Tensor &input, int64_t N) {
@@ -93,6 +74,35 @@ at::Tensor as_2d(const at::Tensor &t) {
   const int64_t last = t.size(-1);
   return t.contiguous().view({t.numel() / std::max<int64_t>(last, 1), last});
 }
+
+// [rows, K] view of t with unit column stride and row stride *ld, sharing
+// t's storage when its leading dimensions collapse into one (a contiguous
+// tensor, or a 2-D tensor whose rows are strided, such as a column slice);
+// otherwise a contiguous copy with *ld = K.
+at::Tensor rows_view(const at::Tensor &t, int64_t *ld) {
+  const int64_t d = t.dim(), K = t.size(-1);
+  bool ok = t.stride(d - 1) == 1 || K == 1;
+  for (int64_t i = 0; ok && i + 2 < d; ++i)
+    ok = t.size(i) == 1 || t.stride(i) == t.stride(i + 1) * t.size(i + 1);
+  const int64_t rows = t.numel() / std::max<int64_t>(K, 1);
+  if (ok && rows > 0) {
+    const int64_t rs = d >= 2 ? t.stride(d - 2) : K;
+    if (rs >= K || rows == 1) {
+      *ld = rows == 1 ? K : rs;
+      return t.as_strided({rows, K}, {*ld, 1});
+    }
+  }
+  *ld = K;
+  return as_2d(t);
+}
+
+// The reference hands zentorch_op_name to ZenDNNL's profiler
+// (MatmulUtils.hpp:763); here it names a ROCTx range around the launches,
+// which rocprofv3 --marker-trace records.
+struct OpRange {
+  explicit OpRange(const std::string &name) { roctxRangePushA(name.c_str()); }
+  ~OpRange() { roctxRangePop(); }
+};
 
 // Shared body of every zentorch_woq_linear* op.  post_ids follow the
 // reference's post-op numbering; binary ops take binary_inputs in order.
@@ -130,12 +140,20 @@ at::Tensor woq_linear_impl(const at::Tensor &input, const at::Tensor &weight,
               ") must divide K (", K, ")");
 
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
-  at::Tensor x2 = as_2d(input);
+  const OpRange range(op_name);
+  int64_t ldx = K;
+  const at::Tensor x2 = rows_view(input, &ldx);
   const int64_t M = x2.size(0);
   // The op's weight is the [K/8, N] view of [N, K/8] storage
-  // (_op_replacements_new.py:376-379); any other strides are materialised.
+  // (_op_replacements_new.py:376-379), which the kernels stream row by row.
+  // A weight in any other layout is transposed into that one on every call.
   at::Tensor w_nk = weight.t();
-  if (!w_nk.is_contiguous()) w_nk = w_nk.contiguous();
+  if (!w_nk.is_contiguous()) {
+    TORCH_WARN_ONCE(op, ": weight is not the [K/8, N] transposed view of a contiguous "
+                    "[N, K/8] tensor (zentorch_woq_repack_weight(...).t()); it is copied into "
+                    "that layout on every call");
+    w_nk = w_nk.contiguous();
+  }
   at::Tensor s = weight_scales.contiguous();
   at::Tensor zp, b;
   if (weight_zero_points.has_value() && weight_zero_points->defined()) {
@@ -155,18 +173,18 @@ at::Tensor woq_linear_impl(const at::Tensor &input, const at::Tensor &weight,
                 "then up rows), got ", N);
   at::Tensor result = at::empty(out_sizes(input, gate_up ? N / 2 : N), input.options());
   if (result.numel() == 0) return result;
+  const zt_stream_t stream = reinterpret_cast<zt_stream_t>(current_stream());
   if (gate_up) {
     const size_t ws = zt_woq_linear_gate_up_workspace_size(M, K, N, G);
-    void *wsp = woq_workspace(input, ws);
+    const at::Tensor wsp = call_workspace(input, ws);
     const int rc = zt_woq_linear_gate_up(
-        x2.data_ptr(), zt_dtype_of(x2), M, K, K,
+        x2.data_ptr(), zt_dtype_of(x2), M, K, ldx,
         reinterpret_cast<const int32_t *>(w_nk.data_ptr()), N, s.data_ptr(),
         zt_dtype_of(s), G, zp.defined() ? zp.data_ptr() : nullptr,
         zp.defined() ? zt_dtype_of(zp) : ZT_DT_NONE,
         b.defined() ? b.data_ptr() : nullptr,
         b.defined() ? zt_dtype_of(b) : ZT_DT_NONE, result.data_ptr(),
-        zt_dtype_of(result), N / 2, wsp, ws,
-        reinterpret_cast<zt_stream_t>(current_stream()));
+        zt_dtype_of(result), N / 2, wsp.data_ptr(), ws, stream);
     TORCH_CHECK(rc == ZT_OK, op, ": ", zt_last_error_string());
     return result;
   }
@@ -184,27 +202,30 @@ at::Tensor woq_linear_impl(const at::Tensor &input, const at::Tensor &weight,
       check_device(bi, input, op, "binary post-op input");
       TORCH_CHECK(bi.numel() == M * N, op, ": binary post-op input has ",
                   bi.numel(), " elements, expected ", M * N);
-      at::Tensor bc = bi.contiguous();
+      TORCH_CHECK(bi.size(-1) == N, op, ": binary post-op input must have N = ", N,
+                  " columns, got ", bi.size(-1));
+      at::Tensor bc = bi;
       if (bc.scalar_type() != at::kBFloat16 && bc.scalar_type() != at::kFloat)
         bc = bc.to(input.scalar_type());
+      int64_t ld = N;
+      bc = rows_view(bc, &ld);
       keep.push_back(bc);
       post.bufs[nb] = bc.data_ptr();
       post.buf_dtypes[nb] = zt_dtype_of(bc);
-      post.buf_ld[nb] = N;
+      post.buf_ld[nb] = ld;
       ++nb;
     }
   }
   const size_t ws = zt_woq_linear_workspace_size(M, K, N, G);
-  void *wsp = woq_workspace(input, ws);
+  const at::Tensor wsp = call_workspace(input, ws);
   const int rc = zt_woq_linear(
-      x2.data_ptr(), zt_dtype_of(x2), M, K, K,
+      x2.data_ptr(), zt_dtype_of(x2), M, K, ldx,
       reinterpret_cast<const int32_t *>(w_nk.data_ptr()), N, s.data_ptr(),
       zt_dtype_of(s), G, zp.defined() ? zp.data_ptr() : nullptr,
       zp.defined() ? zt_dtype_of(zp) : ZT_DT_NONE,
       b.defined() ? b.data_ptr() : nullptr,
       b.defined() ? zt_dtype_of(b) : ZT_DT_NONE, &post, result.data_ptr(),
-      zt_dtype_of(result), N, wsp, ws,
-      reinterpret_cast<zt_stream_t>(current_stream()));
+      zt_dtype_of(result), N, wsp.data_ptr(), ws, stream);
   TORCH_CHECK(rc == ZT_OK, op, ": ", zt_last_error_string());
   return result;
 }
@@ -394,15 +415,18 @@ at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
   if (b.defined()) check_device(b, input, op, "bias");
 
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
+  const OpRange range(name);
   at::Tensor result = at::empty(out_sizes(input, N), input.options());
   if (result.numel() == 0) return result;
+  // the reference quantises a contiguous copy of a strided input
+  // (DynamicQLinear.cpp:163-165); so does the kernel here
   at::Tensor x2 = as_2d(input);
   const int64_t M = x2.size(0);
   at::Tensor wc = weight.contiguous();
   at::Tensor sc = weight_scales.contiguous();
   at::Tensor bc = b.defined() ? b.contiguous() : b;
   const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K);
-  at::Tensor ws = at::empty({(int64_t)ws_bytes}, input.options().dtype(at::kByte));
+  const at::Tensor ws = call_workspace(input, ws_bytes);
   const int rc = zt_dynamic_qlinear(
       x2.data_ptr(), zt_dtype_of(x2), M, K,
       reinterpret_cast<const int8_t *>(wc.data_ptr()), N, sc.data_ptr(),
@@ -427,8 +451,8 @@ void fused_moe(at::Tensor &output, const at::Tensor &input, const at::Tensor &w1
                const at::Tensor &topk_id, bool skip_weighted, c10::string_view act,
                const c10::optional<at::Tensor> &w13_scales,
                const c10::optional<at::Tensor> &w2_scales, c10::string_view zentorch_op_name) {
-  (void)zentorch_op_name;
   const char *op = "zentorch_fused_moe";
+  const OpRange range{std::string(zentorch_op_name)};
   TORCH_CHECK(input.dim() == 2 && input.scalar_type() == at::kBFloat16,
               op, ": input must be a 2D bfloat16 tensor [T, H]");
   TORCH_CHECK(w13.scalar_type() == at::kInt && w2.scalar_type() == at::kInt,

@@ -33,6 +33,7 @@
 
 #include "woq_dequant.hpp"
 #include "zt_launch.hpp"
+#include "zt_tuning.hpp"
 
 namespace zt {
 
@@ -1157,14 +1158,14 @@ static bool aligned16(const void *p) {
 }
 
 WoqKernelKind woq_select_kernel(const WoqArgs &a) {
-  if (const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL")) {
+  if (const char *f = knob(kKnobWoqForceKernel)) {
     if (!std::strcmp(f, "generic")) return kWoqGeneric;
   }
   const bool bf16_ok = a.x_dt == ZT_DT_BF16 && a.ldx % 8 == 0 &&
                        aligned16(a.x) && aligned16(a.w);
   if (!bf16_ok || a.N < 1) return kWoqGeneric;
   const int64_t gs = a.K / a.G;
-  const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");
+  const char *f = knob(kKnobWoqForceKernel);
   const int64_t cpg = gs / 128;
   const bool decode_ok = a.K % 128 == 0 &&
                          (a.G == 1 || (gs % 128 == 0 && (cpg & (cpg - 1)) == 0)) &&
@@ -1179,7 +1180,7 @@ WoqKernelKind woq_select_kernel(const WoqArgs &a) {
 }
 
 static int env_plan(int *v) {
-  const char *p = std::getenv("ZT_WOQ_DECODE_PLAN");
+  const char *p = knob(kKnobWoqDecodePlan);
   if (!p) return 0;
   return std::sscanf(p, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) == 4;
 }
@@ -1343,7 +1344,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // tiles than CUs when x takes most of the LDS (one workgroup per CU)
   const bool big_x = (size_t)a.M * stream_x_pitch((int)a.K) * 2 > 64 * 1024;
   int nw = 8, tpw = tiles >= 512 || (big_x && tiles > 256) ? 2 : 1, cpw = 0;
-  const char *e = std::getenv("ZT_WOQ_STREAM");  // "0" disables; "NW,CPW,TPW" forces
+  const char *e = knob(kKnobWoqStream);  // "0" disables; "NW,CPW,TPW" forces
   if (e && e[0] == '0') return false;
   if (e) std::sscanf(e, "%d,%d,%d", &nw, &cpw, &tpw);
   const int mt = (int)((a.M + 15) / 16) == 3 ? 4 : (int)((a.M + 15) / 16);
@@ -1362,7 +1363,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
       const int cp = C / p;
       if (C % p || (p > 1 && !stream_x_dma(a, p)) || !fits(p)) continue;
       const int cpw_need = p * ((cp + 7) / 8);  // chunks per wave over all phases
-      if (std::getenv("ZT_WOQ_DEBUG"))
+      if (knob(kKnobWoqDebug))
         std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: MT=%d P=%d CPW>=%d\n",
                      (long long)a.M, (long long)a.N, (long long)a.K, mt, p, cpw_need);
 #define ZT_STREAM_PCASE(CPW_, P_, MT_)                                          \
@@ -1395,7 +1396,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     for (int c : {2, 4, 8, 12, 14, 16})
       if (c >= need && (c != 14 || nw == 8)) { cpw = c; break; }
   if (cpw < need) return false;
-  if (std::getenv("ZT_WOQ_DEBUG"))
+  if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: NW=%d CPW=%d TPW=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, nw, cpw, tpw);
 #define ZT_STREAM_CASE(NW_, CPW_, TPW_) \
@@ -1683,12 +1684,12 @@ __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const
 }
 
 bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
-  const char *e = std::getenv("ZT_WOQ_WIDE");  // "0" disables; "KS" forces the split count
+  const char *e = knob(kKnobWoqWide);  // "0" disables; "KS" forces the split count
   if (e && e[0] == '0') return false;
   if (M < 1 || M > 64 || N < 4 || N % 4 || K % kWideKP || G <= 0 || K % G) return false;
   // up to 32 rows of a matrix of at most 4096 x 4096 the stream kernel is
   // faster (measured: the split-K reduce launch outweighs the x savings)
-  const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");
+  const char *f = knob(kKnobWoqForceKernel);
   const bool forced = e || (f && !std::strcmp(f, "wide"));
   if (M < 8 && !forced) return false;
   // while x [M, K] leaves room for two stream-kernel workgroups per CU the
@@ -1725,7 +1726,7 @@ size_t woq_wide_workspace(const WidePlan &p, int64_t M, int64_t N) {
 }
 
 bool woq_wide_ok(const WoqArgs &a, WidePlan *p) {
-  const char *f = std::getenv("ZT_WOQ_FORCE_KERNEL");  // another forced kernel skips this one
+  const char *f = knob(kKnobWoqForceKernel);  // another forced kernel skips this one
   if (f && std::strcmp(f, "wide")) return false;
   if (!woq_wide_plan(a.M, a.N, a.K, a.G, p)) return false;
   return a.x_dt == ZT_DT_BF16 && a.s_dt == ZT_DT_BF16 && !a.zp && a.ldx % 8 == 0 &&
@@ -1742,7 +1743,7 @@ hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace,
   float *partial = p.splits > 1 ? static_cast<float *>(workspace) : nullptr;
   if (p.splits > 1 && !partial) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((a.N + kWideRows - 1) / kWideRows), (unsigned)p.splits);
-  if (std::getenv("ZT_WOQ_DEBUG"))
+  if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq wide M=%lld N=%lld K=%lld: MT=%d splits=%d phases/split=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, p.mt, p.splits, p.pps);
   if (p.mt == 1)
@@ -1770,7 +1771,7 @@ bool woq_try_wide_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   const int gmask = a.G == 1 ? 0 : 0x7fffffff;
   const int gu = (int)(a.N / 2);
   const dim3 grid((unsigned)(a.N / kWideRows), 1u);
-  if (std::getenv("ZT_WOQ_DEBUG"))
+  if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq wide gate_up M=%lld N=%lld K=%lld: MT=%d\n", (long long)a.M,
                  (long long)a.N, (long long)a.K, p.mt);
   if (p.mt == 1)
@@ -1821,7 +1822,7 @@ bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   if (cpw < need) return false;
   const int x_dma = stream_x_dma(a, 1) ? 1 : 0;
   const dim3 grid((unsigned)((I / 16 + tpw / 2 - 1) / (tpw / 2))), block(512);
-  if (std::getenv("ZT_WOQ_DEBUG"))
+  if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq gate_up stream M=%lld N=%lld K=%lld: CPW=%d TPW=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, cpw, tpw);
 #define ZT_GU_CASE(CPW_, TPW_)                                                              \
@@ -1872,7 +1873,7 @@ hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *worksp
     hipError_t err = hipSuccess;
     if (try_launch_stream(a, s, shift, gmask, mode, &err)) return err;
   }
-  if (std::getenv("ZT_WOQ_DEBUG"))
+  if (knob(kKnobWoqDebug))
     std::fprintf(stderr,
                  "[zt] woq decode M=%lld N=%lld K=%lld: NK=%d NT=%d CPW=%d TPW=%d NI=%d xr=%d "
                  "xs=%d grid=%d lds=%zu\n",
@@ -1906,7 +1907,7 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
                     (a.G == 1 || (gs % 128 == 0 && (cpg & (cpg - 1)) == 0)) &&
                     a.M * a.ldx * 2 < (int64_t)kOobOffset &&
                     a.N * (a.K / 2) < (int64_t)kOobOffset;
-    const char *e = std::getenv("ZT_WOQ_GEMM");  // "old" disables, "128" forces 128x128
+    const char *e = knob(kKnobWoqGemm);  // "old" disables, "128" forces 128x128
     if (ok && !(e && e[0] == 'o')) {
       int shift = 0;
       while (cpg > 1 && (1 << shift) < cpg) ++shift;

@@ -1,0 +1,32 @@
+// Kernel-selection overrides of libzentorch_hip.so.
+//
+// Each knob is named after the environment variable that sets it.  The
+// environment is read once, when the library is loaded; zt_set_tuning
+// (include/zentorch_hip.h) changes a knob afterwards.  The host dispatch
+// reads a knob with one atomic load, so no launch calls getenv and a change
+// made while other threads launch is not a data race.
+#pragma once
+
+namespace zt {
+
+enum Knob {
+  kKnobWoqForceKernel,  // ZT_WOQ_FORCE_KERNEL: generic | decode | gemm | wide
+  kKnobWoqDecodePlan,   // ZT_WOQ_DECODE_PLAN: "NK,NT,CPW,TPW" of the decode kernel
+  kKnobWoqStream,       // ZT_WOQ_STREAM: "0" disables, "NW,CPW,TPW" forces a shape
+  kKnobWoqWide,         // ZT_WOQ_WIDE: "0" disables, "KS" forces the K-split count
+  kKnobWoqGemm,         // ZT_WOQ_GEMM: "old" takes the 16x16 kernel, "128" 128x128 tiles
+  kKnobWoqDebug,        // ZT_WOQ_DEBUG: print each launch shape to stderr
+  kKnobS8Skinny32,      // ZT_S8_SKINNY32: "TPW,PF,NW" of the 32-token skinny kernel
+  kKnobS8Skinny,        // ZT_S8_SKINNY: "TPW,PF,NW" of the 16-token skinny kernel
+  kKnobS8Frag,          // ZT_S8_FRAG: "0" never, "1" from M = 1 (fragment-order qx)
+  kKnobS8Force,         // ZT_S8_FORCE: t tiled, s skinny, o 16x16 kernel
+  kKnobS8Tile,          // ZT_S8_TILE: "128" forces 128 x 128 tiles
+  kKnobS8Kind,          // ZT_S8_KIND: r register staging, 2 / 3 DMA kernels
+  kKnobMoeBn,           // ZT_MOE_BN: column tile of the MoE GEMMs
+  kKnobCount
+};
+
+// The knob's value, or nullptr when it is unset.
+const char *knob(Knob k);
+
+}  // namespace zt
