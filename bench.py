@@ -129,12 +129,20 @@ def graph_time(calls, reps, warmup):
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    _hold_device()
     t0.record()
     for _ in range(reps):
         graph.replay()
     t1.record()
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / 1e3 / reps
+
+
+def _hold_device():
+    """Keep the stream busy (a ~100 us spin kernel) while the host submits
+    the timed replay, so the interval between the two events holds the
+    graph's kernels back to back and not the host's submission latency."""
+    torch.cuda._sleep(250_000)
 
 
 def capture(calls):
@@ -184,6 +192,7 @@ def bench_config0(args, gen):
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    _hold_device()
     t0.record()
     timed.replay()
     t1.record()
