@@ -157,6 +157,32 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
 size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K);
 
 /*
+ * zt_dynamic_qlinear without a workspace argument: allocates nothing.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP-graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The quantised activations and row
+ * scales go to a scratch array of ZT_DYN_SCRATCH_BYTES that each GPU holds
+ * from the first call on it until the process ends, so a call is limited to
+ * zt_dynamic_qlinear_workspace_size(M, K) <= ZT_DYN_SCRATCH_BYTES (about
+ * M * K <= 32 Mi; larger calls return ZT_EINVAL and launch nothing).  Every
+ * call on one GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (different streams, or threads without ordering) race and must not be
+ * issued.  Nothing in the scratch needs to start at zero; it keeps the last
+ * call's contents.  Results equal zt_dynamic_qlinear's bit for bit (the same
+ * kernels).  Call with the stream's device current.
+ */
+#define ZT_DYN_SCRATCH_BYTES (32u << 20)
+
+int zt_dynamic_qlinear_scratch(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                               const int8_t *w, int64_t N, const void *w_scales,
+                               int32_t w_scales_dtype, const void *bias, int32_t bias_dtype,
+                               const zt_post_ops *post, void *y, int32_t y_dtype,
+                               zt_stream_t stream);
+
+/* ZT_DYN_SCRATCH_BYTES, for callers that bind the library at run time. */
+size_t zt_dynamic_qlinear_scratch_max(void);
+
+/*
  * The quantisation stage of zt_dynamic_qlinear on its own (same kernel):
  * qx[M, K] int8 and sx[M] fp32, sx = max(amax_k|x|, 1e-12)/127,
  * qx = clamp(round_half_even(x/sx), -128, 127).  Exposes what ZenDNNL

@@ -492,6 +492,66 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   return hip_status(zt::launch_s8_gemm(a, s), op);
 }
 
+}  // extern "C"
+
+// ------------------------------------------ allocation-free dynamic qlinear
+// Scratch of zt_dynamic_qlinear_scratch: the quantised activations and row
+// scales of one call, in a device array each GPU holds for the life of the
+// process.  In host code `scratch` names a host-side stand-in, never the
+// device memory: the device address comes from hipGetSymbolAddress, once
+// per device (g_scratch_ptr), and only that address reaches a kernel.
+static __device__ __align__(256) unsigned char scratch[ZT_DYN_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+int scratch_address(const char *op, void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(ZT_EHIP, "%s: no current HIP device (or device id %d >= %d)", op, dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(ZT_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: HIP error %d (%s)",
+                  op, dev, (int)e, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ZT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t zt_dynamic_qlinear_scratch_max(void) { return ZT_DYN_SCRATCH_BYTES; }
+
+int zt_dynamic_qlinear_scratch(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                               const int8_t *w, int64_t N, const void *w_scales,
+                               int32_t w_scales_dtype, const void *bias, int32_t bias_dtype,
+                               const zt_post_ops *post, void *y, int32_t y_dtype,
+                               zt_stream_t stream) {
+  static const char *op = "zt_dynamic_qlinear_scratch";
+  if (M < 0 || N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
+  if (M == 0 || N == 0) return ZT_OK;
+  const size_t need = zt_dynamic_qlinear_workspace_size(M, K);
+  if (need > (size_t)ZT_DYN_SCRATCH_BYTES)
+    return fail(ZT_EINVAL, "%s: M=%lld x K=%lld needs %zu bytes of scratch, more than the "
+                "%zu this entry point holds (use zt_dynamic_qlinear with a workspace)",
+                op, (long long)M, (long long)K, need, (size_t)ZT_DYN_SCRATCH_BYTES);
+  void *ws = nullptr;
+  const int rc = scratch_address(op, &ws);
+  if (rc) return rc;
+  return zt_dynamic_qlinear(x, x_dtype, M, K, w, N, w_scales, w_scales_dtype, bias, bias_dtype,
+                            post, y, y_dtype, ws, (size_t)ZT_DYN_SCRATCH_BYTES, stream);
+}
+
 int zt_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out,
                          zt_stream_t stream) {
   static const char *op = "zt_woq_repack_weight";
