@@ -152,7 +152,7 @@ def test_woq_op_strided_input_rows(M):
     wide = torch.zeros(M, K + 256, dtype=torch.bfloat16)
     wide[:, 128:128 + K] = x
     xs = wide.to(DEV)[:, 128:128 + K]
-    assert not xs.is_contiguous()
+    assert M == 1 or not xs.is_contiguous()
     y = torch.ops.zentorch.zentorch_woq_linear(xs, wp.to(DEV).t(), s.to(DEV), None)
     torch.testing.assert_close(y.cpu().float(), ref.float(), **TOL)
     yc = torch.ops.zentorch.zentorch_woq_linear(x.to(DEV), wp.to(DEV).t(), s.to(DEV), None)
