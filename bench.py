@@ -548,7 +548,7 @@ def secondary_rooflines(res):
         out.append({"workload": "config 3 int8: dynamic qlinear over the Llama-3-8B layer, M=2048",
                     "bound": "mfma", "achieved": round(d["TOPS"], 2), "peak": INT8_PEAK_TOPS,
                     "unit": "TOP/s", "frac": round(d["frac_int8_peak"], 4),
-                    "kernels": "dyn_quantize_bf16_kernel + s8_gemm32_kernel",
+                    "kernels": "dyn_quantize_bf16_kernel + s8_gemm_ws_kernel",
                     "layer_avg_us": round(d["s_per_pass"] * 1e6, 3)})
     d = res.get("prefill_int4_m2048")
     if d:

@@ -146,3 +146,22 @@ def test_dynamic_qlinear_fragment_kernel_post_ops(post):
     y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV), post_ops=post,
                           post_bufs=[t.to(DEV) for t in bufs]).cpu()
     torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
+# the large-M kernels by name: the load-wave kernel (default) and the
+# 32x32 DMA kernel it replaced, on ragged shapes (M, N past a tile, K not a
+# multiple of the 128-byte step)
+@pytest.mark.parametrize("kind", ["w", "n"])
+@pytest.mark.parametrize("M,N,K", [(257, 200, 144), (520, 4160, 272), (2100, 130, 2064),
+                                   (512, 384, 4096)])
+def test_s8_large_m_kernels_bit_exact(kind, M, N, K, knobs):
+    knobs.set("ZT_S8_KIND", kind)
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    acc = C.s8s8s32_gemm(a.to(DEV), w.to(DEV)).cpu()
+    assert torch.equal(acc, torch._int_mm(a, w.t().contiguous()))
+    x, w2, sw, b = make(M, K, N, seed=M + K)
+    y = C.dynamic_qlinear(x.to(DEV), w2.to(DEV), sw.to(DEV), b.to(DEV)).cpu()
+    torch.testing.assert_close(y.float(), O.dynamic_qlinear(x, w2, sw, b).float(), rtol=1e-2,
+                               atol=1e-2)

@@ -278,12 +278,12 @@ __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i3
 // row scales come from LDS (sx_l).  Same arithmetic as dyn_epilogue:
 // ((float)acc * sx[m]) * sw[n] + bias[n].  Post-ops, int32 output and a row
 // length that is not a multiple of 4 take the general path.
-template <int BM, int BN>
+template <int BM, int BN, int NT = 256>
 __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t *tile,
                                                  const float *sx_l, int m0, int n0, int tid) {
   constexpr int AP = acc_pitch<BN>();
   constexpr int G4 = BN / 4;
-  static_assert(256 % G4 == 0, "four-column groups must divide the threads");
+  static_assert(NT % G4 == 0, "four-column groups must divide the threads");
   const int M = (int)a.M, N = (int)a.N;
   const int c4 = (tid % G4) * 4, n = n0 + c4;
   if (a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0) {
@@ -294,7 +294,7 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
       sw[r] = load_elem(a.sw, a.sw_dt, n + r);
       b[r] = a.bias ? load_elem(a.bias, a.b_dt, n + r) : 0.f;
     }
-    for (int row = tid / G4; row < BM && m0 + row < M; row += 256 / G4) {
+    for (int row = tid / G4; row < BM && m0 + row < M; row += NT / G4) {
       const int m = m0 + row;
       const i32x4_t v = *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4);
       const float sxm = sx_l[row];
@@ -317,7 +317,7 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
     }
     return;
   }
-  for (int idx = tid; idx < BM * G4; idx += 256) {
+  for (int idx = tid; idx < BM * G4; idx += NT) {
     const int row = idx / G4, cc = (idx % G4) * 4;
     const int m = m0 + row, nn = n0 + cc;
     if (m < M && nn < N)
@@ -326,10 +326,10 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
 }
 
 // Stage the row scales of rows m0..m0+BM of the tile for s8_tile_epilogue.
-template <int BM>
+template <int BM, int NT = 256>
 __device__ __forceinline__ void s8_stage_row_scales(const DynArgs &a, float *sx_l, int m0, int tid) {
   if (a.y_dt == ZT_DT_S32) return;
-  for (int r = tid; r < BM; r += 256) sx_l[r] = m0 + r < (int)a.M ? a.sx[m0 + r] : 0.f;
+  for (int r = tid; r < BM; r += NT) sx_l[r] = m0 + r < (int)a.M ? a.sx[m0 + r] : 0.f;
 }
 
 template <int BM, int BN>
@@ -775,6 +775,163 @@ hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Large-M int8 GEMM with warp-specialised loads: BM x BN tiles, K in steps
+// of 128 bytes (each row's slab is one whole 128-byte line), S stages in LDS.
+//  * NC = WM x WN compute waves only read fragments from LDS and run
+//    v_mfma_i32_32x32x32_i8 (each wave (BM/WM) x (BN/WN), fragments of the
+//    next 32-k sub-step read while the current sub-step's MFMAs run);
+//  * ND load waves only move the stages into LDS with the buffer unit
+//    (buffer_load_dwordx4 ... lds, 8 rows x 128 B per instruction).
+// When the same waves issued both, every load instruction the buffer unit
+// could not yet accept held up the MFMAs queued behind it, and the loop ran
+// at the sum of its load and MFMA times.  One s_barrier per step: a load
+// wave first waits for its own loads of the step (in-order vmcnt), so after
+// the barrier the stage is whole, and every compute wave has finished the
+// previous step's reads, so its stage can be refilled.
+// LDS rows are 128 B; the 16-byte chunk c of tile row R sits at
+// c ^ ((R >> 1) & 7), so the 16 rows one read pass touches hit 16 distinct
+// bank groups.  The epilogue stages the whole int32 tile in LDS and all
+// threads finish it (s8_tile_epilogue).
+constexpr int kWsBK = 128;
+
+template <int BM, int BN, int S>
+constexpr size_t s8_ws_lds() {
+  const size_t stages = (size_t)S * (BM + BN) * kWsBK;
+  const size_t tile = (size_t)BM * acc_pitch<BN>() * 4 + (size_t)BM * 4;
+  return stages > tile ? stages : tile;
+}
+
+template <int BM, int BN, int WM, int WN, int ND, int S>
+__global__ __launch_bounds__(64 * (WM * WN + ND)) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
+  constexpr int NC = WM * WN, NT = 64 * (NC + ND);
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32 x 32 tiles per compute wave
+  constexpr int STAGE = (BM + BN) * kWsBK;
+  constexpr int GROUPS = (BM + BN) / 8;  // 1 KB loads (8 rows) per stage
+  constexpr int LPW = GROUPS / ND;       // per load wave
+  static_assert(GROUPS % ND == 0 && (S - 2) * LPW <= 63 && S >= 2, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = (K + kWsBK - 1) / kWsBK;
+  i32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int wm = wv / WN, wn = wv % WN;
+  if (wv >= NC) {
+    // load wave: rows (dw * LPW + q) * 8 + lane / 8 of the [A | B] slab
+    const int dw = wv - NC;
+    const auto a_rs = make_rsrc(a.qx, (uint32_t)((int64_t)M * K));
+    const auto b_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+    uint32_t src[LPW];
+    int chunk[LPW];
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+      const int row = (dw * LPW + q) * 8 + (lane >> 3);
+      chunk[q] = ((lane & 7) ^ ((row >> 1) & 7)) * 16;
+      if (row < BM) src[q] = m0 + row < M ? (uint32_t)((m0 + row) * K + chunk[q]) : kOobOffset;
+      else src[q] = n0 + row - BM < N ? (uint32_t)((n0 + row - BM) * K + chunk[q]) : kOobOffset;
+    }
+    auto dma = [&](int step) {
+      const int k0 = step * kWsBK;
+      int8_t *stage = s8_smem + (step % S) * STAGE;
+#pragma unroll
+      for (int q = 0; q < LPW; ++q) {
+        // K % 16 == 0: a 16-byte chunk lies wholly inside or past its row
+        const uint32_t off = (src[q] == kOobOffset || step >= nk || k0 + chunk[q] >= K)
+                                 ? kOobOffset : src[q] + (uint32_t)k0;
+        lds_ptr_t dst = (lds_ptr_t)(stage + (dw * LPW + q) * 1024);
+        if ((dw * LPW + q) * 8 < BM)  // whole loads lie in A or in B
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, dst, 16, off, 0, 0, 0);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, dst, 16, off, 0, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int p = 0; p < S - 1; ++p) dma(p);
+    for (int ks = 0; ks < nk; ++ks) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait_imm((S - 2) * LPW));
+      asm volatile("s_barrier" ::: "memory");
+      dma(ks + S - 1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  } else {
+    // compute wave: fragments of row R = lane % 32 (+ tile offsets), k
+    // block 2 * sub + lane / 32 of the 128-byte step
+    const int fsw = (lane >> 1) & 7;
+    const int a_base = (wm * (BM / WM) + (lane & 31)) * kWsBK;
+    const int b_base = (BM + wn * (BN / WN) + (lane & 31)) * kWsBK;
+    i32x4_t Fa[2][TM], Fb[2][TN];
+    auto read = [&](int ks, int sub, int buf) {
+      const int8_t *stage = s8_smem + (ks % S) * STAGE;
+      const int pos = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        Fa[buf][i] = *reinterpret_cast<const i32x4_t *>(stage + a_base + i * 32 * kWsBK + pos);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        Fb[buf][j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kWsBK + pos);
+    };
+    for (int ks = 0; ks < nk; ++ks) {
+      asm volatile("s_barrier" ::: "memory");
+      read(ks, 0, 0);
+#pragma unroll
+      for (int sub = 0; sub < kWsBK / 32; ++sub) {
+        if (sub + 1 < kWsBK / 32) read(ks, sub + 1, (sub + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Fb[sub & 1][j], Fa[sub & 1][i],
+                                                              acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+  // epilogue: the whole int32 tile [m][n] in LDS (D is [n][m]: register r of
+  // lane l holds n = 8*(r/4) + 4*(l/32) + r%4, m = l%32 of its 32 x 32
+  // tile), then every thread finishes four columns of its rows
+  __syncthreads();
+  constexpr int AP = acc_pitch<BN>();
+  int32_t *tile = reinterpret_cast<int32_t *>(s8_smem);
+  float *sx_l = reinterpret_cast<float *>(tile + BM * AP);
+  if (wv < NC) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<i32x4_t *>(tile + (wm * (BM / WM) + i * 32 + (lane & 31)) * AP +
+                                       wn * (BN / WN) + j * 32 + 8 * q + 4 * (lane >> 5)) =
+              i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                      acc[i][j][4 * q + 3]};
+  }
+  s8_stage_row_scales<BM, NT>(a, sx_l, m0, tid);
+  __syncthreads();
+  s8_tile_epilogue<BM, BN, NT>(a, tile, sx_l, m0, n0, tid);
+}
+
+template <int BM, int BN, int WM, int WN, int ND, int S>
+hipError_t launch_s8_ws(const DynArgs &a, hipStream_t s) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  s8_gemm_ws_kernel<BM, BN, WM, WN, ND, S>
+      <<<dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * (WM * WN + ND)), s8_ws_lds<BM, BN, S>(),
+         s>>>(a, tiles_m, tiles_n, group_m);
+  return hipGetLastError();
+}
+
 // Skinny int8 GEMM (M <= 16*MT tokens, weight-streaming: the whole of qx
 // is reused by every workgroup from L2, W is read once).  One workgroup per
 // block of TPW 16-row weight tiles over all of K; its NW waves split K into
@@ -1189,8 +1346,9 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
     const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
     const char *tile = knob(kKnobS8Tile);
     const bool big = tile ? tile[0] == '2' : t256 >= 128;
-    const char *kind = knob(kKnobS8Kind);  // r: register staging, 2/3: DMA stages
-    if (!kind || kind[0] == 'n') {  // 32x32x32 kernel, S stages
+    const char *kind = knob(kKnobS8Kind);  // w: load-wave kernel, n: 32x32x32 kernel, r, 2, 3
+    if (!kind || kind[0] == 'w') return launch_s8_ws<256, 128, 2, 2, 4, 3>(a, s);
+    if (kind[0] == 'n') {  // 32x32x32 kernel, S stages
       const int st = kind && kind[1] ? kind[1] - '0' : 3;
       if (st == 2) return big ? launch_s8_gemm32<256, 128, 2>(a, s) : launch_s8_gemm32<128, 128, 2>(a, s);
       return big ? launch_s8_gemm32<256, 128, 3>(a, s) : launch_s8_gemm32<128, 128, 3>(a, s);
