@@ -44,7 +44,9 @@ def test_c_abi_exports_every_declared_symbol():
 def test_c_abi_needs_no_torch():
     out = subprocess.run(["readelf", "-d", os.path.join(PKG, "libzentorch_hip.so")],
                          capture_output=True, text=True, check=True).stdout
-    assert "torch" not in out and "c10" not in out
+    needed = [ln.split("[", 1)[1].rstrip("]") for ln in out.splitlines() if "(NEEDED)" in ln]
+    assert needed, out
+    assert not any("torch" in n or "c10" in n for n in needed), needed
 
 
 def test_aoti_shims_exported():
