@@ -212,3 +212,35 @@ def test_weight_cache_reuses_and_invalidates():
         y3 = f(x)
         torch.testing.assert_close(y3.float(), m(x).float(), **TOL)
         assert not torch.equal(y3, y1)
+
+
+# Zero points: the rewrite drops them (symmetric int4, as the reference's
+# pattern does at _op_replacements_new.py:370,386), so it fires only when the
+# zero-point buffer is all zero at compile time.  A non-zero zero point keeps
+# the stock dequantise-then-matmul (correct, unrewritten); zero points that
+# change after compile are rejected at run time.
+@pytest.mark.parametrize("group_size", [None, 128])
+def test_nonzero_zero_points_not_rewritten(group_size):
+    M, N, K = 8, 256, 512
+    model = WoqLinear(N, K, group_size=group_size, seed=5)
+    g = torch.Generator().manual_seed(6)
+    model.zero_points.copy_(torch.randint(-2, 3, model.zero_points.shape, generator=g,
+                                          dtype=torch.int8))
+    assert bool(model.zero_points.any())
+    x = torch.randn(M, K).bfloat16()
+    ref, out = compiled_vs_eager(model, x)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 0
+    torch.testing.assert_close(out.float(), ref.float(), **TOL)
+
+
+def test_zero_points_changed_after_compile_rejected():
+    M, N, K = 4, 128, 256
+    model = WoqLinear(N, K, seed=7).to(DEV).eval()
+    x = torch.randn(M, K).bfloat16().to(DEV)
+    with torch.no_grad():
+        fn = torch.compile(model, backend="zentorch")
+        fn(x)
+        assert counters["zentorch"]["zentorch_woq_linear"] == 1
+        model.zero_points.fill_(1)
+        with pytest.raises(RuntimeError, match="zero points"):
+            fn(x)

@@ -39,6 +39,7 @@ def trace(fn, *args):
     # some (unused dtype casts) that would add users to pattern nodes.
     gm.graph.eliminate_dead_code()
     gm.recompile()
+    gm._real_inputs = args  # the values a compile would see for its weights
     return gm
 
 
@@ -47,7 +48,10 @@ def targets(gm):
 
 
 def run_passes(gm):
-    optimize(gm.graph)
+    ph = [n for n in gm.graph.nodes if n.op == "placeholder"]
+    static = {n: t for n, t in zip(ph, getattr(gm, "_real_inputs", ()))
+              if isinstance(t, torch.Tensor)}
+    optimize(gm.graph, static)
     gm.recompile()
     return targets(gm)
 
@@ -98,6 +102,42 @@ def test_dequant_matmul_replaced(cpu_passes, gs, bias):
     assert tuple(node.args[2].meta["val"].shape) == ((K // gs) if gs else 1, N)
     assert node.args[3] is None
     assert (len(node.args) > 4 and node.args[4] is not None) == bias
+
+
+@pytest.mark.parametrize("case", ["nonzero_zp", "unsigned_weights", "unknown_values"])
+def test_dequant_matmul_left_alone_unless_symmetric(cpu_passes, case):
+    # the rewrite drops the zero points, which is right only for all-zero
+    # zero points and weights in [-8, 7]; anything else stays stock PyTorch
+    N, K = 64, 256
+    w, zp, s = quantized(N, K)
+    if case == "nonzero_zp":
+        zp = torch.full_like(zp, 3)
+    elif case == "unsigned_weights":
+        w = torch.randint(0, 16, (N, K), dtype=torch.int8)
+    x = torch.randn(4, K).bfloat16()
+    gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)), x, w, zp, s)
+    if case == "unknown_values":
+        gm._real_inputs = ()
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 0
+    assert aten.mm.default in t and zt.zentorch_woq_linear.default not in t
+
+
+def test_zero_point_guard_inserted_and_checked(cpu_passes):
+    from zentorch._optimize import zero_points_guard
+    N, K = 64, 256
+    w, zp, s = quantized(N, K)
+    x = torch.randn(4, K).bfloat16()
+    gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)), x, w, zp, s)
+    run_passes(gm)
+    guards = [n for n in gm.graph.nodes if n.target is zero_points_guard]
+    assert len(guards) == 1 and guards[0].args[0].name == "zp_1"
+    gm.graph.eliminate_dead_code()  # the guard has no users and must survive
+    assert any(n.target is zero_points_guard for n in gm.graph.nodes)
+    zero_points_guard(zp)  # all zero: passes
+    zp.add_(1)
+    with pytest.raises(RuntimeError, match="zero points"):
+        zero_points_guard(zp)
 
 
 def test_per_group_reshape_form_replaced(cpu_passes):

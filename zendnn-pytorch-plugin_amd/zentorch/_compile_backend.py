@@ -92,9 +92,33 @@ def use_weight_cache(graph: torch.fx.Graph, weights: set) -> int:
     return n
 
 
-def _compile_forward(gm: torch.fx.GraphModule, example_inputs: List[Any]) -> Callable:
+def _static_values(graph: torch.fx.Graph, weights: set, real_inputs: List[Any]) -> dict:
+    """Real tensors of the weight placeholders: the forward graph's
+    placeholders are the flattened inputs dynamo handed the backend, in
+    order (inference, no lifted parameters); matched only when every shape
+    and dtype agrees."""
+    ph = [n for n in graph.nodes if n.op == "placeholder"]
+    if len(ph) != len(real_inputs):
+        return {}
+    out = {}
+    for node, real in zip(ph, real_inputs):
+        val = node.meta.get("val", None)
+        if not isinstance(real, torch.Tensor) or not isinstance(val, torch.Tensor):
+            continue
+        if tuple(val.shape) != tuple(real.shape) or val.dtype != real.dtype:
+            return {}
+        if node in weights:
+            out[node] = real
+    return out
+
+
+def _compile_forward(gm: torch.fx.GraphModule, example_inputs: List[Any],
+                     real_inputs: List[Any] = ()) -> Callable:
     weights = _weight_placeholders(gm.graph)
-    optimize(gm.graph)
+    static = _static_values(gm.graph, weights, list(real_inputs))
+    if isinstance(real_inputs, list):
+        real_inputs.clear()  # hold no references to the caller's inputs
+    optimize(gm.graph, static)
     cached = use_weight_cache(gm.graph, weights)
     gm.graph.eliminate_dead_code()
     gm.recompile()
@@ -104,8 +128,10 @@ def _compile_forward(gm: torch.fx.GraphModule, example_inputs: List[Any]) -> Cal
 
 def zentorch_compile(gm: torch.fx.GraphModule, example_inputs: List[torch.Tensor]) -> Callable:
     logger.info("Called the zentorch backend.")
+    real_inputs = list(example_inputs)
     return aot_module_simplified(
-        gm, example_inputs, fw_compiler=_compile_forward,
+        gm, example_inputs,
+        fw_compiler=lambda g, ex: _compile_forward(g, ex, real_inputs),
         decompositions=select_decomp_table(), keep_inference_input_mutations=True)
 
 

@@ -33,6 +33,7 @@ from typing import Any, Callable, List, Optional
 
 import torch
 from torch._inductor import config
+from torch._subclasses.fake_tensor import unset_fake_temporarily
 from torch._inductor.pattern_matcher import (
     Arg,
     CallFunction,
@@ -43,12 +44,28 @@ from torch._inductor.pattern_matcher import (
 )
 from torch.fx.graph import Graph
 
-from ._utils import counters, on_gpu, tensor_meta
+from ._utils import counters, on_gpu, placeholder_of, static_value, tensor_meta
 
 aten = torch.ops.aten
 prims = torch.ops.prims
 
 pass_pattern = PatternMatcherPass(pass_name="zentorch_woq_replacement_pass")
+
+# zero-point placeholders a rewrite of the last pass assumed to be zero
+ASSUMED_ZERO_ZP = []
+
+
+def _symmetric_int4(w_node, zp_node) -> bool:
+    """True if the compile-time values show a symmetric signed int4 weight:
+    every zero point 0 and every weight value in [-8, 7]."""
+    zp, w = static_value(zp_node), static_value(w_node)
+    if zp is None or w is None or placeholder_of(zp_node) is None:
+        return False
+    # the passes run under the compile's fake mode; these are real tensors
+    with unset_fake_temporarily():
+        if bool(zp.any()):
+            return False
+        return bool(((w >= -8) & (w <= 7)).all())
 
 
 def _bf16(arg):
@@ -75,7 +92,7 @@ def _dequant_check(has_bias: bool, per_group: bool) -> Callable[[Match], bool]:
     def check(match: Match) -> bool:
         args = list(match.args)
         bias = args.pop(0) if has_bias else None
-        x, w, _zp, scale = args[:4]
+        x, w, zp, scale = args[:4]
         shape = args[4] if per_group else None
         dims = args[-1]
         xv, wv, sv = tensor_meta(x), tensor_meta(w), tensor_meta(scale)
@@ -106,6 +123,9 @@ def _dequant_check(has_bias: bool, per_group: bool) -> Callable[[Match], bool]:
             bv = tensor_meta(bias)
             if bv is None or bv.dim() != 1 or bv.shape[0] != N or not on_gpu(bv):
                 return False
+        if not _symmetric_int4(w, zp):
+            return False
+        ASSUMED_ZERO_ZP.append(placeholder_of(zp))
         return True
 
     return check
@@ -190,8 +210,11 @@ def _register_all() -> None:
 
 
 def replace_with_zentorch_ops_new(fx_graph: Graph) -> Graph:
-    """Apply the WOQ replacement patterns to ``fx_graph`` in place."""
+    """Apply the WOQ replacement patterns to ``fx_graph`` in place; the
+    zero-point placeholders its rewrites assumed zero are in
+    ``ASSUMED_ZERO_ZP`` afterwards."""
     _register_all()
+    ASSUMED_ZERO_ZP.clear()
     if config.pattern_matcher:
         assert fx_graph.owning_module is not None, "Graph has no owning module"
         torch.fx.passes.graph_transform_observer.GraphTransformObserver(

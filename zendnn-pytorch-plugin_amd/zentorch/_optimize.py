@@ -6,17 +6,64 @@ binary-binary (:117) and unary (:118) post-op fusions.  The reference skips
 all passes without AVX-512 (:87-91); here the gate is the graph's device: the
 passes only rewrite subgraphs whose tensors live on the GPU.
 """
+import threading
+
+import torch
+
+from . import _utils
 from ._logging import get_logger
-from ._op_replacements_new import replace_with_zentorch_ops_new
+from ._op_replacements_new import ASSUMED_ZERO_ZP, replace_with_zentorch_ops_new
 from ._woq_linear_binary_binary_fusion import woq_linear_binary_binary_post_op_fusions
 from ._woq_linear_unary_fusion import woq_linear_unary_post_op_fusions
 
 logger = get_logger(__name__)
 
 
-def optimize(fx_graph):
+_checked = {}
+_lock = threading.Lock()
+
+
+def zero_points_guard(zp: torch.Tensor) -> None:
+    """Raise if zero points a compiled graph assumed zero are not (checked
+    once per storage and version, so a forward pays a device sync only the
+    first time and after an in-place update)."""
+    key = (zp.device, zp.data_ptr(), tuple(zp.shape))
+    with _lock:
+        if _checked.get(key) == zp._version:
+            return
+    if bool(zp.any()):
+        raise RuntimeError(
+            "zentorch: this graph was compiled for all-zero weight zero points (symmetric "
+            "int4) and they have changed since; recompile the model")
+    with _lock:
+        _checked[key] = zp._version
+
+
+torch.fx.node._side_effectful_functions.add(zero_points_guard)
+
+
+def _insert_zero_point_guards(fx_graph) -> None:
+    placeholders = [n for n in fx_graph.nodes if n.op == "placeholder"]
+    if not placeholders:
+        return
+    with fx_graph.inserting_after(placeholders[-1]):
+        for zp in dict.fromkeys(ASSUMED_ZERO_ZP):
+            fx_graph.call_function(zero_points_guard, (zp,))
+
+
+def optimize(fx_graph, static_values=None):
+    """Run the WOQ passes on ``fx_graph`` in place.  ``static_values`` maps
+    placeholder nodes to the real tensors they carry when known at compile
+    time (module weights and buffers); the replacement reads zero points
+    from it."""
     logger.info("Optimizing the fx_graph with zentorch ops.")
-    g = replace_with_zentorch_ops_new(fx_graph)
-    g = woq_linear_binary_binary_post_op_fusions(g)
-    g = woq_linear_unary_post_op_fusions(g)
+    _utils.STATIC_VALUES.clear()
+    _utils.STATIC_VALUES.update(static_values or {})
+    try:
+        g = replace_with_zentorch_ops_new(fx_graph)
+        _insert_zero_point_guards(g)
+        g = woq_linear_binary_binary_post_op_fusions(g)
+        g = woq_linear_unary_post_op_fusions(g)
+    finally:
+        _utils.STATIC_VALUES.clear()
     return g

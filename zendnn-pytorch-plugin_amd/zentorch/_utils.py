@@ -42,3 +42,37 @@ PASS_DEVICE_TYPES = ("cuda",)
 def on_gpu(*vals):
     """True if every example tensor lives on a device the ops run on."""
     return all(v is not None and v.device.type in PASS_DEVICE_TYPES for v in vals)
+
+
+# Real values of graph inputs known at compile time (module weights and
+# buffers), keyed by placeholder node; set by optimize() for the duration of
+# the passes.  A pass that needs a value it cannot see leaves its subgraph
+# alone.
+STATIC_VALUES = {}
+
+
+def static_value(node):
+    """The real tensor behind ``node`` (a placeholder, possibly through
+    views), or None when it is not known at compile time."""
+    import torch
+
+    view_ops = (torch.ops.aten.view.default, torch.ops.aten.reshape.default,
+                torch.ops.aten._unsafe_view.default)
+    while isinstance(node, torch.fx.Node) and node.op == "call_function" \
+            and node.target in view_ops:
+        node = node.args[0]
+    if not isinstance(node, torch.fx.Node) or node.op != "placeholder":
+        return None
+    return STATIC_VALUES.get(node)
+
+
+def placeholder_of(node):
+    """The placeholder ``node`` is a view chain of, or None."""
+    import torch
+
+    view_ops = (torch.ops.aten.view.default, torch.ops.aten.reshape.default,
+                torch.ops.aten._unsafe_view.default)
+    while isinstance(node, torch.fx.Node) and node.op == "call_function" \
+            and node.target in view_ops:
+        node = node.args[0]
+    return node if isinstance(node, torch.fx.Node) and node.op == "placeholder" else None
