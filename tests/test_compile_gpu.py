@@ -244,3 +244,35 @@ def test_zero_points_changed_after_compile_rejected():
         model.zero_points.fill_(1)
         with pytest.raises(RuntimeError, match="zero points"):
             fn(x)
+
+
+class GateUpMLP(torch.nn.Module):
+    """vLLM-style merged gate_up + SiluAndMul over a dequantised int4 weight
+    [2I, K] (gate rows first)."""
+
+    def __init__(self, I, K, group_size=None, bias=False, split="split", seed=0):
+        super().__init__()
+        self.lin = WoqLinear(2 * I, K, group_size=group_size, bias=bias, seed=seed)
+        self.I, self.split = I, split
+
+    def forward(self, x):
+        h = self.lin(x)
+        if self.split == "slice":
+            g, u = h[..., :self.I], h[..., self.I:]
+        else:
+            g, u = h.split(self.I, dim=-1)
+        return torch.nn.functional.silu(g) * u
+
+
+@pytest.mark.parametrize("M", [1, 16, 40])
+@pytest.mark.parametrize("split", ["split", "slice"])
+@pytest.mark.parametrize("group_size,bias", [(128, False), (None, True)])
+def test_gate_up_silu_mul_fused(M, split, group_size, bias):
+    I, K = 256, 512
+    model = GateUpMLP(I, K, group_size=group_size, bias=bias, split=split, seed=M)
+    x = torch.randn(M, K).bfloat16()
+    ref, out = compiled_vs_eager(model, x)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
+    assert counters["zentorch"]["zentorch_woq_linear_gate_up_silu_mul"] == 1
+    assert out.shape == (M, I) and out.dtype == torch.bfloat16
+    torch.testing.assert_close(out.float(), ref.float(), **TOL)

@@ -348,3 +348,69 @@ def test_compile_backend_runs_the_passes(cpu_passes):
             torch.compile(M(), backend="zentorch")(x)
     assert counters["zentorch"]["zentorch_woq_linear"] == 1
     torch._dynamo.reset()
+
+
+# ------------------------------------------------------- merged gate_up
+def gate_up_inputs(M=4, I=64, K=256, gs=128):
+    x = torch.randn(M, K).bfloat16()
+    wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (2 * I, K // 8), dtype=torch.int32).t()
+    s = torch.rand(K // gs, 2 * I).bfloat16()
+    b = torch.randn(2 * I).bfloat16()
+    return x, wp, s, b
+
+
+@pytest.mark.parametrize("form", ["split", "chunk", "slice", "view3d", "decomposed_silu",
+                                  "up_first", "bias"])
+def test_gate_up_silu_mul_fused(cpu_passes, form):
+    I = 64
+    x, wp, s, b = gate_up_inputs(I=I)
+    silu = (lambda t: t * torch.sigmoid(t)) if form == "decomposed_silu" else \
+        torch.nn.functional.silu
+
+    def f(x, wp, s, b):
+        h = zt.zentorch_woq_linear(x, wp, s, None, b if form == "bias" else None)
+        if form == "view3d":
+            h = h.view(2, 2, 2 * I)
+        if form == "chunk":
+            g, u = h.chunk(2, dim=-1)
+        elif form == "slice":
+            g, u = h[:, :I], h[:, I:]
+        else:
+            g, u = h.split(I, dim=-1)
+        return u * silu(g) if form == "up_first" else silu(g) * u
+
+    gm = trace(f, x, wp, s, b)
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear_gate_up_silu_mul"] == 1, (form, t)
+    assert zt.zentorch_woq_linear_gate_up_silu_mul.default in t
+    assert zt.zentorch_woq_linear.default not in t
+    assert not {aten.mul.Tensor, aten.sigmoid.default, aten.silu.default} & set(t)
+    node = next(n for n in gm.graph.nodes if n.target == zt.zentorch_woq_linear_gate_up_silu_mul.default)
+    assert (node.args[4] is not None) == (form == "bias")
+    out = [n for n in gm.graph.nodes if n.op == "output"][0].args[0]
+    out = out[0] if isinstance(out, (list, tuple)) else out
+    assert tuple(out.meta["val"].shape) == ((2, 2, I) if form == "view3d" else (4, I))
+
+
+@pytest.mark.parametrize("case", ["uneven_split", "gate_reused", "not_silu", "up_reused"])
+def test_gate_up_left_alone(cpu_passes, case):
+    I = 64
+    x, wp, s, b = gate_up_inputs(I=I)
+
+    def f(x, wp, s, b):
+        h = zt.zentorch_woq_linear(x, wp, s, None, None)
+        if case == "uneven_split":
+            g, u = h[:, :32], h[:, 32:64]
+        else:
+            g, u = h.split(I, dim=-1)
+        act = torch.relu(g) if case == "not_silu" else torch.nn.functional.silu(g)
+        out = act * u
+        if case == "gate_reused":
+            return out, g
+        if case == "up_reused":
+            return out, u
+        return out
+
+    gm = trace(f, x, wp, s, b)
+    run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear_gate_up_silu_mul"] == 0

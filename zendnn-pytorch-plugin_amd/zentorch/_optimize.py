@@ -1,8 +1,10 @@
 """Pass orchestrator for the quantized-linear hot path.
 
 Order follows the reference's optimize() (src/cpu/python/zentorch/_optimize.py:80-160)
-restricted to the WOQ passes: the WOQ op replacement (:104), then the
-binary-binary (:117) and unary (:118) post-op fusions.  The reference skips
+restricted to the WOQ passes: the WOQ op replacement (:104), the merged
+gate_up SiLU-and-mul fusion (the WOQ form of the reference's split-mm
+pattern, _fusion_patterns.py:72-109, applied there in the fusion passes),
+then the binary-binary (:117) and unary (:118) post-op fusions.  The reference skips
 all passes without AVX-512 (:87-91); here the gate is the graph's device: the
 passes only rewrite subgraphs whose tensors live on the GPU.
 """
@@ -14,6 +16,7 @@ from . import _utils
 from ._logging import get_logger
 from ._op_replacements_new import ASSUMED_ZERO_ZP, replace_with_zentorch_ops_new
 from ._woq_linear_binary_binary_fusion import woq_linear_binary_binary_post_op_fusions
+from ._woq_linear_gate_up_fusion import woq_linear_gate_up_fusion
 from ._woq_linear_unary_fusion import woq_linear_unary_post_op_fusions
 
 logger = get_logger(__name__)
@@ -62,6 +65,7 @@ def optimize(fx_graph, static_values=None):
     try:
         g = replace_with_zentorch_ops_new(fx_graph)
         _insert_zero_point_guards(g)
+        g = woq_linear_gate_up_fusion(g)
         g = woq_linear_binary_binary_post_op_fusions(g)
         g = woq_linear_unary_post_op_fusions(g)
     finally:
