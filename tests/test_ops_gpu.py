@@ -247,3 +247,23 @@ def test_dynamic_qlinear_op_under_graph_capture():
         torch.cuda.synchronize()
         assert torch.equal(y_graph, eager)
     torch.testing.assert_close(eager.cpu().float(), O.dynamic_qlinear(x, w, sw, b).float(), **TOL)
+
+
+# extension ops: dynamic qlinear with a fused silu * mul or residual add
+@pytest.mark.parametrize("M,N,K", [(4, 96, 256), (128, 11008, 4096), (300, 136, 1024),
+                                   (2048, 512, 1024)])
+@pytest.mark.parametrize("op", ["silu_mul", "add"])
+def test_dynamic_qlinear_fused_epilogue_ops(M, N, K, op):
+    x, w, sw, b = dyn_case(M, N, K, seed=M + N + K)
+    g = torch.Generator().manual_seed(M)
+    other = torch.randn(M, N, generator=g).bfloat16()
+    post = ("silu", "mul") if op == "silu_mul" else ("add",)
+    ref = O.dynamic_qlinear(x, w, sw, b, post_ops=post, post_bufs=[other])
+    fn = getattr(torch.ops.zentorch, f"zentorch_dynamic_qlinear_{op}")
+    y = fn(x.to(DEV), w.to(DEV), sw.to(DEV), other.to(DEV), b.to(DEV))
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    torch.testing.assert_close(y.cpu().float(), ref.float(), **TOL)
+    # 3-D input and operand
+    y3 = fn(x.view(1, M, K).to(DEV), w.to(DEV), sw.to(DEV), other.view(1, M, N).to(DEV),
+            b.to(DEV))
+    assert torch.equal(y3.view(M, N), y)

@@ -368,11 +368,16 @@ at::Tensor woq_repack_from_int4pack(const at::Tensor &packed_weight) {
   return out;
 }
 
-at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
-                           const at::Tensor &weight_scales,
-                           const c10::optional<at::Tensor> &bias,
-                           c10::string_view zentorch_op_name) {
-  const std::string name(zentorch_op_name);
+namespace {
+
+// Shared body of zentorch_dynamic_qlinear and its fused-epilogue
+// extensions: post_ids in list order, binary operands [*, N] in order.
+at::Tensor dynamic_qlinear_impl(const at::Tensor &input, const at::Tensor &weight,
+                                const at::Tensor &weight_scales,
+                                const c10::optional<at::Tensor> &bias,
+                                const std::vector<int32_t> &post_ids,
+                                const std::vector<at::Tensor> &binary_inputs,
+                                const std::string &name) {
   // dtype / size checks with the messages of DynamicQLinear.cpp:15-70.
   TORCH_CHECK(input.scalar_type() == at::kBFloat16 ||
                   input.scalar_type() == at::kFloat,
@@ -425,17 +430,71 @@ at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
   at::Tensor wc = weight.contiguous();
   at::Tensor sc = weight_scales.contiguous();
   at::Tensor bc = b.defined() ? b.contiguous() : b;
+  zt_post_ops post{};
+  post.count = (int32_t)post_ids.size();
+  std::vector<at::Tensor> keep;
+  size_t nb = 0;
+  for (size_t i = 0; i < post_ids.size(); ++i) {
+    post.ids[i] = post_ids[i];
+    if (post_ids[i] == ZT_PO_ADD || post_ids[i] == ZT_PO_MUL) {
+      const at::Tensor &bi = binary_inputs[nb];
+      check_device(bi, input, op, "binary post-op input");
+      TORCH_CHECK(bi.numel() == M * N && bi.size(-1) == N, name,
+                  ": binary post-op input must have the output's shape [*, ", N, "], got ",
+                  bi.sizes());
+      at::Tensor bt = bi;
+      if (bt.scalar_type() != at::kBFloat16 && bt.scalar_type() != at::kFloat)
+        bt = bt.to(input.scalar_type());
+      int64_t ld = N;
+      bt = rows_view(bt, &ld);
+      keep.push_back(bt);
+      post.bufs[nb] = bt.data_ptr();
+      post.buf_dtypes[nb] = zt_dtype_of(bt);
+      post.buf_ld[nb] = ld;
+      ++nb;
+    }
+  }
   const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K);
   const at::Tensor ws = call_workspace(input, ws_bytes);
   const int rc = zt_dynamic_qlinear(
       x2.data_ptr(), zt_dtype_of(x2), M, K,
       reinterpret_cast<const int8_t *>(wc.data_ptr()), N, sc.data_ptr(),
       zt_dtype_of(sc), bc.defined() ? bc.data_ptr() : nullptr,
-      bc.defined() ? zt_dtype_of(bc) : ZT_DT_NONE, nullptr, result.data_ptr(),
-      zt_dtype_of(result), ws.data_ptr(), ws_bytes,
+      bc.defined() ? zt_dtype_of(bc) : ZT_DT_NONE, post.count ? &post : nullptr,
+      result.data_ptr(), zt_dtype_of(result), ws.data_ptr(), ws_bytes,
       reinterpret_cast<zt_stream_t>(current_stream()));
   TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
   return result;
+}
+
+}  // namespace
+
+at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
+                           const at::Tensor &weight_scales,
+                           const c10::optional<at::Tensor> &bias,
+                           c10::string_view zentorch_op_name) {
+  return dynamic_qlinear_impl(input, weight, weight_scales, bias, {}, {},
+                              std::string(zentorch_op_name));
+}
+
+// Extensions: the reference's dynamic qlinear has no fused post-ops
+// (docs/zentorch_dynamic_qlinear.md:99).  silu(linear) * mul_input (the gate
+// of a gated MLP) and linear + add_input (a residual), in fp32 before the one
+// rounding, as zentorch_woq_linear_silu_mul / _add do.
+at::Tensor dynamic_qlinear_silu_mul(const at::Tensor &input, const at::Tensor &weight,
+                                    const at::Tensor &weight_scales, const at::Tensor &mul_input,
+                                    const c10::optional<at::Tensor> &bias,
+                                    c10::string_view zentorch_op_name) {
+  return dynamic_qlinear_impl(input, weight, weight_scales, bias, {ZT_PO_SILU, ZT_PO_MUL},
+                              {mul_input}, std::string(zentorch_op_name));
+}
+
+at::Tensor dynamic_qlinear_add(const at::Tensor &input, const at::Tensor &weight,
+                               const at::Tensor &weight_scales, const at::Tensor &add_input,
+                               const c10::optional<at::Tensor> &bias,
+                               c10::string_view zentorch_op_name) {
+  return dynamic_qlinear_impl(input, weight, weight_scales, bias, {ZT_PO_ADD}, {add_input},
+                              std::string(zentorch_op_name));
 }
 
 // zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema :728-736)
@@ -583,6 +642,15 @@ TORCH_LIBRARY(zentorch, m) {
         "Tensor weight_scales, Tensor? bias=None, *, "
         "str zentorch_op_name="
         "'zentorch::zentorch_dynamic_qlinear') -> Tensor");
+  // Extensions: dynamic qlinear with fused silu * mul and residual add.
+  m.def("zentorch_dynamic_qlinear_silu_mul(Tensor input, Tensor weight, "
+        "Tensor weight_scales, Tensor mul_input, Tensor? bias=None, *, "
+        "str zentorch_op_name='zentorch::zentorch_dynamic_qlinear_silu_mul') -> Tensor",
+        {at::Tag::needs_fixed_stride_order});
+  m.def("zentorch_dynamic_qlinear_add(Tensor input, Tensor weight, "
+        "Tensor weight_scales, Tensor add_input, Tensor? bias=None, *, "
+        "str zentorch_op_name='zentorch::zentorch_dynamic_qlinear_add') -> Tensor",
+        {at::Tag::needs_fixed_stride_order});
   m.def("zentorch_fused_moe(Tensor(a!) output, Tensor input, "
         "Tensor w13, Tensor w2, "
         "Tensor? w13_bias, Tensor? w2_bias, "
@@ -608,5 +676,7 @@ TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
   m.impl("zentorch_woq_repack_weight", woq_repack_weight);
   m.impl("zentorch_woq_repack_from_int4pack", woq_repack_from_int4pack);
   m.impl("zentorch_dynamic_qlinear", dynamic_qlinear);
+  m.impl("zentorch_dynamic_qlinear_silu_mul", dynamic_qlinear_silu_mul);
+  m.impl("zentorch_dynamic_qlinear_add", dynamic_qlinear_add);
   m.impl("zentorch_fused_moe", fused_moe);
 }

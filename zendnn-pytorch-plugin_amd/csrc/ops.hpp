@@ -72,5 +72,13 @@ at::Tensor dynamic_qlinear(const at::Tensor &input, const at::Tensor &weight,
                            const at::Tensor &weight_scales,
                            const c10::optional<at::Tensor> &bias,
                            c10::string_view zentorch_op_name);
+at::Tensor dynamic_qlinear_silu_mul(const at::Tensor &input, const at::Tensor &weight,
+                                    const at::Tensor &weight_scales, const at::Tensor &mul_input,
+                                    const c10::optional<at::Tensor> &bias,
+                                    c10::string_view zentorch_op_name);
+at::Tensor dynamic_qlinear_add(const at::Tensor &input, const at::Tensor &weight,
+                               const at::Tensor &weight_scales, const at::Tensor &add_input,
+                               const c10::optional<at::Tensor> &bias,
+                               c10::string_view zentorch_op_name);
 
 }  // namespace zentorch_hip

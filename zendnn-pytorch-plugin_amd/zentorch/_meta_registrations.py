@@ -80,6 +80,18 @@ def meta_zentorch_dynamic_qlinear(input, weight, weight_scales, bias=None,
     return input.new_empty(out)
 
 
+@register_meta("zentorch_dynamic_qlinear_silu_mul")
+def meta_zentorch_dynamic_qlinear_silu_mul(input, weight, weight_scales, mul_input, bias=None,
+                                           zentorch_op_name=""):
+    return meta_zentorch_dynamic_qlinear(input, weight, weight_scales, bias)
+
+
+@register_meta("zentorch_dynamic_qlinear_add")
+def meta_zentorch_dynamic_qlinear_add(input, weight, weight_scales, add_input, bias=None,
+                                      zentorch_op_name=""):
+    return meta_zentorch_dynamic_qlinear(input, weight, weight_scales, bias)
+
+
 @register_meta("zentorch_woq_repack_weight")
 def meta_zentorch_woq_repack_weight(unpacked_weight):
     # [N, K/8] int32 (the reference's meta returns the input dtype, int8, which
