@@ -88,6 +88,19 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear(
     AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
     AtenTensorHandle *B, const char *zentorch_op_name, AtenTensorHandle *ret0);
 
+/* No reference counterpart: shims of the dynamic-qlinear extensions with a
+ * fused silu * mul or residual add, shaped like the dynamic_qlinear shim with
+ * the binary operand after the weight scales. */
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear_silu_mul(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
+    AtenTensorHandle mul_input, AtenTensorHandle *B, const char *zentorch_op_name,
+    AtenTensorHandle *ret0);
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear_add(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
+    AtenTensorHandle add_input, AtenTensorHandle *B, const char *zentorch_op_name,
+    AtenTensorHandle *ret0);
+
 #ifdef __cplusplus
 }
 #endif

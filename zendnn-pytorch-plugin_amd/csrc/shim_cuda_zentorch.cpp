@@ -107,4 +107,26 @@ AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear(
   });
 }
 
+AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear_silu_mul(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
+    AtenTensorHandle mul_input, AtenTensorHandle *B, const char *zentorch_op_name,
+    AtenTensorHandle *ret0) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    auto r = zentorch_hip::dynamic_qlinear_silu_mul(ZT_T(X), ZT_T(W), ZT_T(weight_scales),
+                                                    ZT_T(mul_input), ZT_OPT(B), zentorch_op_name);
+    *ret0 = new_tensor_handle(std::move(r));
+  });
+}
+
+AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear_add(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle weight_scales,
+    AtenTensorHandle add_input, AtenTensorHandle *B, const char *zentorch_op_name,
+    AtenTensorHandle *ret0) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    auto r = zentorch_hip::dynamic_qlinear_add(ZT_T(X), ZT_T(W), ZT_T(weight_scales),
+                                               ZT_T(add_input), ZT_OPT(B), zentorch_op_name);
+    *ret0 = new_tensor_handle(std::move(r));
+  });
+}
+
 }  // extern "C"

@@ -4,7 +4,8 @@ Importing the package loads the two in-tree native libraries
 (libzentorch_hip.so: HIP kernels + C-ABI; _C.so: TORCH_LIBRARY(zentorch) +
 AOTInductor shims) with RTLD_GLOBAL, as the reference loads libzentorch.so
 (src/cpu/python/zentorch/__init__.py:69-78), then registers the Meta kernels
-and the ``"zentorch"`` torch.compile backend.  A missing library is an
+the ``"zentorch"`` torch.compile backend and the Inductor lowerings that
+call the ops' AOTInductor shims.  A missing library is an
 ImportError: there is no CPU fallback.
 """
 import ctypes
@@ -38,6 +39,7 @@ _hip = _load_native()
 from . import _meta_registrations  # noqa: E402,F401
 from ._utils import counters  # noqa: E402,F401
 from ._compile_backend import zentorch  # noqa: E402,F401
+from . import _lowerings  # noqa: E402,F401
 
 
 def native_libraries():
