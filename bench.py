@@ -29,6 +29,7 @@ bounded sample of the same workload on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME]
        python bench.py --only traffic   (eager launches for rocprofv3 --pmc)
+       python bench.py --only pmc       (eager GEMM launches for the MFMA counters)
 """
 import argparse
 import json
@@ -224,6 +225,28 @@ def traffic_pass(gen):
     torch.cuda.synchronize()
     print(json.dumps({"traffic_pass": "done", "woq_calls": 64, "copy_calls": 16,
                       "copy_bytes_each_way": CAL_BYTES}))
+
+
+def pmc_pass(gen):
+    """Eager launches of the GEMM workloads for rocprofv3 --pmc runs (MFMA
+    counters): 4 calls of BASELINE config 1 (dynamic qlinear M=128, N=11008,
+    K=4096), then 2 calls of each Llama-3-8B layer GEMM at M=2048, int8
+    dynamic qlinear and int4 WOQ."""
+    dyn = DynLinear(128, 11008, 4096, gen=gen)
+    for _ in range(4):
+        dyn()
+    for N, K in [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]:
+        lin = DynLinear(2048, N, K, gen=gen)
+        for _ in range(2):
+            lin()
+        del lin
+    for _, N, K, _post in LLAMA:
+        lin = WoqLinear(2048, N, K, gen=gen)
+        for _ in range(2):
+            lin()
+        del lin
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": "done", "config1_calls": 4, "prefill_calls_per_shape": 2}))
 
 
 def read_traffic():
@@ -466,7 +489,8 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default=None,
-                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | moe | traffic")
+                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | moe | traffic"
+                         " | pmc")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline-child", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -484,6 +508,9 @@ def main():
         only = args.only
         if only == "traffic":
             traffic_pass(gen)
+            return
+        if only == "pmc":
+            pmc_pass(gen)
             return
         res = {}
         if only in (None, "config0"):

@@ -199,6 +199,47 @@ int zt_dynamic_quantize(const void *x, int32_t x_dtype, int64_t M, int64_t K,
 int zt_s8s8s32_gemm(const int8_t *qa, const int8_t *w, int64_t M, int64_t N,
                     int64_t K, int32_t *acc, zt_stream_t stream);
 
+/*
+ * Dynamic int8 linear with per-token ASYMMETRIC uint8 activations.  No
+ * counterpart in the reference, whose dynamic qlinear is symmetric s8
+ * (DynamicQLinear.cpp:94-110); this is an opt-in for callers whose
+ * activations are one-signed (after SiLU / GELU / ReLU), where a zero point
+ * spends all 256 levels on the row's range.  Per row m:
+ *   lo = min(0, min_k x), hi = max(0, max_k x),
+ *   sx = max(hi - lo, 1e-12) / 255, zp = clamp(rint(-lo / sx), 0, 255),
+ *   q  = clamp(rint(x / sx) + zp, 0, 255)       (fp32, rint half-to-even)
+ *   y  = (float)(sum_k (q - zp) * w[n][k]) * sx * sw[n] + bias[n]
+ * The GEMM runs on q - 128 stored as s8 (the symmetric kernels unchanged)
+ * and the epilogue subtracts (zp - 128) * w_colsum[n] from each int32
+ * accumulator, which is exact.
+ *
+ *  w_colsum  [N] int32, sum_k w[n][k] (zt_s8_weight_colsum), 16-byte aligned;
+ *            computed once per weight and kept beside it
+ *  y_dtype   bf16 / fp32, or ZT_DT_S32 for the corrected accumulators
+ *            sum_k (q - zp) * w exactly (no scales, bias or post-ops)
+ *  workspace zt_dynamic_qlinear_asym_workspace_size(M, K) bytes
+ * Other arguments as zt_dynamic_qlinear.
+ */
+int zt_dynamic_qlinear_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                            const int8_t *w, int64_t N, const void *w_scales,
+                            int32_t w_scales_dtype, const int32_t *w_colsum,
+                            const void *bias, int32_t bias_dtype, const zt_post_ops *post,
+                            void *y, int32_t y_dtype, void *workspace,
+                            size_t workspace_bytes, zt_stream_t stream);
+
+size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K);
+
+/* The asymmetric quantisation stage on its own (same kernel): qx[M, K] =
+ * q - 128 as int8, sx[M] fp32, azp[M] = zp - 128 int32.  No reference
+ * counterpart (extension above). */
+int zt_dynamic_quantize_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                             int8_t *qx, float *sx, int32_t *azp, zt_stream_t stream);
+
+/* colsum[n] = sum_k w[n][k] of an int8 [N, K] row-major weight, exactly in
+ * int32.  No reference counterpart (extension above). */
+int zt_s8_weight_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,
+                        zt_stream_t stream);
+
 /* Repack int8 [N, K] int4 values into int32 [N, K/8] on the GPU.
  * Replaces zentorch_woq_repack_weight (src/cpu/cpp/WOQ_Linear.cpp:294-357). */
 int zt_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out,

@@ -51,6 +51,10 @@ def lib():
         L.zto_dynamic_qlinear.argtypes = [
             _vp, _int, _i64, _i64, _vp, _i64, _vp, _int, _vp, _int, _int, _vp,
             _vp, _vp, _vp, _vp, _int, _vp, _vp, _vp, _int]
+        L.zto_dynamic_quantize_asym.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int]
+        L.zto_dynamic_qlinear_asym.argtypes = [
+            _vp, _int, _i64, _i64, _vp, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp,
+            _int]
         L.zto_woq_moe.argtypes = [
             _vp, _i64, _i64, _vp, _vp, _int, _i64, _int, _int, _vp, _vp, _i64, _vp, _vp,
             _vp, _i64, _vp, _i64, _i64, _vp, _int]
@@ -176,6 +180,38 @@ def dynamic_qlinear(x, w, w_scales, bias=None, post_ops=(), post_bufs=(),
     if return_intermediates:
         return y, qx, sx, acc
     return y
+
+
+def dynamic_quantize_asym(x, nthreads=0):
+    """Per-token asymmetric uint8 (extension, zt_oracle.c): returns
+    (q uint8 [M,K], sx fp32 [M], zp int32 [M])."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    q = torch.empty(M, K, dtype=torch.uint8)
+    sx = torch.empty(M, dtype=torch.float32)
+    zp = torch.empty(M, dtype=torch.int32)
+    lib().zto_dynamic_quantize_asym(_ptr(x2), DT[x2.dtype], M, K, _ptr(q), _ptr(sx), _ptr(zp),
+                                    nthreads)
+    return q, sx, zp
+
+
+def dynamic_qlinear_asym(x, w, w_scales, bias=None, out_dtype=None, nthreads=0):
+    """zentorch_dynamic_qlinear_asym semantics (extension, zt_oracle.c);
+    out_dtype torch.int32 returns sum_k (q - zp) * w."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    wc = w.contiguous()
+    N = wc.shape[0]
+    sw = w_scales.reshape(-1).contiguous()
+    b = bias.contiguous() if bias is not None else None
+    y = torch.empty(M, N, dtype=out_dtype or x.dtype)
+    lib().zto_dynamic_qlinear_asym(
+        _ptr(x2), DT[x2.dtype], M, K, _ptr(wc), N, _ptr(sw), DT[sw.dtype],
+        _ptr(b), DT[b.dtype] if b is not None else -1, _ptr(y), DT[y.dtype],
+        None, None, None, nthreads)
+    return y.reshape(*x.shape[:-1], N)
 
 
 MOE_ACT = {"silu": PO["silu"], "gelu": PO["gelu_erf"], "gelu_tanh": PO["gelu_tanh"]}

@@ -27,6 +27,15 @@
  *                           (compute=s8, transB=true, ldb=K).
  *   zto_dynamic_qlinear     DynamicQLinear.cpp:74-181: y = acc*sx[m]*sw[n] + b[n]
  *                           in fp32, rounded once to the output dtype.
+ *   zto_dynamic_quantize_asym, zto_dynamic_qlinear_asym
+ *                           no reference counterpart: the per-token
+ *                           asymmetric-uint8 opt-in beside the reference's
+ *                           symmetric s8 (DynamicQLinear.cpp:94-110); the
+ *                           epilogue is zto_dynamic_qlinear's with
+ *                           acc = sum_k (q - zp) * w.  Parity unpinned by the
+ *                           reference (no golden data exists); pinned by the
+ *                           round-trip, zero-point and range identities the
+ *                           CPU tests check.
  *   zto_woq_moe             FusedMoE.cpp:443-700 and the per-expert loop of
  *                           vllm/_int8_moe_patch.py:149-206 with int4 expert
  *                           weights: per (token, k) pair of expert e,
@@ -354,6 +363,74 @@ int zto_dynamic_qlinear(const void *x, int x_dt, int64_t M, int64_t K,
   if (!qx_out) free(qx);
   if (!sx_out) free(sx);
   if (!acc_out) free(acc);
+  return ZTO_OK;
+}
+
+/* Per-token asymmetric uint8 (extension).  fp32 after the exact widening:
+ *   lo = min(0, min_k x), hi = max(0, max_k x)
+ *   sx = max(hi - lo, 1e-12f) / 255.0f              (IEEE divide)
+ *   zp = clamp(rint(-lo / sx), 0, 255)
+ *   q  = clamp(rint(x / sx) + zp, 0, 255)           (rint: half to even) */
+int zto_dynamic_quantize_asym(const void *x, int x_dt, int64_t M, int64_t K,
+                              uint8_t *q, float *sx, int32_t *zp, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    float lo = 0.f, hi = 0.f;
+    for (int64_t k = 0; k < K; ++k) {
+      const float v = load_f(x, x_dt, m * K + k);
+      lo = v < lo ? v : lo;
+      hi = v > hi ? v : hi;
+    }
+    float range = hi - lo;
+    if (!(range >= 1e-12f)) range = 1e-12f;
+    const float s = range / 255.0f;
+    float z = rintf(-lo / s);
+    z = z < 0.f ? 0.f : (z > 255.f ? 255.f : z);
+    sx[m] = s;
+    zp[m] = (int32_t)z;
+    for (int64_t k = 0; k < K; ++k) {
+      float r = rintf(load_f(x, x_dt, m * K + k) / s) + z;
+      r = r < 0.f ? 0.f : (r > 255.f ? 255.f : r);
+      q[m * K + k] = (uint8_t)r;
+    }
+  }
+  return ZTO_OK;
+}
+
+/* y = ((float)acc * sx[m]) * sw[n] + b[n] with acc = sum_k (q - zp[m]) *
+ * w[n,k] exactly (int64, then int32: |acc| < 2^31 for K < 2^16); y_dt
+ * ZT_DT_S32 stores acc itself.  q/sx/zp go to the optional out pointers. */
+int zto_dynamic_qlinear_asym(const void *x, int x_dt, int64_t M, int64_t K,
+                             const int8_t *w, int64_t N, const void *sw, int sw_dt,
+                             const void *bias, int b_dt, void *y, int y_dt,
+                             uint8_t *q_out, float *sx_out, int32_t *zp_out, int nthreads) {
+  uint8_t *q = q_out ? q_out : (uint8_t *)malloc((size_t)(M * K > 0 ? M * K : 1));
+  float *sx = sx_out ? sx_out : (float *)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1));
+  int32_t *zp = zp_out ? zp_out : (int32_t *)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
+  if (!q || !sx || !zp) return ZTO_EINVAL;
+  zto_dynamic_quantize_asym(x, x_dt, M, K, q, sx, zp, nthreads);
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      int64_t a = 0;
+      for (int64_t k = 0; k < K; ++k)
+        a += ((int64_t)q[m * K + k] - zp[m]) * (int64_t)w[n * K + k];
+      const int32_t acc = (int32_t)a;
+      if (y_dt == ZT_DT_S32) {
+        ((int32_t *)y)[m * N + n] = acc;
+        continue;
+      }
+      float v = (float)acc * sx[m];
+      v = v * load_f(sw, sw_dt, n);
+      if (bias) v = v + load_f(bias, b_dt, n);
+      store_f(y, y_dt, m * N + n, v);
+    }
+  }
+  if (!q_out) free(q);
+  if (!sx_out) free(sx);
+  if (!zp_out) free(zp);
   return ZTO_OK;
 }
 

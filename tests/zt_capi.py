@@ -53,6 +53,13 @@ def lib():
         L.zt_dynamic_qlinear_workspace_size.restype = _sz
         L.zt_dynamic_quantize.argtypes = [_vp, _i32, _i64, _i64, _vp, _vp, _vp]
         L.zt_s8s8s32_gemm.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp]
+        L.zt_dynamic_qlinear_asym.argtypes = [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _i32,
+                                              _vp, _vp, _i32, ctypes.POINTER(PostOps), _vp,
+                                              _i32, _vp, _sz, _vp]
+        L.zt_dynamic_qlinear_asym_workspace_size.argtypes = [_i64, _i64]
+        L.zt_dynamic_qlinear_asym_workspace_size.restype = _sz
+        L.zt_dynamic_quantize_asym.argtypes = [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp]
+        L.zt_s8_weight_colsum.argtypes = [_vp, _i64, _i64, _vp, _vp]
         L.zt_woq_repack_weight.argtypes = [_vp, _i64, _i64, _vp, _vp]
         L.zt_woq_repack_from_int4pack.argtypes = [_vp, _i64, _i64, _vp, _vp]
         L.zt_woq_moe.argtypes = [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp,
@@ -198,6 +205,49 @@ def dynamic_quantize(x):
     _check(lib().zt_dynamic_quantize(_p(x2), DT[x2.dtype], M, K, _p(qx), _p(sx), _stream()))
     torch.cuda.synchronize()
     return qx, sx
+
+
+def s8_weight_colsum(w):
+    N, K = w.shape
+    out = torch.empty(N, dtype=torch.int32, device=w.device)
+    _check(lib().zt_s8_weight_colsum(_p(w), N, K, _p(out), _stream()))
+    torch.cuda.synchronize()
+    return out
+
+
+def dynamic_quantize_asym(x):
+    """(qx int8 = q - 128, sx fp32, azp int32 = zp - 128)."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    qx = torch.empty(M, K, dtype=torch.int8, device=x.device)
+    sx = torch.empty(M, dtype=torch.float32, device=x.device)
+    azp = torch.empty(M, dtype=torch.int32, device=x.device)
+    _check(lib().zt_dynamic_quantize_asym(_p(x2), DT[x2.dtype], M, K, _p(qx), _p(sx), _p(azp),
+                                          _stream()))
+    torch.cuda.synchronize()
+    return qx, sx, azp
+
+
+def dynamic_qlinear_asym(x, w, sw, colsum, bias=None, out_dtype=None, post_ops=(),
+                         post_bufs=()):
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    N = w.shape[0]
+    y = torch.empty(M, N, dtype=out_dtype or x.dtype, device=x.device)
+    po, keep = make_post(post_ops, post_bufs, N)
+    ws_bytes = lib().zt_dynamic_qlinear_asym_workspace_size(M, K)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    rc = lib().zt_dynamic_qlinear_asym(
+        _p(x2), DT[x2.dtype], M, K, _p(w), N, _p(sw), DT[sw.dtype], _p(colsum), _p(bias),
+        DT[bias.dtype] if bias is not None else -1,
+        ctypes.byref(po) if post_ops else None, _p(y), DT[y.dtype], _p(ws), ws_bytes,
+        _stream())
+    _check(rc)
+    torch.cuda.synchronize()
+    del keep
+    return y
 
 
 def s8s8s32_gemm(qa, w):

@@ -455,14 +455,17 @@ int zt_s8s8s32_gemm(const int8_t *qa, const int8_t *w, int64_t M, int64_t N,
   return hip_status(zt::launch_s8_gemm(a, reinterpret_cast<hipStream_t>(stream)), op);
 }
 
-int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
-                       const int8_t *w, int64_t N, const void *w_scales,
-                       int32_t w_scales_dtype, const void *bias,
-                       int32_t bias_dtype, const zt_post_ops *post, void *y,
-                       int32_t y_dtype, void *workspace, size_t workspace_bytes,
-                       zt_stream_t stream) {
-  static const char *op = "zt_dynamic_qlinear";
-  if (!is_float_dt(x_dtype) || !is_float_dt(y_dtype))
+// The dynamic qlinear of both quantisation schemes: symmetric s8 when
+// colsum is null, per-token asymmetric u8 otherwise (the azp row offsets
+// then follow sx in the workspace).
+static int dynamic_qlinear_common(const char *op, const void *x, int32_t x_dtype, int64_t M,
+                                  int64_t K, const int8_t *w, int64_t N, const void *w_scales,
+                                  int32_t w_scales_dtype, const int32_t *colsum,
+                                  const void *bias, int32_t bias_dtype, const zt_post_ops *post,
+                                  void *y, int32_t y_dtype, void *workspace,
+                                  size_t workspace_bytes, zt_stream_t stream) {
+  const bool asym = colsum != nullptr;
+  if (!is_float_dt(x_dtype) || !(is_float_dt(y_dtype) || (asym && y_dtype == ZT_DT_S32)))
     return fail(ZT_EINVAL, "%s: input and output must be bf16 or fp32", op);
   if (!is_float_dt(w_scales_dtype))
     return fail(ZT_EINVAL, "%s: weight_scales must be float32 or bfloat16", op);
@@ -471,7 +474,10 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   if (M < 0 || N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
   if (M == 0 || N == 0) return ZT_OK;
   if (!x || !w || !w_scales || !y) return fail(ZT_EINVAL, "%s: null pointer", op);
-  const size_t need = zt_dynamic_qlinear_workspace_size(M, K);
+  if (asym && (reinterpret_cast<uintptr_t>(colsum) & 15u))
+    return fail(ZT_EINVAL, "%s: weight_colsum must be 16-byte aligned", op);
+  const size_t need = asym ? zt_dynamic_qlinear_asym_workspace_size(M, K)
+                           : zt_dynamic_qlinear_workspace_size(M, K);
   if (!workspace || workspace_bytes < need)
     return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op,
                 need, workspace ? workspace_bytes : (size_t)0);
@@ -482,14 +488,68 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
   a.y = y, a.y_dt = y_dtype;
   int rc = convert_post_ops(post, &a.post, op);
   if (rc) return rc;
-  int8_t *qx = reinterpret_cast<int8_t *>(workspace);
-  float *sx = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + dyn_qx_bytes(M, K));
-  a.qx = qx, a.sx = sx;
+  char *ws = reinterpret_cast<char *>(workspace);
+  int8_t *qx = reinterpret_cast<int8_t *>(ws);
+  float *sx = reinterpret_cast<float *>(ws + dyn_qx_bytes(M, K));
+  int32_t *azp = asym ? reinterpret_cast<int32_t *>(ws + dyn_qx_bytes(M, K) + M * 4) : nullptr;
+  a.qx = qx, a.sx = sx, a.azp = azp, a.colsum = colsum;
   a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s), op);
+  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s, azp), op);
   if (rc) return rc;
   return hip_status(zt::launch_s8_gemm(a, s), op);
+}
+
+int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                       const int8_t *w, int64_t N, const void *w_scales,
+                       int32_t w_scales_dtype, const void *bias,
+                       int32_t bias_dtype, const zt_post_ops *post, void *y,
+                       int32_t y_dtype, void *workspace, size_t workspace_bytes,
+                       zt_stream_t stream) {
+  return dynamic_qlinear_common("zt_dynamic_qlinear", x, x_dtype, M, K, w, N, w_scales,
+                                w_scales_dtype, nullptr, bias, bias_dtype, post, y, y_dtype,
+                                workspace, workspace_bytes, stream);
+}
+
+size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  return dyn_qx_bytes(M, K) + (size_t)M * (sizeof(float) + sizeof(int32_t));
+}
+
+int zt_dynamic_quantize_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                             int8_t *qx, float *sx, int32_t *azp, zt_stream_t stream) {
+  static const char *op = "zt_dynamic_quantize_asym";
+  if (!is_float_dt(x_dtype))
+    return fail(ZT_EINVAL, "%s: input must be bf16 or fp32", op);
+  if (M < 0 || K < 1) return fail(ZT_EINVAL, "%s: need M >= 0, K >= 1", op);
+  if (M == 0) return ZT_OK;
+  if (!x || !qx || !sx || !azp) return fail(ZT_EINVAL, "%s: null pointer", op);
+  return hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, false,
+                                            reinterpret_cast<hipStream_t>(stream), azp),
+                    op);
+}
+
+int zt_s8_weight_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,
+                        zt_stream_t stream) {
+  static const char *op = "zt_s8_weight_colsum";
+  if (N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
+  if (N == 0) return ZT_OK;
+  if (!w || !colsum) return fail(ZT_EINVAL, "%s: null pointer", op);
+  return hip_status(zt::launch_s8_colsum(w, N, K, colsum, reinterpret_cast<hipStream_t>(stream)),
+                    op);
+}
+
+int zt_dynamic_qlinear_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
+                            const int8_t *w, int64_t N, const void *w_scales,
+                            int32_t w_scales_dtype, const int32_t *w_colsum,
+                            const void *bias, int32_t bias_dtype, const zt_post_ops *post,
+                            void *y, int32_t y_dtype, void *workspace,
+                            size_t workspace_bytes, zt_stream_t stream) {
+  if (!w_colsum && M > 0 && N > 0)
+    return fail(ZT_EINVAL, "zt_dynamic_qlinear_asym: null weight_colsum");
+  return dynamic_qlinear_common("zt_dynamic_qlinear_asym", x, x_dtype, M, K, w, N, w_scales,
+                                w_scales_dtype, w_colsum, bias, bias_dtype, post, y, y_dtype,
+                                workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -11,6 +11,13 @@
 //    y = ((float)acc * sx[m]) * sw[n] + bias[n] (+ post-ops), or the raw
 //    int32 accumulators.
 //  * s8_generic_kernel    K not a multiple of 16: one wave per output.
+//
+// Per-token asymmetric uint8 (an opt-in beside the reference's symmetric
+// s8): lo = min(0, min_k x), hi = max(0, max_k x), sx = max(hi - lo, 1e-12)
+// / 255, zp = clamp(rint(-lo / sx), 0, 255), q = clamp(rint(x / sx) + zp,
+// 0, 255).  qx stores q - 128 as s8 so the s8 x s8 GEMMs run unchanged, and
+// the epilogue subtracts (zp - 128) * colsum[n] from the int32 accumulator,
+// which leaves sum_k (q - zp) * w exactly.
 #include <cstdio>
 #include <cstdlib>
 
@@ -31,29 +38,74 @@ __device__ __forceinline__ int64_t qx_frag_offset(int64_t m, int64_t k, int64_t 
          ((((k >> 5) & 1) * 32 + (m & 31)) * 16) + (k & 15);
 }
 
+// Row scale (and zero point) from the row's extremes: symmetric s8 from
+// lo = -amax, hi = amax; asymmetric u8 from lo <= 0 <= hi.  Sets s and the
+// value added to rint(x / s) before the clamp to [qlo, qlo + 255].
+template <bool ASYM>
+__device__ __forceinline__ void row_qparams(float lo, float hi, float &s, float &zp) {
+  if (ASYM) {
+    float range = hi - lo;
+    if (!(range >= 1e-12f)) range = 1e-12f;
+    s = __fdiv_rn(range, 255.0f);
+    zp = fminf(fmaxf(rintf(__fdiv_rn(-lo, s)), 0.f), 255.f);
+  } else {
+    float amax = hi;
+    if (!(amax >= 1e-12f)) amax = 1e-12f;
+    s = __fdiv_rn(amax, 127.0f);
+    zp = 0.f;
+  }
+}
+
+// q as stored in qx: clamp(rint(x / s) + zp) in [-128, 127] (symmetric) or
+// [0, 255] (asymmetric, stored minus 128)
+template <bool ASYM>
+__device__ __forceinline__ int quant_one(float x, float s, float zp) {
+  float r = rintf(__fdiv_rn(x, s));
+  if (ASYM) return (int)fminf(fmaxf(r + zp, 0.f), 255.f) - 128;
+  return (int)fminf(fmaxf(r, -128.f), 127.f);
+}
+
+// Reduce (lo, hi) over the 256 threads; returns the workgroup's values.
+__device__ __forceinline__ void block_minmax(float &lo, float &hi, float *red, int tid) {
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, kWave));
+    hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+  }
+  if (lane == 0) red[wv] = lo, red[4 + wv] = hi;
+  __syncthreads();
+  lo = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
+  hi = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+}
+
+template <bool ASYM>
 __global__ __launch_bounds__(256) void dyn_quantize_kernel(
-    const void *x, int x_dt, int64_t K, int8_t *qx, float *sx, int frag) {
-  __shared__ float wmax[4];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const void *x, int x_dt, int64_t K, int8_t *qx, float *sx, int frag, int32_t *azp) {
+  __shared__ float red[8];
+  const int tid = threadIdx.x;
   const int64_t m = blockIdx.x;
   const int64_t base = m * K;
-  float amax = 0.f;
-  for (int64_t k = tid; k < K; k += 256)
-    amax = fmaxf(amax, fabsf(load_elem(x, x_dt, base + k)));
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-    amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
-  if (lane == 0) wmax[wv] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  if (!(amax >= 1e-12f)) amax = 1e-12f;
-  const float s = __fdiv_rn(amax, 127.0f);
-  if (tid == 0) sx[m] = s;
+  float lo = 0.f, hi = 0.f;
   for (int64_t k = tid; k < K; k += 256) {
-    float r = rintf(__fdiv_rn(load_elem(x, x_dt, base + k), s));
-    r = fminf(fmaxf(r, -128.f), 127.f);
-    qx[frag ? qx_frag_offset(m, k, K) : base + k] = (int8_t)(int)r;
+    const float v = load_elem(x, x_dt, base + k);
+    if (ASYM) {
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    } else {
+      hi = fmaxf(hi, fabsf(v));
+    }
   }
+  block_minmax(lo, hi, red, tid);
+  float s, zp;
+  row_qparams<ASYM>(lo, hi, s, zp);
+  if (tid == 0) {
+    sx[m] = s;
+    if (ASYM) azp[m] = (int32_t)zp - 128;
+  }
+  for (int64_t k = tid; k < K; k += 256)
+    qx[frag ? qx_frag_offset(m, k, K) : base + k] =
+        (int8_t)quant_one<ASYM>(load_elem(x, x_dt, base + k), s, zp);
 }
 
 // The same per-row quantisation for bf16 rows with K % 8 == 0, 16-byte
@@ -61,40 +113,41 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(
 // registers between the amax and the quantise pass and writes 8 bytes of qx
 // at a time (row-major, or in fragment order when FRAG).  Bit-identical to
 // dyn_quantize_kernel.
-template <int VPT, bool FRAG>
+template <int VPT, bool FRAG, bool ASYM>
 __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *x, int64_t K,
-                                                                 int8_t *qx, float *sx) {
-  __shared__ float wmax[4];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+                                                                 int8_t *qx, float *sx,
+                                                                 int32_t *azp) {
+  __shared__ float red[8];
+  const int tid = threadIdx.x;
   const int64_t m = blockIdx.x;
   const u32x4_t *row = reinterpret_cast<const u32x4_t *>(x + m * K);
   const int nv = (int)(K / 8);
   u32x4_t v[VPT];
-  float amax = 0.f;
+  float lo = 0.f, hi = 0.f;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int j = tid + 256 * i;
     v[i] = j < nv ? row[j] : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[i][w] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[i][w] & 0xffff0000u)));
+      const float e0 = __uint_as_float(v[i][w] << 16);
+      const float e1 = __uint_as_float(v[i][w] & 0xffff0000u);
+      if (ASYM) {
+        lo = fminf(lo, fminf(e0, e1));
+        hi = fmaxf(hi, fmaxf(e0, e1));
+      } else {
+        hi = fmaxf(hi, fmaxf(fabsf(e0), fabsf(e1)));
+      }
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-    amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
-  if (lane == 0) wmax[wv] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  if (!(amax >= 1e-12f)) amax = 1e-12f;
-  const float s = __fdiv_rn(amax, 127.0f);
-  if (tid == 0) sx[m] = s;
-  auto q1 = [&](float f) {
-    float r = rintf(__fdiv_rn(f, s));
-    r = fminf(fmaxf(r, -128.f), 127.f);
-    return (uint32_t)(uint8_t)(int8_t)(int)r;
-  };
+  block_minmax(lo, hi, red, tid);
+  float s, zp;
+  row_qparams<ASYM>(lo, hi, s, zp);
+  if (tid == 0) {
+    sx[m] = s;
+    if (ASYM) azp[m] = (int32_t)zp - 128;
+  }
+  auto q1 = [&](float f) { return (uint32_t)(uint8_t)(int8_t)quant_one<ASYM>(f, s, zp); };
   u32x2_t *out = reinterpret_cast<u32x2_t *>(qx + m * K);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
@@ -116,6 +169,7 @@ __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *
 
 __device__ __forceinline__ void dyn_epilogue(const DynArgs &a, int64_t m,
                                              int64_t n, int32_t acc) {
+  if (a.azp) acc -= a.azp[m] * a.colsum[n];
   if (a.y_dt == ZT_DT_S32) {
     reinterpret_cast<int32_t *>(a.y)[m * a.N + n] = acc;
     return;
@@ -238,9 +292,18 @@ constexpr size_t s8_tiled_lds() {
 
 // Epilogue of four consecutive columns n..n+3 of row m: one 8/16-byte store
 // when the row has them all, element by element otherwise.
+// The asymmetric-activation correction of four accumulators of row m from
+// column n (the row's four columns are n..n+3 < N).
+__device__ __forceinline__ i32x4_t asym_fix4(const DynArgs &a, int m, int n, i32x4_t v) {
+  const int32_t z = a.azp[m];
+  const i32x4_t c = *reinterpret_cast<const i32x4_t *>(a.colsum + n);
+  return v - c * z;
+}
+
 __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i32x4_t v) {
   const int N = (int)a.N;
   if (n + 3 < N && (N & 3) == 0) {
+    if (a.azp) v = asym_fix4(a, m, n, v);
     if (a.y_dt == ZT_DT_S32) {
       *reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(a.y) + (int64_t)m * N + n) = v;
       return;
@@ -296,7 +359,8 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
     }
     for (int row = tid / G4; row < BM && m0 + row < M; row += NT / G4) {
       const int m = m0 + row;
-      const i32x4_t v = *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4);
+      i32x4_t v = *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4);
+      if (a.azp) v = asym_fix4(a, m, n, v);
       const float sxm = sx_l[row];
       float f[4];
 #pragma unroll
@@ -993,6 +1057,7 @@ __device__ __forceinline__ void skinny_epilogue(const DynArgs &a, const int32_t 
       dyn_epilogue4(a, m, n, v);
       continue;
     }
+    if (a.azp) v = asym_fix4(a, m, n, v);
     const float sxm = a.sx[m];
     float f[4];
 #pragma unroll
@@ -1289,27 +1354,67 @@ hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
-                               int8_t *qx, float *sx, bool frag, hipStream_t s) {
+                               int8_t *qx, float *sx, bool frag, hipStream_t s,
+                               int32_t *azp) {
   if (M == 0) return hipSuccess;
   if (frag && K % 64 != 0) return hipErrorInvalidValue;
   const bool vec = x_dt == ZT_DT_BF16 && K % 8 == 0 &&
                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(qx)) & 15u) == 0;
   const int64_t per = (K / 8 + 255) / 256;  // 8-element vectors per thread
+  const dim3 grid((unsigned)M), block(256);
   if (vec && per <= 8) {
     const uint16_t *xb = static_cast<const uint16_t *>(x);
-#define ZT_QB(V_)                                                                      \
-  if (per <= V_) {                                                                     \
-    if (frag)                                                                          \
-      dyn_quantize_bf16_kernel<V_, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx); \
-    else                                                                               \
-      dyn_quantize_bf16_kernel<V_, false><<<dim3((unsigned)M), dim3(256), 0, s>>>(xb, K, qx, sx); \
-    return hipGetLastError();                                                          \
+#define ZT_QB(V_)                                                                          \
+  if (per <= V_) {                                                                         \
+    if (azp)                                                                               \
+      frag ? dyn_quantize_bf16_kernel<V_, true, true><<<grid, block, 0, s>>>(xb, K, qx, sx, azp) \
+           : dyn_quantize_bf16_kernel<V_, false, true><<<grid, block, 0, s>>>(xb, K, qx, sx, azp); \
+    else                                                                                   \
+      frag ? dyn_quantize_bf16_kernel<V_, true, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp) \
+           : dyn_quantize_bf16_kernel<V_, false, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp); \
+    return hipGetLastError();                                                              \
   }
     ZT_QB(2) ZT_QB(4) ZT_QB(8)
 #undef ZT_QB
   }
-  hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)M), dim3(256), 0, s, x,
-                     x_dt, K, qx, sx, (int)frag);
+  if (azp)
+    dyn_quantize_kernel<true><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp);
+  else
+    dyn_quantize_kernel<false><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp);
+  return hipGetLastError();
+}
+
+// colsum[n] = sum_k w[n][k]: one wave per weight row, 16 bytes per lane per
+// step where the row is 16-byte aligned.
+__global__ __launch_bounds__(256) void s8_colsum_kernel(const int8_t *w, int64_t N, int64_t K,
+                                                       int32_t *colsum) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int8_t *row = w + n * K;
+  int32_t acc = 0;
+  int64_t k0 = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+    const int64_t nv = K / 16;
+    for (int64_t j = lane; j < nv; j += kWave) {
+      const i32x4_t v = *reinterpret_cast<const i32x4_t *>(row + 16 * j);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc += (int32_t)(int8_t)(v[r] >> (8 * b));
+    }
+    k0 = nv * 16;
+  }
+  for (int64_t k = k0 + lane; k < K; k += kWave) acc += row[k];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+  if (lane == 0) colsum[n] = acc;
+}
+
+hipError_t launch_s8_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,
+                            hipStream_t s) {
+  if (N == 0) return hipSuccess;
+  s8_colsum_kernel<<<dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s>>>(w, N, K, colsum);
   return hipGetLastError();
 }
 

@@ -377,7 +377,8 @@ at::Tensor dynamic_qlinear_impl(const at::Tensor &input, const at::Tensor &weigh
                                 const c10::optional<at::Tensor> &bias,
                                 const std::vector<int32_t> &post_ids,
                                 const std::vector<at::Tensor> &binary_inputs,
-                                const std::string &name) {
+                                const std::string &name,
+                                const at::Tensor &colsum = at::Tensor()) {
   // dtype / size checks with the messages of DynamicQLinear.cpp:15-70.
   TORCH_CHECK(input.scalar_type() == at::kBFloat16 ||
                   input.scalar_type() == at::kFloat,
@@ -418,6 +419,15 @@ at::Tensor dynamic_qlinear_impl(const at::Tensor &input, const at::Tensor &weigh
   check_device(weight, input, op, "weight");
   check_device(weight_scales, input, op, "weight_scales");
   if (b.defined()) check_device(b, input, op, "bias");
+  at::Tensor cs;
+  if (colsum.defined()) {
+    TORCH_CHECK(colsum.scalar_type() == at::kInt && colsum.numel() == N, name,
+                ": weight_colsum must be int32 with one entry per output channel (", N,
+                "), got ", colsum.scalar_type(), " ", colsum.sizes());
+    check_device(colsum, input, op, "weight_colsum");
+    cs = colsum.contiguous();
+    if (reinterpret_cast<uintptr_t>(cs.data_ptr()) & 15u) cs = cs.clone();
+  }
 
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
   const OpRange range(name);
@@ -454,15 +464,25 @@ at::Tensor dynamic_qlinear_impl(const at::Tensor &input, const at::Tensor &weigh
       ++nb;
     }
   }
-  const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K);
-  const at::Tensor ws = call_workspace(input, ws_bytes);
-  const int rc = zt_dynamic_qlinear(
-      x2.data_ptr(), zt_dtype_of(x2), M, K,
-      reinterpret_cast<const int8_t *>(wc.data_ptr()), N, sc.data_ptr(),
-      zt_dtype_of(sc), bc.defined() ? bc.data_ptr() : nullptr,
-      bc.defined() ? zt_dtype_of(bc) : ZT_DT_NONE, post.count ? &post : nullptr,
-      result.data_ptr(), zt_dtype_of(result), ws.data_ptr(), ws_bytes,
-      reinterpret_cast<zt_stream_t>(current_stream()));
+  const int8_t *wp = reinterpret_cast<const int8_t *>(wc.data_ptr());
+  const void *bp = bc.defined() ? bc.data_ptr() : nullptr;
+  const int32_t bdt = bc.defined() ? zt_dtype_of(bc) : ZT_DT_NONE;
+  const zt_stream_t st = reinterpret_cast<zt_stream_t>(current_stream());
+  int rc;
+  if (cs.defined()) {
+    const size_t ws_bytes = zt_dynamic_qlinear_asym_workspace_size(M, K);
+    const at::Tensor ws = call_workspace(input, ws_bytes);
+    rc = zt_dynamic_qlinear_asym(x2.data_ptr(), zt_dtype_of(x2), M, K, wp, N, sc.data_ptr(),
+                                 zt_dtype_of(sc), cs.data_ptr<int32_t>(), bp, bdt,
+                                 post.count ? &post : nullptr, result.data_ptr(),
+                                 zt_dtype_of(result), ws.data_ptr(), ws_bytes, st);
+  } else {
+    const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K);
+    const at::Tensor ws = call_workspace(input, ws_bytes);
+    rc = zt_dynamic_qlinear(x2.data_ptr(), zt_dtype_of(x2), M, K, wp, N, sc.data_ptr(),
+                            zt_dtype_of(sc), bp, bdt, post.count ? &post : nullptr,
+                            result.data_ptr(), zt_dtype_of(result), ws.data_ptr(), ws_bytes, st);
+  }
   TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
   return result;
 }
@@ -495,6 +515,34 @@ at::Tensor dynamic_qlinear_add(const at::Tensor &input, const at::Tensor &weight
                                c10::string_view zentorch_op_name) {
   return dynamic_qlinear_impl(input, weight, weight_scales, bias, {ZT_PO_ADD}, {add_input},
                               std::string(zentorch_op_name));
+}
+
+// Extension: per-token asymmetric uint8 activations (the reference's dynamic
+// qlinear is symmetric s8, DynamicQLinear.cpp:94-110).  weight_colsum is
+// zentorch_s8_weight_colsum(weight), computed once per weight.
+at::Tensor dynamic_qlinear_asym(const at::Tensor &input, const at::Tensor &weight,
+                                const at::Tensor &weight_scales, const at::Tensor &weight_colsum,
+                                const c10::optional<at::Tensor> &bias,
+                                c10::string_view zentorch_op_name) {
+  return dynamic_qlinear_impl(input, weight, weight_scales, bias, {}, {},
+                              std::string(zentorch_op_name), weight_colsum);
+}
+
+// sum_k weight[n][k] in int32 for an int8 [N, K] weight.
+at::Tensor s8_weight_colsum(const at::Tensor &weight) {
+  TORCH_CHECK(weight.scalar_type() == at::kChar && weight.dim() == 2,
+              "zentorch_s8_weight_colsum: weight must be int8 [N, K], got ",
+              weight.scalar_type(), " ", weight.sizes());
+  check_device(weight, weight, "zentorch_s8_weight_colsum", "weight");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(weight.device());
+  const at::Tensor wc = weight.contiguous();
+  at::Tensor out = at::empty({weight.size(0)}, weight.options().dtype(at::kInt));
+  if (out.numel() == 0) return out;
+  const int rc = zt_s8_weight_colsum(reinterpret_cast<const int8_t *>(wc.data_ptr()),
+                                     wc.size(0), wc.size(1), out.data_ptr<int32_t>(),
+                                     reinterpret_cast<zt_stream_t>(current_stream()));
+  TORCH_CHECK(rc == ZT_OK, "zentorch_s8_weight_colsum: ", zt_last_error_string());
+  return out;
 }
 
 // zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema :728-736)
@@ -651,6 +699,12 @@ TORCH_LIBRARY(zentorch, m) {
         "Tensor weight_scales, Tensor add_input, Tensor? bias=None, *, "
         "str zentorch_op_name='zentorch::zentorch_dynamic_qlinear_add') -> Tensor",
         {at::Tag::needs_fixed_stride_order});
+  // Extension: per-token asymmetric uint8 activations (opt-in).
+  m.def("zentorch_dynamic_qlinear_asym(Tensor input, Tensor weight, "
+        "Tensor weight_scales, Tensor weight_colsum, Tensor? bias=None, *, "
+        "str zentorch_op_name='zentorch::zentorch_dynamic_qlinear_asym') -> Tensor",
+        {at::Tag::needs_fixed_stride_order});
+  m.def("zentorch_s8_weight_colsum(Tensor weight) -> Tensor");
   m.def("zentorch_fused_moe(Tensor(a!) output, Tensor input, "
         "Tensor w13, Tensor w2, "
         "Tensor? w13_bias, Tensor? w2_bias, "
@@ -678,5 +732,7 @@ TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
   m.impl("zentorch_dynamic_qlinear", dynamic_qlinear);
   m.impl("zentorch_dynamic_qlinear_silu_mul", dynamic_qlinear_silu_mul);
   m.impl("zentorch_dynamic_qlinear_add", dynamic_qlinear_add);
+  m.impl("zentorch_dynamic_qlinear_asym", dynamic_qlinear_asym);
+  m.impl("zentorch_s8_weight_colsum", s8_weight_colsum);
   m.impl("zentorch_fused_moe", fused_moe);
 }

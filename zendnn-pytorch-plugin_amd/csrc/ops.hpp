@@ -80,5 +80,10 @@ at::Tensor dynamic_qlinear_add(const at::Tensor &input, const at::Tensor &weight
                                const at::Tensor &weight_scales, const at::Tensor &add_input,
                                const c10::optional<at::Tensor> &bias,
                                c10::string_view zentorch_op_name);
+at::Tensor dynamic_qlinear_asym(const at::Tensor &input, const at::Tensor &weight,
+                                const at::Tensor &weight_scales, const at::Tensor &weight_colsum,
+                                const c10::optional<at::Tensor> &bias,
+                                c10::string_view zentorch_op_name);
+at::Tensor s8_weight_colsum(const at::Tensor &weight);
 
 }  // namespace zentorch_hip

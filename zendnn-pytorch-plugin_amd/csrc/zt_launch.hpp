@@ -94,12 +94,22 @@ struct DynArgs {
   const int8_t *qx;  // [M, K] quantised activations (row-major unless qx_frag)
   const float *sx;   // [M]
   int qx_frag;       // qx in the 32-token fragment order of s8_skinny32_kernel
+  // asymmetric activations: qx holds q_u8 - 128 and the accumulator of
+  // (m, n) is corrected by - azp[m] * colsum[n] (azp[m] = zp_u8[m] - 128,
+  // colsum[n] = sum_k w[n][k]); both null for symmetric s8
+  const int32_t *azp;     // [M]
+  const int32_t *colsum;  // [N]
 };
 
 // frag: write qx in the fragment order (K % 64 == 0; the buffer holds
 // ceil(M / 32) * 32 rows)
+// azp non-null: per-token asymmetric uint8 (qx = q_u8 - 128, azp = zp - 128)
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
-                               int8_t *qx, float *sx, bool frag, hipStream_t s);
+                               int8_t *qx, float *sx, bool frag, hipStream_t s,
+                               int32_t *azp = nullptr);
+// colsum[n] = sum_k w[n][k] of an int8 [N, K] weight
+hipError_t launch_s8_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,
+                            hipStream_t s);
 // whether launch_s8_gemm takes qx in fragment order for this call (a.qx set)
 bool s8_frag_ok(const DynArgs &a);
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);

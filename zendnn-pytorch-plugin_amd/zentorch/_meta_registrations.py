@@ -92,6 +92,17 @@ def meta_zentorch_dynamic_qlinear_add(input, weight, weight_scales, add_input, b
     return meta_zentorch_dynamic_qlinear(input, weight, weight_scales, bias)
 
 
+@register_meta("zentorch_dynamic_qlinear_asym")
+def meta_zentorch_dynamic_qlinear_asym(input, weight, weight_scales, weight_colsum, bias=None,
+                                       zentorch_op_name=""):
+    return meta_zentorch_dynamic_qlinear(input, weight, weight_scales, bias)
+
+
+@register_meta("zentorch_s8_weight_colsum")
+def meta_zentorch_s8_weight_colsum(weight):
+    return weight.new_empty((weight.size(0),), dtype=torch.int32)
+
+
 @register_meta("zentorch_woq_repack_weight")
 def meta_zentorch_woq_repack_weight(unpacked_weight):
     # [N, K/8] int32 (the reference's meta returns the input dtype, int8, which
