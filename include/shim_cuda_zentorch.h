@@ -101,6 +101,58 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear_add(
     AtenTensorHandle add_input, AtenTensorHandle *B, const char *zentorch_op_name,
     AtenTensorHandle *ret0);
 
+/* Static int8 qlinear: shim_cpu_zentorch.hpp:28-74.  X_zero_points and
+ * W_zero_points may be uninitialized handles (None); output_dtype is a
+ * c10::ScalarType code or NULL (None). */
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_qlinear(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,
+    AtenTensorHandle X_zero_points, AtenTensorHandle W_scales,
+    AtenTensorHandle W_zero_points, AtenTensorHandle *B,
+    AtenTensorHandle *output_scales, AtenTensorHandle *output_zero_points,
+    const int32_t *output_dtype, const char *zentorch_op_name,
+    AtenTensorHandle *ret0);
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_qlinear_relu(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,
+    AtenTensorHandle X_zero_points, AtenTensorHandle W_scales,
+    AtenTensorHandle W_zero_points, AtenTensorHandle *B,
+    AtenTensorHandle *output_scales, AtenTensorHandle *output_zero_points,
+    const int32_t *output_dtype, const char *zentorch_op_name,
+    AtenTensorHandle *ret0);
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_qlinear_sigmoid(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,
+    AtenTensorHandle X_zero_points, AtenTensorHandle W_scales,
+    AtenTensorHandle W_zero_points, AtenTensorHandle *B,
+    AtenTensorHandle *output_scales, AtenTensorHandle *output_zero_points,
+    const int32_t *output_dtype, const char *zentorch_op_name,
+    AtenTensorHandle *ret0);
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_qlinear_mul_add(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,
+    AtenTensorHandle X_zero_points, AtenTensorHandle W_scales,
+    AtenTensorHandle W_zero_points, AtenTensorHandle mul_input,
+    AtenTensorHandle add_input, AtenTensorHandle *B,
+    AtenTensorHandle *output_scales, AtenTensorHandle *output_zero_points,
+    const int32_t *output_dtype, const char *zentorch_op_name,
+    AtenTensorHandle *ret0);
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_qlinear_out(
+    AtenTensorHandle out, AtenTensorHandle X, AtenTensorHandle W,
+    AtenTensorHandle X_scales, AtenTensorHandle X_zero_points,
+    AtenTensorHandle W_scales, AtenTensorHandle W_zero_points,
+    AtenTensorHandle *B, AtenTensorHandle *output_scales,
+    AtenTensorHandle *output_zero_points, const int32_t *output_dtype,
+    const char *zentorch_op_name);
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_zentorch_qlinear_relu_out(
+    AtenTensorHandle out, AtenTensorHandle X, AtenTensorHandle W,
+    AtenTensorHandle X_scales, AtenTensorHandle X_zero_points,
+    AtenTensorHandle W_scales, AtenTensorHandle W_zero_points,
+    AtenTensorHandle *B, AtenTensorHandle *output_scales,
+    AtenTensorHandle *output_zero_points, const int32_t *output_dtype,
+    const char *zentorch_op_name);
+
 #ifdef __cplusplus
 }
 #endif

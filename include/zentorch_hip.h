@@ -235,6 +235,43 @@ size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K);
 int zt_dynamic_quantize_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                              int8_t *qx, float *sx, int32_t *azp, zt_stream_t stream);
 
+/*
+ * Static int8 linear: per-tensor quantisation of x with a given scale (and
+ * zero point), int8 x int8 -> int32 GEMM, y = acc * x_scale * w_scale[n] +
+ * bias[n], post-ops, then a float output or one requantised to u8 / s8.
+ *
+ * Replaces zendnnl_quantized_matmul_impl (src/cpu/cpp/QLinear.cpp:66-347)
+ * behind zentorch_qlinear / _relu / _sigmoid / _mul_add and the .out forms
+ * (QLinear.cpp:367-521, schemas :525-573).
+ *
+ *  x             [M, K]: fp32 / bf16 (quantised here, QLinear.cpp:118-157),
+ *                or already quantised s8 / u8 (:113-116)
+ *  x_scale       device fp32 scalar; q = clamp(rint(x * (1 / x_scale)) + zp)
+ *  x_zero_point  device int32 scalar or NULL.  Given: u8 activations over
+ *                [0, 255] (QLinear.cpp:16-22).  NULL: symmetric s8 over
+ *                [-128, 127].  acc = sum_k (q - zp) * w.
+ *  w             [N, K] int8 row-major (the op's weight, used as weight.t())
+ *  w_scales      fp32, 1 (per tensor) or N (per channel) entries
+ *  w_colsum      [N] int32 sum_k w[n][k], 16-byte aligned; required when x is
+ *                u8 or x_zero_point is given, ignored otherwise
+ *  post          relu / sigmoid / mul + add (QLinear.cpp:367-521), or NULL
+ *  y             y_dtype fp32 / bf16 without y_scale; with y_scale (device
+ *                fp32 scalar) u8 when y_zero_point (device int32) is given
+ *                and s8 when not, y = clamp(rint(v * (1 / y_scale)) + zp)
+ *                (the reference scales by 1 / output_scales, QLinear.cpp:163-166).
+ *  workspace     zt_qlinear_workspace_size(M, K) bytes
+ * Weight zero points are not an argument: the reference's matmul path leaves
+ * them unused (QLinear.cpp:248-262), so weights are symmetric.
+ */
+int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float *x_scale,
+               const int32_t *x_zero_point, const int8_t *w, int64_t N, const float *w_scales,
+               int64_t n_w_scales, const int32_t *w_colsum, const void *bias,
+               int32_t bias_dtype, const zt_post_ops *post, void *y, int32_t y_dtype,
+               const float *y_scale, const int32_t *y_zero_point, void *workspace,
+               size_t workspace_bytes, zt_stream_t stream);
+
+size_t zt_qlinear_workspace_size(int64_t M, int64_t K);
+
 /* colsum[n] = sum_k w[n][k] of an int8 [N, K] row-major weight, exactly in
  * int32.  No reference counterpart (extension above). */
 int zt_s8_weight_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,

@@ -55,6 +55,10 @@ def lib():
         L.zto_dynamic_qlinear_asym.argtypes = [
             _vp, _int, _i64, _i64, _vp, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp,
             _int]
+        L.zto_qlinear.argtypes = [
+            _vp, _int, _i64, _i64, ctypes.c_float, _int, ctypes.c_int32, _vp, _i64, _vp, _i64,
+            _vp, _int, _int, _vp, _vp, _vp, _vp, _vp, _int, _int, ctypes.c_float, _int,
+            ctypes.c_int32, _int]
         L.zto_woq_moe.argtypes = [
             _vp, _i64, _i64, _vp, _vp, _int, _i64, _int, _int, _vp, _vp, _i64, _vp, _vp,
             _vp, _i64, _vp, _i64, _i64, _vp, _int]
@@ -211,6 +215,30 @@ def dynamic_qlinear_asym(x, w, w_scales, bias=None, out_dtype=None, nthreads=0):
         _ptr(x2), DT[x2.dtype], M, K, _ptr(wc), N, _ptr(sw), DT[sw.dtype],
         _ptr(b), DT[b.dtype] if b is not None else -1, _ptr(y), DT[y.dtype],
         None, None, None, nthreads)
+    return y.reshape(*x.shape[:-1], N)
+
+
+def qlinear(x, w, x_scale, x_zp, w_scales, bias=None, post_ops=(), post_bufs=(),
+            out_dtype=torch.float32, y_scale=None, y_zp=None, nthreads=0):
+    """zentorch_qlinear* semantics (QLinear.cpp:66-347; zt_oracle.c).  Scales
+    and zero points are one-element tensors (or None for the zero points and
+    the output scale); w is [N, K] int8."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    wc = w.contiguous()
+    N = wc.shape[0]
+    sw = w_scales.reshape(-1).float().contiguous()
+    b = bias.contiguous() if bias is not None else None
+    y = torch.empty(M, N, dtype=out_dtype)
+    n, ids, bp, bd, bl, keep = _post_arrays(post_ops, [pb.reshape(-1, N) for pb in post_bufs])
+    lib().zto_qlinear(
+        _ptr(x2), DT[x2.dtype], M, K, float(x_scale.reshape(-1)[0]), int(x_zp is not None),
+        int(x_zp.reshape(-1)[0]) if x_zp is not None else 0, _ptr(wc), N, _ptr(sw), sw.numel(),
+        _ptr(b), DT[b.dtype] if b is not None else -1, n, ids, bp, bd, bl, _ptr(y), DT[y.dtype],
+        int(y_scale is not None), float(y_scale.reshape(-1)[0]) if y_scale is not None else 1.0,
+        int(y_zp is not None), int(y_zp.reshape(-1)[0]) if y_zp is not None else 0, nthreads)
+    del keep
     return y.reshape(*x.shape[:-1], N)
 
 

@@ -36,6 +36,15 @@
  *                           reference (no golden data exists); pinned by the
  *                           round-trip, zero-point and range identities the
  *                           CPU tests check.
+ *   zto_qlinear             QLinear.cpp:66-347 (zentorch_qlinear*): per-tensor
+ *                           input quantisation q = clamp(rint(x * (1/s)) + zp)
+ *                           over u8 with a zero point (QLinear.cpp:16-22,
+ *                           :139-149) or s8 without; s8/u8 inputs as given;
+ *                           acc = sum_k (q - zp) * w exactly; y = acc * s_x *
+ *                           s_w[n] + b[n]; post-ops; output float, or
+ *                           clamp(rint(y * (1/s_out)) + zp_out) in u8 (zero
+ *                           point given) / s8 (:163-166, validators
+ *                           MatmulUtils.hpp:325-433).
  *   zto_woq_moe             FusedMoE.cpp:443-700 and the per-expert loop of
  *                           vllm/_int8_moe_patch.py:149-206 with int4 expert
  *                           weights: per (token, k) pair of expert e,
@@ -431,6 +440,63 @@ int zto_dynamic_qlinear_asym(const void *x, int x_dt, int64_t M, int64_t K,
   if (!q_out) free(q);
   if (!sx_out) free(sx);
   if (!zp_out) free(zp);
+  return ZTO_OK;
+}
+
+/* ------------------------------------------------------------ (f)4 */
+/* Static int8 linear.  x_dt f32/bf16/s8/u8; w_scales 1 or N fp32; y_dt
+ * f32/bf16 (has_y_scale = 0) or u8/s8 (requantised). */
+int zto_qlinear(const void *x, int x_dt, int64_t M, int64_t K, float x_scale, int has_x_zp,
+                int32_t x_zp, const int8_t *w, int64_t N, const float *w_scales,
+                int64_t n_w_scales, const void *bias, int b_dt, int n_post,
+                const int *post_ids, const void *const *post_bufs, const int *post_dts,
+                const int64_t *post_lds, void *y, int y_dt, int has_y_scale, float y_scale,
+                int has_y_zp, int32_t y_zp, int nthreads) {
+  int32_t *q = (int32_t *)malloc(sizeof(int32_t) * (size_t)(M * K > 0 ? M * K : 1));
+  if (!q) return ZTO_EINVAL;
+  const int32_t off = has_x_zp ? x_zp : 0;
+  const float inv = 1.0f / x_scale;
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * K; ++i) {
+    if (x_dt == ZT_DT_S8) {
+      q[i] = ((const int8_t *)x)[i];
+    } else if (x_dt == ZT_DT_U8) {
+      q[i] = ((const uint8_t *)x)[i];
+    } else {
+      float r = rintf(load_f(x, x_dt, i) * inv);
+      if (has_x_zp) {
+        r += (float)x_zp;
+        r = r < 0.f ? 0.f : (r > 255.f ? 255.f : r);
+      } else {
+        r = r < -128.f ? -128.f : (r > 127.f ? 127.f : r);
+      }
+      q[i] = (int32_t)r;
+    }
+  }
+  const float inv_y = has_y_scale ? 1.0f / y_scale : 0.f;
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      int64_t a = 0;
+      for (int64_t k = 0; k < K; ++k)
+        a += (int64_t)(q[m * K + k] - off) * (int64_t)w[n * K + k];
+      float v = (float)(int32_t)a * x_scale;
+      v = v * w_scales[n_w_scales == 1 ? 0 : n];
+      if (bias) v = v + load_f(bias, b_dt, n);
+      v = apply_post_ops(v, n_post, post_ids, post_bufs, post_dts, post_lds, m, n);
+      if (has_y_scale) {
+        float r = rintf(v * inv_y) + (has_y_zp ? (float)y_zp : 0.f);
+        if (y_dt == ZT_DT_U8)
+          ((uint8_t *)y)[m * N + n] = (uint8_t)(r < 0.f ? 0.f : (r > 255.f ? 255.f : r));
+        else
+          ((int8_t *)y)[m * N + n] = (int8_t)(r < -128.f ? -128.f : (r > 127.f ? 127.f : r));
+      } else {
+        store_f(y, y_dt, m * N + n, v);
+      }
+    }
+  }
+  free(q);
   return ZTO_OK;
 }
 

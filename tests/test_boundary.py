@@ -51,7 +51,8 @@ def test_c_abi_needs_no_torch():
 
 def test_aoti_shims_exported():
     names = declared("shim_cuda_zentorch.h")
-    assert len(names) == 13  # the reference's 9 WOQ/dynamic shims + 4 extensions
+    # the reference's 9 WOQ/dynamic + 6 static qlinear shims, and 4 extensions
+    assert len(names) == 19
     syms = exported(os.path.join(PKG, "_C.so"))
     assert not [n for n in names if n not in syms]
 

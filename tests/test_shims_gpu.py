@@ -164,6 +164,50 @@ def test_dynamic_qlinear_shims(name):
         h.release()
 
 
+SCALAR_TYPE = {torch.uint8: 0, torch.int8: 1, torch.float32: 6, torch.bfloat16: 15}
+
+
+@pytest.mark.parametrize("name,out_dtype", [("qlinear", torch.uint8),
+                                            ("qlinear_relu", torch.bfloat16),
+                                            ("qlinear_sigmoid", torch.float32),
+                                            ("qlinear_mul_add", torch.float32)])
+def test_qlinear_shims(name, out_dtype):
+    g = torch.Generator().manual_seed(31)
+    M, N, K = 6, 48, 128
+    x = torch.randn(M, K, generator=g).to(DEV)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8).to(DEV)
+    xs = torch.tensor([0.03], device=DEV)
+    xz = torch.tensor([120], dtype=torch.int32, device=DEV)
+    ws = (torch.rand(N, generator=g) * 0.01 + 0.001).to(DEV)
+    wz = torch.zeros(1, dtype=torch.int32, device=DEV)
+    b = torch.randn(N, generator=g).to(out_dtype if out_dtype.is_floating_point
+                                       else torch.float32).to(DEV)
+    ys = torch.tensor([0.05], device=DEV) if out_dtype == torch.uint8 else None
+    yz = torch.tensor([9], dtype=torch.int32, device=DEV) if out_dtype == torch.uint8 else None
+    mul, add = (torch.randn(M, N, generator=g).to(DEV) for _ in range(2))
+    dt = ctypes.c_int32(SCALAR_TYPE[out_dtype])
+    h = Handles()
+    try:
+        head = [h(x), h(w), h(xs), h(xz), h(ws), h(wz)]
+        if name == "qlinear_mul_add":
+            head += [h(mul), h(add)]
+        rc, y = call(name, *head, h.opt(b), h.opt(ys), h.opt(yz), ctypes.byref(dt))
+        assert rc == 0
+        fn = getattr(torch.ops.zentorch, f"zentorch_{name}")
+        extra = (mul, add) if name == "qlinear_mul_add" else ()
+        ref = fn(x, w, xs, xz, ws, wz, *extra, b, ys, yz, out_dtype)
+        assert y.dtype == out_dtype and torch.equal(y, ref)
+        if name in ("qlinear", "qlinear_relu"):
+            out = torch.empty_like(ref)
+            shim_out = shim(f"{name}_out")
+            rc = shim_out(h(out), *head, h.opt(b), h.opt(ys), h.opt(yz), ctypes.byref(dt),
+                          f"zentorch::zentorch_{name}.out".encode())
+            torch.cuda.synchronize()
+            assert rc == 0 and torch.equal(out, ref)
+    finally:
+        h.release()
+
+
 def test_shim_failure_is_an_error_code():
     # a CPU input makes the op raise; the shim turns that into
     # AOTI_TORCH_FAILURE and leaves the output handle unset
@@ -178,7 +222,7 @@ def test_shim_failure_is_an_error_code():
         h.release()
 
 
-def _all_ops(x, wp, s, b, a1, a2, xq, wq, sq, bq, oq):
+def _all_ops(x, wp, s, b, a1, a2, xq, wq, sq, bq, oq, zq):
     z = torch.ops.zentorch
     w = wp.t()
     return [
@@ -195,6 +239,12 @@ def _all_ops(x, wp, s, b, a1, a2, xq, wq, sq, bq, oq):
         z.zentorch_dynamic_qlinear(xq, wq, sq, bq),
         z.zentorch_dynamic_qlinear_silu_mul(xq, wq, sq, oq, bq),
         z.zentorch_dynamic_qlinear_add(xq, wq, sq, oq),
+        z.zentorch_qlinear(xq, wq, sq[:1], None, sq, None, bq, None, None, torch.bfloat16),
+        z.zentorch_qlinear_relu(xq, wq, sq[:1], zq, sq, None, None, None, None),
+        z.zentorch_qlinear_sigmoid(xq, wq, sq[:1], zq, sq[:1], None, None, sq[:1] * 4, zq,
+                                   torch.uint8),
+        z.zentorch_qlinear_mul_add(xq, wq, sq[:1], None, sq, None, oq, oq, None, None, None,
+                                   torch.bfloat16),
     ]
 
 
@@ -212,7 +262,8 @@ def test_inductor_lowerings_call_the_shims(cpp_wrapper):
     sq = (torch.rand(96, generator=g) * 0.009 + 0.001).to(DEV)
     bq = torch.randn(96, generator=g).bfloat16().to(DEV)
     oq = torch.randn(8, 96, generator=g).bfloat16().to(DEV)
-    args = (x, wp, s, b, a1, a2, xq, wq, sq, bq, oq)
+    zq = torch.tensor([100], dtype=torch.int32, device=DEV)
+    args = (x, wp, s, b, a1, a2, xq, wq, sq, bq, oq, zq)
     ref = _all_ops(*args)
     torch._dynamo.reset()
     fn = torch.compile(_all_ops, options={"cpp_wrapper": cpp_wrapper})

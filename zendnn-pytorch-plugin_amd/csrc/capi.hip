@@ -511,6 +511,68 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                                 workspace, workspace_bytes, stream);
 }
 
+size_t zt_qlinear_workspace_size(int64_t M, int64_t K) {
+  return zt_dynamic_qlinear_asym_workspace_size(M, K);
+}
+
+int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float *x_scale,
+               const int32_t *x_zero_point, const int8_t *w, int64_t N, const float *w_scales,
+               int64_t n_w_scales, const int32_t *w_colsum, const void *bias,
+               int32_t bias_dtype, const zt_post_ops *post, void *y, int32_t y_dtype,
+               const float *y_scale, const int32_t *y_zero_point, void *workspace,
+               size_t workspace_bytes, zt_stream_t stream) {
+  static const char *op = "zt_qlinear";
+  if (!(is_float_dt(x_dtype) || x_dtype == ZT_DT_S8 || x_dtype == ZT_DT_U8))
+    return fail(ZT_EINVAL, "%s: input must be float32, bfloat16, uint8 or int8", op);
+  if (y_scale) {
+    if (y_dtype != (y_zero_point ? ZT_DT_U8 : ZT_DT_S8))
+      return fail(ZT_EINVAL,
+                  "%s: a requantised output is uint8 with an output zero point, int8 without",
+                  op);
+  } else if (!is_float_dt(y_dtype)) {
+    return fail(ZT_EINVAL, "%s: output must be float32 or bfloat16 without output scales", op);
+  }
+  if (bias && !is_float_dt(bias_dtype))
+    return fail(ZT_EINVAL, "%s: bias must be float32 or bfloat16", op);
+  if (M < 0 || N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
+  if (n_w_scales != 1 && n_w_scales != N)
+    return fail(ZT_EINVAL, "%s: %lld weight scales for %lld output channels", op,
+                (long long)n_w_scales, (long long)N);
+  if (M == 0 || N == 0) return ZT_OK;
+  if (!x || !x_scale || !w || !w_scales || !y) return fail(ZT_EINVAL, "%s: null pointer", op);
+  // activations carry an offset (u8, or an s8 zero point): the epilogue
+  // subtracts offset * colsum[n]
+  const bool offset = x_dtype == ZT_DT_U8 || x_zero_point != nullptr;
+  if (offset && !w_colsum)
+    return fail(ZT_EINVAL, "%s: weight_colsum is required for uint8 / zero-point activations",
+                op);
+  if (offset && (reinterpret_cast<uintptr_t>(w_colsum) & 15u))
+    return fail(ZT_EINVAL, "%s: weight_colsum must be 16-byte aligned", op);
+  const size_t need = zt_qlinear_workspace_size(M, K);
+  if (!workspace || workspace_bytes < need)
+    return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need,
+                workspace ? workspace_bytes : (size_t)0);
+  zt::DynArgs a{};
+  a.x = x, a.x_dt = x_dtype, a.M = M, a.K = K, a.w = w, a.N = N;
+  a.sw = w_scales, a.sw_dt = ZT_DT_F32, a.sw_bcast = n_w_scales == 1 && N > 1;
+  a.bias = bias, a.b_dt = bias ? bias_dtype : ZT_DT_NONE;
+  a.y = y, a.y_dt = y_dtype, a.out_scale = y_scale, a.out_zp = y_zero_point;
+  int rc = convert_post_ops(post, &a.post, op);
+  if (rc) return rc;
+  char *ws = reinterpret_cast<char *>(workspace);
+  int8_t *qx = reinterpret_cast<int8_t *>(ws);
+  float *sx = reinterpret_cast<float *>(ws + dyn_qx_bytes(M, K));
+  int32_t *azp = offset ? reinterpret_cast<int32_t *>(ws + dyn_qx_bytes(M, K) + M * 4) : nullptr;
+  a.qx = qx, a.sx = sx, a.azp = azp, a.colsum = offset ? w_colsum : nullptr;
+  a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  rc = hip_status(zt::launch_static_quantize(x, x_dtype, M, K, qx, a.qx_frag != 0, x_scale,
+                                             x_zero_point, sx, azp, s),
+                  op);
+  if (rc) return rc;
+  return hip_status(zt::launch_s8_gemm(a, s), op);
+}
+
 size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K) {
   if (M <= 0 || K <= 0) return 0;
   return dyn_qx_bytes(M, K) + (size_t)M * (sizeof(float) + sizeof(int32_t));

@@ -167,6 +167,56 @@ __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *
   }
 }
 
+// Static per-tensor quantisation of zentorch_qlinear's activations, one
+// workgroup per row.  fp32 / bf16 x: q = clamp(rint(x * inv) + zp) with
+// inv = 1 / scale in fp32, over [0, 255] when a zero point is given (stored
+// q - 128, offset zp - 128) and over [-128, 127] when not (offset 0).  s8 x
+// is taken as is (offset zp, or 0); u8 x is stored x - 128 (offset zp - 128,
+// zp = 0 when absent).  sx[m] = scale; azp[m] = the offset, when azp is set.
+__global__ __launch_bounds__(256) void static_quantize_kernel(
+    const void *x, int x_dt, int64_t K, int8_t *qx, int frag, const float *scale,
+    const int32_t *zp, float *sx, int32_t *azp) {
+  const int tid = threadIdx.x;
+  const int64_t m = blockIdx.x, base = m * K;
+  const float s = *scale;
+  const int32_t z = zp ? *zp : 0;
+  const bool u8 = x_dt == ZT_DT_U8 || ((x_dt == ZT_DT_F32 || x_dt == ZT_DT_BF16) && zp);
+  if (tid == 0) {
+    sx[m] = s;
+    if (azp) azp[m] = u8 ? z - 128 : z;
+  }
+  const float inv = __fdiv_rn(1.0f, s);
+  for (int64_t k = tid; k < K; k += 256) {
+    int q;
+    if (x_dt == ZT_DT_S8) {
+      q = reinterpret_cast<const int8_t *>(x)[base + k];
+    } else if (x_dt == ZT_DT_U8) {
+      q = (int)reinterpret_cast<const uint8_t *>(x)[base + k] - 128;
+    } else {
+      const float r = rintf(load_elem(x, x_dt, base + k) * inv);
+      q = u8 ? (int)fminf(fmaxf(r + (float)z, 0.f), 255.f) - 128
+             : (int)fminf(fmaxf(r, -128.f), 127.f);
+    }
+    qx[frag ? qx_frag_offset(m, k, K) : base + k] = (int8_t)q;
+  }
+}
+
+// Requantised int8 output (zentorch_qlinear with output scales):
+// clamp(rint(v * inv) + zp) with inv = 1 / scale in fp32.
+__device__ __forceinline__ void store_q8(const DynArgs &a, int64_t i, float v) {
+  const float inv = __fdiv_rn(1.0f, *a.out_scale);
+  float r = rintf(v * inv) + (a.out_zp ? (float)*a.out_zp : 0.f);
+  if (a.y_dt == ZT_DT_U8)
+    reinterpret_cast<uint8_t *>(a.y)[i] = (uint8_t)(int)fminf(fmaxf(r, 0.f), 255.f);
+  else
+    reinterpret_cast<int8_t *>(a.y)[i] = (int8_t)(int)fminf(fmaxf(r, -128.f), 127.f);
+}
+
+// The weight scale of column n (one shared scale when sw_bcast).
+__device__ __forceinline__ float wscale(const DynArgs &a, int64_t n) {
+  return load_elem(a.sw, a.sw_dt, a.sw_bcast ? 0 : n);
+}
+
 __device__ __forceinline__ void dyn_epilogue(const DynArgs &a, int64_t m,
                                              int64_t n, int32_t acc) {
   if (a.azp) acc -= a.azp[m] * a.colsum[n];
@@ -175,10 +225,13 @@ __device__ __forceinline__ void dyn_epilogue(const DynArgs &a, int64_t m,
     return;
   }
   float v = (float)acc * a.sx[m];
-  v = v * load_elem(a.sw, a.sw_dt, n);
+  v = v * wscale(a, n);
   if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
   v = apply_post_ops(v, a.post, m, n);
-  store_elem(a.y, a.y_dt, m * a.N + n, v);
+  if (a.y_dt == ZT_DT_U8 || a.y_dt == ZT_DT_S8)
+    store_q8(a, m * a.N + n, v);
+  else
+    store_elem(a.y, a.y_dt, m * a.N + n, v);
 }
 
 __global__ __launch_bounds__(256) void s8_generic_kernel(DynArgs a) {
@@ -302,7 +355,8 @@ __device__ __forceinline__ i32x4_t asym_fix4(const DynArgs &a, int m, int n, i32
 
 __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i32x4_t v) {
   const int N = (int)a.N;
-  if (n + 3 < N && (N & 3) == 0) {
+  const bool vec_out = a.y_dt == ZT_DT_S32 || a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32;
+  if (n + 3 < N && (N & 3) == 0 && vec_out) {
     if (a.azp) v = asym_fix4(a, m, n, v);
     if (a.y_dt == ZT_DT_S32) {
       *reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(a.y) + (int64_t)m * N + n) = v;
@@ -313,7 +367,7 @@ __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i3
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float t = (float)v[r] * sxm;
-      t = t * load_elem(a.sw, a.sw_dt, n + r);
+      t = t * wscale(a, n + r);
       if (a.bias) t = t + load_elem(a.bias, a.b_dt, n + r);
       f[r] = apply_post_ops(t, a.post, m, n + r);
     }
@@ -349,12 +403,12 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
   static_assert(NT % G4 == 0, "four-column groups must divide the threads");
   const int M = (int)a.M, N = (int)a.N;
   const int c4 = (tid % G4) * 4, n = n0 + c4;
-  if (a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0) {
+  if ((a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32) && a.post.count == 0 && (N & 3) == 0) {
     if (n >= N) return;
     float sw[4], b[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sw[r] = load_elem(a.sw, a.sw_dt, n + r);
+      sw[r] = wscale(a, n + r);
       b[r] = a.bias ? load_elem(a.bias, a.b_dt, n + r) : 0.f;
     }
     for (int row = tid / G4; row < BM && m0 + row < M; row += NT / G4) {
@@ -1039,12 +1093,13 @@ __device__ __forceinline__ void skinny_epilogue(const DynArgs &a, const int32_t 
   }
   const int c4 = (tid % G4) * 4, n = n0 + c4;
   if (n >= N) return;
-  const bool fast = a.y_dt != ZT_DT_S32 && a.post.count == 0 && (N & 3) == 0;
+  const bool fast =
+      (a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32) && a.post.count == 0 && (N & 3) == 0;
   float sw[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
   if (fast) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sw[r] = load_elem(a.sw, a.sw_dt, n + r);
+      sw[r] = wscale(a, n + r);
       if (a.bias) b[r] = load_elem(a.bias, a.b_dt, n + r);
     }
   }
@@ -1381,6 +1436,16 @@ hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
     dyn_quantize_kernel<true><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp);
   else
     dyn_quantize_kernel<false><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp);
+  return hipGetLastError();
+}
+
+hipError_t launch_static_quantize(const void *x, int x_dt, int64_t M, int64_t K, int8_t *qx,
+                                  bool frag, const float *scale, const int32_t *zp, float *sx,
+                                  int32_t *azp, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  if (frag && K % 64 != 0) return hipErrorInvalidValue;
+  static_quantize_kernel<<<dim3((unsigned)M), dim3(256), 0, s>>>(x, x_dt, K, qx, (int)frag, scale,
+                                                                 zp, sx, azp);
   return hipGetLastError();
 }
 

@@ -545,6 +545,270 @@ at::Tensor s8_weight_colsum(const at::Tensor &weight) {
   return out;
 }
 
+// ----------------------------------------------------------- static qlinear
+// zentorch_qlinear / _relu / _sigmoid / _mul_add and the .out forms
+// (src/cpu/cpp/QLinear.cpp:367-573), with the argument checks and messages of
+// check_valid_dtypes_for_quantized_matmul / _sizes_ (MatmulUtils.hpp:325-518).
+namespace {
+
+void qlinear_checks(const at::Tensor &input, const at::Tensor &weight, const at::Tensor &result,
+                    const at::Tensor &bias, const at::Tensor &input_scales,
+                    const at::Tensor &input_zero_points, const at::Tensor &weight_scales,
+                    const at::Tensor &weight_zero_points, const at::Tensor &output_scales,
+                    const at::Tensor &output_zero_points,
+                    const std::vector<at::Tensor> &post_bufs) {
+  const auto it = input.scalar_type();
+  TORCH_CHECK(it == at::kFloat || it == at::kBFloat16 || it == at::kByte || it == at::kChar,
+              "unsupported dtype for input tensor, only float32/bfloat16/uint8/int8 is supported");
+  TORCH_CHECK(weight.scalar_type() == at::kChar,
+              "unsupported dtype for weight tensor, only int8 is supported");
+  const auto rt = result.scalar_type();
+  TORCH_CHECK(rt == at::kFloat || rt == at::kBFloat16 || rt == at::kByte || rt == at::kChar,
+              "unsupported dtype for result tensor, only float32/bfloat16/uint8/int8 is supported");
+  if (bias.defined())
+    TORCH_CHECK(bias.scalar_type() == at::kFloat || bias.scalar_type() == at::kBFloat16,
+                "unsupported dtype for bias tensor, only float32 or bfloat16 is supported");
+  TORCH_CHECK(input_scales.scalar_type() == at::kFloat,
+              "unsupported dtype for input_scales, only float32 is supported");
+  if (input_zero_points.defined())
+    TORCH_CHECK(input_zero_points.scalar_type() == at::kInt,
+                "unsupported dtype for input_zero_points, only int32 supported");
+  TORCH_CHECK(weight_scales.scalar_type() == at::kFloat,
+              "unsupported dtype for weight_scales, only float32 is supported");
+  if (weight_zero_points.defined())
+    TORCH_CHECK(weight_zero_points.scalar_type() == at::kInt,
+                "unsupported dtype for weight_zero_points, only int32 is supported");
+  if (output_scales.defined()) {
+    TORCH_CHECK(output_scales.scalar_type() == at::kFloat,
+                "unsupported dtype for output_scales, only float32 is supported");
+    if (output_zero_points.defined()) {
+      TORCH_CHECK(output_zero_points.scalar_type() == at::kInt,
+                  "unsupported dtype for output_zero_points, only int32 is supported");
+      TORCH_CHECK(rt == at::kByte,
+                  "unsupported dtype for result tensor when output_zero_points are defined, "
+                  "uint8 are supported dtype");
+    } else {
+      TORCH_CHECK(rt == at::kChar,
+                  "unsupported dtype for result tensor when output_zero_points are not "
+                  "defined while output_scales are defined, int8 are supported dtype");
+    }
+  } else {
+    TORCH_CHECK(rt == at::kFloat || rt == at::kBFloat16,
+                "unsupported dtype for result tensor, only float32/bfloat16 is supported "
+                "when output_scales are not defined");
+  }
+  for (const auto &b : post_bufs)
+    TORCH_CHECK(b.scalar_type() == at::kFloat || b.scalar_type() == at::kBFloat16,
+                "unsupported dtype for post_ops, only float32/bfloat16 is supported");
+  // sizes (check_valid_sizes_for_matmul + the quantised ones)
+  TORCH_CHECK(input.dim() >= 2 && weight.dim() == 2,
+              "unsupported dims for input and weight");
+  TORCH_CHECK(input.size(-1) == weight.size(1),
+              "unsupported sizes for input and weight: input last dim (", input.size(-1),
+              ") must match weight dim 1 (", weight.size(1), ")");
+  const int64_t N = weight.size(0);
+  if (bias.defined())
+    TORCH_CHECK(bias.dim() == 1 && bias.size(0) == N, "unsupported sizes for bias");
+  TORCH_CHECK(input_scales.dim() <= 1, "unsupported dims for input_scales with respect to input "
+                                       "tensor");
+  if (input_zero_points.defined()) {
+    TORCH_CHECK(input_zero_points.dim() <= 1,
+                "only scalar and 1-d input_zero_points are supported");
+    TORCH_CHECK(input_zero_points.numel() == 1,
+                "only supporting per-tensor quantization for input");
+  }
+  TORCH_CHECK(input_scales.numel() == 1,
+              "unsupported number of elements for input_scales with respect to input tensor");
+  TORCH_CHECK(weight_scales.dim() <= 1,
+              "unsupported dims for weight_scales with respect to weight tensor");
+  TORCH_CHECK(weight_scales.numel() == 1 || weight_scales.numel() == N,
+              "unsupported number of elements for weight_scales with respect to weight tensor");
+  if (weight_zero_points.defined()) {
+    TORCH_CHECK(weight_zero_points.dim() <= 1,
+                "only scalar and 1-d weight_zero_points are supported");
+    TORCH_CHECK(weight_zero_points.numel() == 1 || weight_zero_points.numel() == N,
+                "only supporting per-tensor and per-channel quantization for weight");
+  }
+  if (output_scales.defined() && output_zero_points.defined()) {
+    TORCH_CHECK(output_scales.dim() <= 1,
+                "unsupported dims for output_scales with respect to output tensor");
+    TORCH_CHECK(output_zero_points.dim() <= 1,
+                "unsupported dims for output_zero_points with respect to output tensor");
+    TORCH_CHECK(output_scales.numel() == 1,
+                "unsupported number of elements for output_scales with respect to output tensor");
+    TORCH_CHECK(output_zero_points.numel() == 1,
+                "unsupported number of elements for output_zero_points with respect to output "
+                "tensor");
+  }
+  const auto osz = out_sizes(input, N);
+  for (const auto &b : post_bufs) {
+    TORCH_CHECK(b.dim() == input.dim(), "unsupported dims for post op buffers for input and "
+                                        "weight");
+    TORCH_CHECK(b.sizes() == c10::IntArrayRef(osz),
+                "unsupported shapes for post op buffers for input and weight");
+  }
+  TORCH_CHECK(result.sizes() == c10::IntArrayRef(osz), "unsupported shape for the result tensor");
+}
+
+void qlinear_into(at::Tensor &result, const at::Tensor &input, const at::Tensor &weight,
+                  const at::Tensor &input_scales, const at::Tensor &input_zero_points,
+                  const at::Tensor &weight_scales, const at::Tensor &weight_zero_points,
+                  const c10::optional<at::Tensor> &bias_opt,
+                  const c10::optional<at::Tensor> &output_scales_opt,
+                  const c10::optional<at::Tensor> &output_zero_points_opt,
+                  const std::vector<int32_t> &post_ids,
+                  const std::vector<at::Tensor> &post_bufs, const std::string &name) {
+  const at::Tensor bias = bias_opt.has_value() ? *bias_opt : at::Tensor();
+  const at::Tensor os = output_scales_opt.has_value() ? *output_scales_opt : at::Tensor();
+  const at::Tensor oz = output_zero_points_opt.has_value() ? *output_zero_points_opt : at::Tensor();
+  qlinear_checks(input, weight, result, bias, input_scales, input_zero_points, weight_scales,
+                 weight_zero_points, os, oz, post_bufs);
+  const char *op = "zentorch_qlinear";
+  for (const at::Tensor *t : std::initializer_list<const at::Tensor *>{
+           &weight, &input_scales, &weight_scales, &result})
+    check_device(*t, input, op, "argument");
+  for (const at::Tensor *t :
+       std::initializer_list<const at::Tensor *>{&input_zero_points, &bias, &os, &oz})
+    if (t->defined()) check_device(*t, input, op, "argument");
+  for (const auto &b : post_bufs) check_device(b, input, op, "post-op buffer");
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
+  const OpRange range(name);
+  if (result.numel() == 0) return;
+  const at::Tensor x2 = as_2d(input);
+  const int64_t M = x2.size(0), K = x2.size(1), N = weight.size(0);
+  const at::Tensor wc = weight.contiguous();
+  const at::Tensor sx = input_scales.contiguous(), sw = weight_scales.contiguous();
+  const at::Tensor zx = input_zero_points.defined() ? input_zero_points.contiguous() : at::Tensor();
+  const at::Tensor bc = bias.defined() ? bias.contiguous() : at::Tensor();
+  const at::Tensor osc = os.defined() ? os.contiguous() : at::Tensor();
+  const at::Tensor ozc = oz.defined() ? oz.contiguous() : at::Tensor();
+  const hipStream_t st = current_stream();
+  const zt_stream_t zst = reinterpret_cast<zt_stream_t>(st);
+  // activations with an offset (u8, or a zero point) need sum_k w[n][k]
+  at::Tensor colsum;
+  if (x2.scalar_type() == at::kByte || zx.defined()) {
+    colsum = at::empty({N}, weight.options().dtype(at::kInt));
+    const int rc = zt_s8_weight_colsum(reinterpret_cast<const int8_t *>(wc.data_ptr()), N, K,
+                                       colsum.data_ptr<int32_t>(), zst);
+    TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
+  }
+  zt_post_ops post{};
+  post.count = (int32_t)post_ids.size();
+  std::vector<at::Tensor> keep;
+  for (size_t i = 0, nb = 0; i < post_ids.size(); ++i) {
+    post.ids[i] = post_ids[i];
+    if (post_ids[i] == ZT_PO_ADD || post_ids[i] == ZT_PO_MUL) {
+      int64_t ld = N;
+      at::Tensor bt = rows_view(post_bufs[nb], &ld);
+      keep.push_back(bt);
+      post.bufs[nb] = bt.data_ptr();
+      post.buf_dtypes[nb] = zt_dtype_of(bt);
+      post.buf_ld[nb] = ld;
+      ++nb;
+    }
+  }
+  // the result may be a strided .out tensor: compute into a contiguous one
+  at::Tensor y = result.is_contiguous() ? result : at::empty_like(result, at::MemoryFormat::Contiguous);
+  const size_t ws_bytes = zt_qlinear_workspace_size(M, K);
+  const at::Tensor ws = call_workspace(input, ws_bytes);
+  const int rc = zt_qlinear(
+      x2.data_ptr(), zt_dtype_of(x2), M, K, sx.data_ptr<float>(),
+      zx.defined() ? zx.data_ptr<int32_t>() : nullptr,
+      reinterpret_cast<const int8_t *>(wc.data_ptr()), N, sw.data_ptr<float>(), sw.numel(),
+      colsum.defined() ? colsum.data_ptr<int32_t>() : nullptr,
+      bc.defined() ? bc.data_ptr() : nullptr, bc.defined() ? zt_dtype_of(bc) : ZT_DT_NONE,
+      post.count ? &post : nullptr, y.data_ptr(), zt_dtype_of(y),
+      osc.defined() ? osc.data_ptr<float>() : nullptr,
+      ozc.defined() ? ozc.data_ptr<int32_t>() : nullptr, ws.data_ptr(), ws_bytes, zst);
+  TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
+  if (!y.is_same(result)) result.copy_(y);
+}
+
+at::Tensor qlinear_alloc(const at::Tensor &input, const at::Tensor &weight,
+                         c10::optional<c10::ScalarType> output_dtype) {
+  TORCH_CHECK(weight.dim() == 2, "unsupported dims for input and weight");
+  const auto dt = output_dtype.has_value() ? *output_dtype : at::kFloat;
+  TORCH_CHECK(dt == at::kFloat || dt == at::kBFloat16 || dt == at::kByte || dt == at::kChar,
+              "output_dtype received is not yet supported, only float32/bfloat16/uint8/int8 is "
+              "supported");
+  return at::empty(out_sizes(input, weight.size(0)), input.options().dtype(dt));
+}
+
+}  // namespace
+
+template <int32_t PO>
+at::Tensor qlinear_unary(const at::Tensor &input, const at::Tensor &weight,
+                         const at::Tensor &input_scales, const at::Tensor &input_zero_points,
+                         const at::Tensor &weight_scales, const at::Tensor &weight_zero_points,
+                         const c10::optional<at::Tensor> &bias,
+                         const c10::optional<at::Tensor> &output_scales,
+                         const c10::optional<at::Tensor> &output_zero_points,
+                         c10::optional<c10::ScalarType> output_dtype,
+                         c10::string_view zentorch_op_name) {
+  at::Tensor result = qlinear_alloc(input, weight, output_dtype);
+  std::vector<int32_t> ids;
+  if (PO != ZT_PO_NONE) ids.push_back(PO);
+  qlinear_into(result, input, weight, input_scales, input_zero_points, weight_scales,
+               weight_zero_points, bias, output_scales, output_zero_points, ids, {},
+               std::string(zentorch_op_name));
+  return result;
+}
+
+template <int32_t PO>
+void qlinear_unary_out(at::Tensor &out, const at::Tensor &input, const at::Tensor &weight,
+                       const at::Tensor &input_scales, const at::Tensor &input_zero_points,
+                       const at::Tensor &weight_scales, const at::Tensor &weight_zero_points,
+                       const c10::optional<at::Tensor> &bias,
+                       const c10::optional<at::Tensor> &output_scales,
+                       const c10::optional<at::Tensor> &output_zero_points,
+                       c10::optional<c10::ScalarType> output_dtype,
+                       c10::string_view zentorch_op_name) {
+  TORCH_CHECK(output_dtype.has_value() && *output_dtype == out.scalar_type(),
+              "output_dtype received does not match the dtype of the output tensor");
+  TORCH_CHECK(out.scalar_type() == at::kFloat || out.scalar_type() == at::kBFloat16 ||
+                  out.scalar_type() == at::kByte || out.scalar_type() == at::kChar,
+              "output_dtype received is not yet supported, only float32/bfloat16/uint8/int8 is "
+              "supported");
+  std::vector<int32_t> ids;
+  if (PO != ZT_PO_NONE) ids.push_back(PO);
+  qlinear_into(out, input, weight, input_scales, input_zero_points, weight_scales,
+               weight_zero_points, bias, output_scales, output_zero_points, ids, {},
+               std::string(zentorch_op_name));
+}
+
+at::Tensor qlinear_mul_add(const at::Tensor &input, const at::Tensor &weight,
+                           const at::Tensor &input_scales, const at::Tensor &input_zero_points,
+                           const at::Tensor &weight_scales, const at::Tensor &weight_zero_points,
+                           const at::Tensor &mul_input, const at::Tensor &add_input,
+                           const c10::optional<at::Tensor> &bias,
+                           const c10::optional<at::Tensor> &output_scales,
+                           const c10::optional<at::Tensor> &output_zero_points,
+                           c10::optional<c10::ScalarType> output_dtype,
+                           c10::string_view zentorch_op_name) {
+  at::Tensor result = qlinear_alloc(input, weight, output_dtype);
+  qlinear_into(result, input, weight, input_scales, input_zero_points, weight_scales,
+               weight_zero_points, bias, output_scales, output_zero_points,
+               {ZT_PO_MUL, ZT_PO_ADD}, {mul_input, add_input}, std::string(zentorch_op_name));
+  return result;
+}
+
+#define ZT_QLIN_INST(PO_)                                                                       \
+  template at::Tensor qlinear_unary<PO_>(                                                       \
+      const at::Tensor &, const at::Tensor &, const at::Tensor &, const at::Tensor &,           \
+      const at::Tensor &, const at::Tensor &, const c10::optional<at::Tensor> &,                \
+      const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,                     \
+      c10::optional<c10::ScalarType>, c10::string_view);                                        \
+  template void qlinear_unary_out<PO_>(                                                         \
+      at::Tensor &, const at::Tensor &, const at::Tensor &, const at::Tensor &,                 \
+      const at::Tensor &, const at::Tensor &, const at::Tensor &,                               \
+      const c10::optional<at::Tensor> &, const c10::optional<at::Tensor> &,                     \
+      const c10::optional<at::Tensor> &, c10::optional<c10::ScalarType>, c10::string_view);
+ZT_QLIN_INST(ZT_PO_NONE)
+ZT_QLIN_INST(ZT_PO_RELU)
+ZT_QLIN_INST(ZT_PO_SIGMOID)
+#undef ZT_QLIN_INST
+
 // zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema :728-736)
 // for int4-packed expert weights: w13 int32 [E, 2I, H/8], w2 int32
 // [E, H, I/8] (each expert packed by zentorch_woq_repack_weight) with bf16
@@ -705,6 +969,43 @@ TORCH_LIBRARY(zentorch, m) {
         "str zentorch_op_name='zentorch::zentorch_dynamic_qlinear_asym') -> Tensor",
         {at::Tag::needs_fixed_stride_order});
   m.def("zentorch_s8_weight_colsum(Tensor weight) -> Tensor");
+  // Static int8 qlinear (QLinear.cpp:525-573).
+  m.def("zentorch_qlinear(Tensor input, Tensor weight, "
+        "Tensor input_scales, Tensor input_zero_points, "
+        "Tensor weight_scales, Tensor weight_zero_points, Tensor? bias, "
+        "Tensor? output_scales, Tensor? output_zero_points, "
+        "ScalarType? output_dtype=None, str zentorch_op_name="
+        "'zentorch::zentorch_qlinear') -> Tensor");
+  m.def("zentorch_qlinear_relu(Tensor input, Tensor weight, "
+        "Tensor input_scales, Tensor input_zero_points, "
+        "Tensor weight_scales, Tensor weight_zero_points, Tensor? bias, "
+        "Tensor? output_scales, Tensor? output_zero_points, "
+        "ScalarType? output_dtype=None, str zentorch_op_name="
+        "'zentorch::zentorch_qlinear_relu') -> Tensor");
+  m.def("zentorch_qlinear_sigmoid(Tensor input, Tensor weight, "
+        "Tensor input_scales, Tensor input_zero_points, "
+        "Tensor weight_scales, Tensor weight_zero_points, Tensor? bias, "
+        "Tensor? output_scales, Tensor? output_zero_points, "
+        "ScalarType? output_dtype=None, str zentorch_op_name="
+        "'zentorch::zentorch_qlinear_sigmoid') -> Tensor");
+  m.def("zentorch_qlinear_mul_add(Tensor input, Tensor weight, "
+        "Tensor input_scales, Tensor input_zero_points, "
+        "Tensor weight_scales, Tensor weight_zero_points, Tensor mul_input, "
+        "Tensor add_input, Tensor? bias, Tensor? output_scales, "
+        "Tensor? output_zero_points, ScalarType? output_dtype=None, str "
+        "zentorch_op_name='zentorch::zentorch_qlinear_mul_add') -> Tensor");
+  m.def("zentorch_qlinear.out(Tensor(a!) out, Tensor input, Tensor weight, "
+        "Tensor input_scales, Tensor input_zero_points, "
+        "Tensor weight_scales, Tensor weight_zero_points, Tensor? bias, "
+        "Tensor? output_scales, Tensor? output_zero_points, "
+        "ScalarType? output_dtype=None, "
+        "str zentorch_op_name='zentorch::zentorch_qlinear.out') -> ()");
+  m.def("zentorch_qlinear_relu.out(Tensor(a!) out, Tensor input, Tensor weight, "
+        "Tensor input_scales, Tensor input_zero_points, "
+        "Tensor weight_scales, Tensor weight_zero_points, Tensor? bias, "
+        "Tensor? output_scales, Tensor? output_zero_points, "
+        "ScalarType? output_dtype=None, "
+        "str zentorch_op_name='zentorch::zentorch_qlinear_relu.out') -> ()");
   m.def("zentorch_fused_moe(Tensor(a!) output, Tensor input, "
         "Tensor w13, Tensor w2, "
         "Tensor? w13_bias, Tensor? w2_bias, "
@@ -734,5 +1035,11 @@ TORCH_LIBRARY_IMPL(zentorch, CUDA, m) {
   m.impl("zentorch_dynamic_qlinear_add", dynamic_qlinear_add);
   m.impl("zentorch_dynamic_qlinear_asym", dynamic_qlinear_asym);
   m.impl("zentorch_s8_weight_colsum", s8_weight_colsum);
+  m.impl("zentorch_qlinear", qlinear_unary<ZT_PO_NONE>);
+  m.impl("zentorch_qlinear_relu", qlinear_unary<ZT_PO_RELU>);
+  m.impl("zentorch_qlinear_sigmoid", qlinear_unary<ZT_PO_SIGMOID>);
+  m.impl("zentorch_qlinear_mul_add", qlinear_mul_add);
+  m.impl("zentorch_qlinear.out", qlinear_unary_out<ZT_PO_NONE>);
+  m.impl("zentorch_qlinear_relu.out", qlinear_unary_out<ZT_PO_RELU>);
   m.impl("zentorch_fused_moe", fused_moe);
 }

@@ -129,4 +129,71 @@ AOTITorchError aoti_torch_cuda_zentorch_dynamic_qlinear_add(
   });
 }
 
+// static int8 qlinear (shim_cpu_zentorch.cpp:72-190 of the reference)
+#define ZT_DTYPE_OPT(p)                                                         \
+  ((p) ? c10::optional<c10::ScalarType>(static_cast<c10::ScalarType>(*(p)))      \
+       : c10::optional<c10::ScalarType>())
+
+#define ZT_QLINEAR_SHIM(NAME, PO)                                                           \
+  AOTITorchError aoti_torch_cuda_zentorch_##NAME(                                           \
+      AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,                    \
+      AtenTensorHandle X_zero_points, AtenTensorHandle W_scales,                            \
+      AtenTensorHandle W_zero_points, AtenTensorHandle *B, AtenTensorHandle *output_scales, \
+      AtenTensorHandle *output_zero_points, const int32_t *output_dtype,                    \
+      const char *zentorch_op_name, AtenTensorHandle *ret0) {                               \
+    AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({                                            \
+      auto r = zentorch_hip::qlinear_unary<PO>(                                             \
+          ZT_T(X), ZT_T(W), ZT_T(X_scales), ZT_T(X_zero_points), ZT_T(W_scales),            \
+          ZT_T(W_zero_points), ZT_OPT(B), ZT_OPT(output_scales), ZT_OPT(output_zero_points), \
+          ZT_DTYPE_OPT(output_dtype), zentorch_op_name);                                    \
+      *ret0 = new_tensor_handle(std::move(r));                                              \
+    });                                                                                     \
+  }                                                                                         \
+  AOTITorchError aoti_torch_cuda_zentorch_##NAME##_out(                                     \
+      AtenTensorHandle out, AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales, \
+      AtenTensorHandle X_zero_points, AtenTensorHandle W_scales,                            \
+      AtenTensorHandle W_zero_points, AtenTensorHandle *B, AtenTensorHandle *output_scales, \
+      AtenTensorHandle *output_zero_points, const int32_t *output_dtype,                    \
+      const char *zentorch_op_name) {                                                       \
+    AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({                                            \
+      zentorch_hip::qlinear_unary_out<PO>(                                                  \
+          ZT_T(out), ZT_T(X), ZT_T(W), ZT_T(X_scales), ZT_T(X_zero_points), ZT_T(W_scales), \
+          ZT_T(W_zero_points), ZT_OPT(B), ZT_OPT(output_scales), ZT_OPT(output_zero_points), \
+          ZT_DTYPE_OPT(output_dtype), zentorch_op_name);                                    \
+    });                                                                                     \
+  }
+
+ZT_QLINEAR_SHIM(qlinear, ZT_PO_NONE)
+ZT_QLINEAR_SHIM(qlinear_relu, ZT_PO_RELU)
+#undef ZT_QLINEAR_SHIM
+
+AOTITorchError aoti_torch_cuda_zentorch_qlinear_sigmoid(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,
+    AtenTensorHandle X_zero_points, AtenTensorHandle W_scales, AtenTensorHandle W_zero_points,
+    AtenTensorHandle *B, AtenTensorHandle *output_scales, AtenTensorHandle *output_zero_points,
+    const int32_t *output_dtype, const char *zentorch_op_name, AtenTensorHandle *ret0) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    auto r = zentorch_hip::qlinear_unary<ZT_PO_SIGMOID>(
+        ZT_T(X), ZT_T(W), ZT_T(X_scales), ZT_T(X_zero_points), ZT_T(W_scales),
+        ZT_T(W_zero_points), ZT_OPT(B), ZT_OPT(output_scales), ZT_OPT(output_zero_points),
+        ZT_DTYPE_OPT(output_dtype), zentorch_op_name);
+    *ret0 = new_tensor_handle(std::move(r));
+  });
+}
+
+AOTITorchError aoti_torch_cuda_zentorch_qlinear_mul_add(
+    AtenTensorHandle X, AtenTensorHandle W, AtenTensorHandle X_scales,
+    AtenTensorHandle X_zero_points, AtenTensorHandle W_scales, AtenTensorHandle W_zero_points,
+    AtenTensorHandle mul_input, AtenTensorHandle add_input, AtenTensorHandle *B,
+    AtenTensorHandle *output_scales, AtenTensorHandle *output_zero_points,
+    const int32_t *output_dtype, const char *zentorch_op_name, AtenTensorHandle *ret0) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    auto r = zentorch_hip::qlinear_mul_add(
+        ZT_T(X), ZT_T(W), ZT_T(X_scales), ZT_T(X_zero_points), ZT_T(W_scales),
+        ZT_T(W_zero_points), ZT_T(mul_input), ZT_T(add_input), ZT_OPT(B), ZT_OPT(output_scales),
+        ZT_OPT(output_zero_points), ZT_DTYPE_OPT(output_dtype), zentorch_op_name);
+    *ret0 = new_tensor_handle(std::move(r));
+  });
+}
+
 }  // extern "C"

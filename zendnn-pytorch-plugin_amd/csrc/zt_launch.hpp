@@ -99,6 +99,11 @@ struct DynArgs {
   // colsum[n] = sum_k w[n][k]); both null for symmetric s8
   const int32_t *azp;     // [M]
   const int32_t *colsum;  // [N]
+  int sw_bcast;           // one weight scale for every column (sw[0])
+  // y_dt ZT_DT_U8 / ZT_DT_S8: requantised output clamp(rint(v * (1 / *out_scale))
+  // + *out_zp) (out_zp null = 0)
+  const float *out_scale;
+  const int32_t *out_zp;
 };
 
 // frag: write qx in the fragment order (K % 64 == 0; the buffer holds
@@ -107,6 +112,12 @@ struct DynArgs {
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                                int8_t *qx, float *sx, bool frag, hipStream_t s,
                                int32_t *azp = nullptr);
+// Static per-tensor quantisation of zentorch_qlinear's activations into qx
+// (fragment order when frag), with sx[m] = *scale and, when azp is set,
+// azp[m] = the offset o with q - zp = qx - o (see static_quantize_kernel).
+hipError_t launch_static_quantize(const void *x, int x_dt, int64_t M, int64_t K, int8_t *qx,
+                                  bool frag, const float *scale, const int32_t *zp, float *sx,
+                                  int32_t *azp, hipStream_t s);
 // colsum[n] = sum_k w[n][k] of an int8 [N, K] weight
 hipError_t launch_s8_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,
                             hipStream_t s);

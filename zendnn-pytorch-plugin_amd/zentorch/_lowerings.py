@@ -37,6 +37,7 @@ SHIM_OPS = (
     "woq_linear_gelu_erf", "woq_linear_add", "woq_linear_mul_add", "woq_linear_add_add",
     "woq_linear_silu_mul", "woq_linear_gate_up_silu_mul", "dynamic_qlinear",
     "dynamic_qlinear_silu_mul", "dynamic_qlinear_add",
+    "qlinear", "qlinear_relu", "qlinear_sigmoid", "qlinear_mul_add",
 )
 
 
@@ -62,16 +63,20 @@ class ZentorchShimKernel(ir.ExternKernelAlloc):
     """One zentorch op, called through ``aoti_torch_cuda_zentorch_<op>``.
 
     ``slots[i]`` is the index in ``inputs`` of the i-th positional schema
-    argument, or None when that (optional) argument is absent.
+    argument, None when that (optional) argument is absent, or ``("const",
+    value)`` for a non-tensor argument (qlinear's output_dtype).
     """
 
-    def __init__(self, layout, inputs: Sequence[ir.IRNode], slots: List[Optional[int]],
-                 op_name: str, op, shim: str) -> None:
-        super().__init__(layout, inputs, (), {"zentorch_op_name": op_name},
+    def __init__(self, layout, inputs: Sequence[ir.IRNode], slots: List[Any],
+                 op_name: Optional[str], op, shim: str) -> None:
+        # op_name is None when the schema takes the name positionally (it is
+        # then one of the constant slots)
+        kw = {} if op_name is None else {"zentorch_op_name": op_name}
+        super().__init__(layout, inputs, (), kw,
                          python_kernel_name=f"torch.ops.zentorch.{op._schema.name.split('::')[1]}"
                                             ".default",
                          cpp_kernel_name=shim,
-                         ordered_kwargs_for_cpp_kernel=["zentorch_op_name"],
+                         ordered_kwargs_for_cpp_kernel=list(kw),
                          op_overload=op)
         self.slots = slots
 
@@ -84,10 +89,21 @@ class ZentorchShimKernel(ir.ExternKernelAlloc):
 
     def codegen_args(self) -> List[str]:
         wrapper = V.graph.wrapper_code
-        vals = [None if s is None else self.inputs[s] for s in self.slots]
+        vals = [None if s is None else (s[1] if isinstance(s, tuple) else self.inputs[s])
+                for s in self.slots]
         if V.graph.cpp_wrapper:
             pos = [a for a in self.op_overload._schema.arguments if not a.kwarg_only]
-            return [wrapper.val_to_arg_str(v, a.type) for v, a in zip(vals, pos)]
+            out = []
+            for v, a in zip(vals, pos):
+                if isinstance(v, torch.dtype):
+                    # the shims take a ScalarType as const int32_t *
+                    # (shim_cpu_zentorch.hpp:33 of the reference)
+                    var = f"var_{next(wrapper.arg_var_id)}"
+                    wrapper.writeline(f"int32_t {var} = {wrapper.codegen_dtype(v)};")
+                    out.append(f"&{var}")
+                else:
+                    out.append(wrapper.val_to_arg_str(v, a.type))
+            return out
         return [wrapper.val_to_arg_str(v) for v in vals]
 
     def apply_constraint(self) -> None:
@@ -99,9 +115,15 @@ class ZentorchShimKernel(ir.ExternKernelAlloc):
         values = _schema_values(op, args, kwargs)
         examples = _schema_values(op, fx_node.args, fx_node.kwargs)
         inputs, slots = [], []
-        for v, ex in zip(values, examples):
+        pos = [a for a in op._schema.arguments if not a.kwarg_only]
+        for v, ex, arg in zip(values, examples, pos):
             if v is None:
                 slots.append(None)
+                continue
+            if not isinstance(arg.type, (torch.TensorType, torch.OptionalType)) or (
+                    isinstance(arg.type, torch.OptionalType)
+                    and not isinstance(arg.type.getElementType(), torch.TensorType)):
+                slots.append(("const", v))
                 continue
             x = cls.realize_input(v)
             ev = ex.meta.get("val") if isinstance(ex, torch.fx.Node) else None
@@ -114,7 +136,8 @@ class ZentorchShimKernel(ir.ExternKernelAlloc):
         layout = ir.FixedLayout(out.device, out.dtype, size,
                                 ir.FlexibleLayout.contiguous_strides(size))
         name_arg = next(a for a in op._schema.arguments if a.name == "zentorch_op_name")
-        op_name = kwargs.get("zentorch_op_name", name_arg.default_value)
+        op_name = (kwargs.get("zentorch_op_name", name_arg.default_value)
+                   if name_arg.kwarg_only else None)
         return cls(layout, inputs, slots, op_name, op, shim)
 
 

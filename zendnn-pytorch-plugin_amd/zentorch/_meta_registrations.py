@@ -103,6 +103,52 @@ def meta_zentorch_s8_weight_colsum(weight):
     return weight.new_empty((weight.size(0),), dtype=torch.int32)
 
 
+def _qlinear_out(input, weight, output_dtype):
+    out = list(input.size())
+    out[-1] = weight.size(0)
+    return input.new_empty(out, dtype=output_dtype or torch.float32)
+
+
+@register_meta("zentorch_qlinear")
+def meta_zentorch_qlinear(input, weight, input_scales, input_zero_points, weight_scales,
+                          weight_zero_points, bias=None, output_scales=None,
+                          output_zero_points=None, output_dtype=None, zentorch_op_name=""):
+    return _qlinear_out(input, weight, output_dtype)
+
+
+@register_meta("zentorch_qlinear_relu")
+def meta_zentorch_qlinear_relu(input, weight, input_scales, input_zero_points, weight_scales,
+                               weight_zero_points, bias=None, output_scales=None,
+                               output_zero_points=None, output_dtype=None, zentorch_op_name=""):
+    return _qlinear_out(input, weight, output_dtype)
+
+
+@register_meta("zentorch_qlinear_sigmoid")
+def meta_zentorch_qlinear_sigmoid(input, weight, input_scales, input_zero_points,
+                                  weight_scales, weight_zero_points, bias=None,
+                                  output_scales=None, output_zero_points=None,
+                                  output_dtype=None, zentorch_op_name=""):
+    return _qlinear_out(input, weight, output_dtype)
+
+
+@register_meta("zentorch_qlinear_mul_add")
+def meta_zentorch_qlinear_mul_add(input, weight, input_scales, input_zero_points,
+                                  weight_scales, weight_zero_points, mul_input, add_input,
+                                  bias=None, output_scales=None, output_zero_points=None,
+                                  output_dtype=None, zentorch_op_name=""):
+    return _qlinear_out(input, weight, output_dtype)
+
+
+@register_meta("zentorch_qlinear", "out")
+def meta_zentorch_qlinear_out(out, *args, **kwargs):
+    return None
+
+
+@register_meta("zentorch_qlinear_relu", "out")
+def meta_zentorch_qlinear_relu_out(out, *args, **kwargs):
+    return None
+
+
 @register_meta("zentorch_woq_repack_weight")
 def meta_zentorch_woq_repack_weight(unpacked_weight):
     # [N, K/8] int32 (the reference's meta returns the input dtype, int8, which
