@@ -1517,7 +1517,13 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
     const char *tile = knob(kKnobS8Tile);
     const bool big = tile ? tile[0] == '2' : t256 >= 128;
     const char *kind = knob(kKnobS8Kind);  // w: load-wave kernel, n: 32x32x32 kernel, r, 2, 3
-    if (!kind || kind[0] == 'w') return launch_s8_ws<256, 128, 2, 2, 4, 3>(a, s);
+    if (!kind || kind[0] == 'w') {
+      // ZT_S8_TILE: "2" 256 x 128 tiles, "1" 128 x 128 with 3 stages, "0" 128 x 128 with 2
+      // stages (two workgroups per CU)
+      if (tile && tile[0] == '1') return launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s);
+      if (tile && tile[0] == '0') return launch_s8_ws<128, 128, 2, 2, 4, 2>(a, s);
+      return launch_s8_ws<256, 128, 2, 2, 4, 3>(a, s);
+    }
     if (kind[0] == 'n') {  // 32x32x32 kernel, S stages
       const int st = kind && kind[1] ? kind[1] - '0' : 3;
       if (st == 2) return big ? launch_s8_gemm32<256, 128, 2>(a, s) : launch_s8_gemm32<128, 128, 2>(a, s);
