@@ -18,6 +18,7 @@ DEV = "cuda"
 
 @pytest.fixture(autouse=True)
 def _announce(request):
+    import zentorch  # noqa: F401  (the torch ops)
     print(f"\n[case] {request.node.name}", flush=True)
 
 
