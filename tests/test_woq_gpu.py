@@ -375,3 +375,35 @@ def test_empty_and_error_paths():
     assert y.shape == (0, 32)
     with pytest.raises(RuntimeError, match="divide K"):
         C.woq_linear(xd, wd, torch.ones(3, 32, dtype=torch.bfloat16, device=DEV))
+
+
+# the wave-independent decode kernel (fast mode, M <= 16, N % 16 == 0,
+# K = 16 waves x 1 / 2 / 4 chunks): group sizes 128 / 256 / 1024 and per
+# channel, every M up to the LDS limit, bias and post-ops, strided x, and
+# the same result as the stream kernel it replaces on these shapes
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 13, 16])
+@pytest.mark.parametrize("K,N,G", [(2048, 16, 16), (4096, 4096, 32), (4096, 496, 16),
+                                   (8192, 256, 8), (8192, 112, 1)])
+def test_wave_kernel_vs_oracle(M, K, N, G, knobs):
+    knobs.set("ZT_WOQ_DEBUG", None)
+    y, y_ref = run_case(M, K, N, G, seed=M * 3 + G)
+    knobs.set("ZT_WOQ_WAVE", "0")
+    y_stream, _ = run_case(M, K, N, G, seed=M * 3 + G)
+    check_close(y, y_stream.cpu())
+
+
+@pytest.mark.parametrize("post,nbuf", [(("relu",), 0), (("gelu_erf",), 0), (("add",), 1),
+                                       (("mul", "add"), 2)])
+def test_wave_kernel_post_ops(post, nbuf):
+    run_case(4, 4096, 512, 32, post=post, nbuf=nbuf, seed=5, bias=True)
+
+
+def test_wave_kernel_strided_x():
+    M, K, N, G = 4, 4096, 256, 32
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=78)
+    xs = torch.randn(M, K + 64).bfloat16()
+    xs[:, :K] = x
+    y_ref = O.woq_linear(x, wp, s)
+    xd = xs.to(DEV)[:, :K]
+    y = C.woq_linear(xd, wp.to(DEV), s.to(DEV))
+    check_close(y, y_ref)

@@ -1300,6 +1300,145 @@ static hipError_t launch_decode_t(const WoqArgs &a, const DecodePlan &p, hipStre
 
 // x goes to LDS by DMA when its rows (or each phase's part of them) are
 // whole 1 KB pieces, 16-byte aligned, within 32-bit offsets
+// ------------------------------------------- wave-independent decode
+// One 16-row weight tile per workgroup, K split over NW waves of CPW
+// 128-wide chunks each, and no barrier until the final reduction: each wave
+// moves its own slice of x (its chunks' columns of the M token rows) into
+// its own LDS region by DMA, loads its own row scales per lane and issues
+// all its weight loads at once, then computes its chunks as they land.
+// (The stream kernel's shared x copy needs one barrier before any wave
+// computes; here the waves start as soon as their own loads arrive.)  The
+// NW partial tiles meet in LDS and are added in wave order, as the stream
+// kernel does.  Fast mode only: signed int4, bf16 scales, bf16 x, M <= 16.
+// A wave's region holds its [M][CPW * 256 B] slice rounded up to whole
+// 1 KB DMA instructions (each writes 64 lanes x 16 B, the lanes past the
+// slice writing zeros), so no DMA reaches the next wave's region.
+__host__ __device__ constexpr int wave_region_bytes(int M, int CPW) {
+  return (M * CPW * 256 + 1023) / 1024 * 1024;
+}
+template <int NW, int CPW>
+constexpr size_t wave_x_bytes(int M) {
+  return (size_t)NW * wave_region_bytes(M, CPW);
+}
+
+template <int NW, int CPW>
+__global__ __launch_bounds__(64 * NW) void woq_wave_kernel(WoqArgs a, int cpg_shift, int gmask) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
+  const int rb = blockIdx.x * 16;  // N % 16 == 0 (host-checked)
+  constexpr int RB = CPW * 256;    // bytes of one token row of the wave's slice
+  constexpr int UPR = RB / 16;     // 16-byte units per row
+  const int c0 = wv * CPW;         // the wave's first chunk (K == NW * CPW * 128)
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
+  unsigned char *xw = smem + (size_t)wv * wave_region_bytes(M, CPW);
+  // 1. the wave's x slice [M][RB] by DMA: unit u = 64 j + lane is row u / UPR,
+  //    16-byte column u % UPR
+  const int units = M * UPR;
+  for (int j = 0; j * 64 < units; ++j) {
+    const int u = j * 64 + lane;
+    const int row = u / UPR, col = u - row * UPR;
+    const uint32_t off = u < units ? (uint32_t)(row * a.ldx * 2 + c0 * 256 + col * 16) : kOobOffset;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(xw + j * 1024), 16, off, 0, 0, 0);
+  }
+  // 2. the row scales of its chunks, 3. all its weights
+  uint32_t sr[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const uint32_t g = (uint32_t)(((c0 + c) >> cpg_shift) & gmask);
+    sr[c] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, (g * (uint32_t)N + (uint32_t)(rb + lr)) * 2u,
+                                                 0, 0);
+  }
+  u32x4_t wr[CPW];
+  const uint32_t row_off = (uint32_t)(rb + lr) * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+    wr[c] = __builtin_bit_cast(
+        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, row_off + (uint32_t)(c0 + c) * 64u, 0, 0));
+  // the x DMA was issued first: once at most the 2 CPW later loads are
+  // outstanding it has landed in this wave's region (no other wave writes it)
+  constexpr int after = 2 * CPW > 63 ? 63 : 2 * CPW;
+  __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  // token columns past M repeat row M-1: their sums are never stored
+  const int row = min(lr, M - 1);
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const float sc = __uint_as_float(sr[c] << 16);
+    u32x4_t xb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xb[i] = *reinterpret_cast<const u32x4_t *>(xw + row * RB + (c * 128 + 32 * lg + 8 * i) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dq_word<kDecFast>(wr[c][i], sc, 0.f, 0),
+                                                    __builtin_bit_cast(bf16x8_t, xb[i]), acc, 0, 0, 0);
+  }
+  // 4. partial D[row = 4 lg + r][token = lr] -> slab[wave] (over x, after every
+  //    wave is done with its slice), then each output adds the NW partials in
+  //    wave order
+  __syncthreads();
+  float *slab = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) slab[(wv * 16 + 4 * lg + r) * 17 + lr] = acc[r];
+  __syncthreads();
+  for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
+    const int m = idx / 16, nr = idx - m * 16;
+    const int n = rb + nr;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += slab[(w * 16 + nr) * 17 + m];
+    if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
+    v = apply_post_ops(v, a.post, m, n);
+    store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
+  }
+}
+
+template <int NW, int CPW>
+static hipError_t launch_wave_t(const WoqArgs &a, hipStream_t s, int shift, int gmask) {
+  const size_t slab = (size_t)NW * 16 * 17 * 4;
+  const size_t x = wave_x_bytes<NW, CPW>((int)a.M);
+  woq_wave_kernel<NW, CPW><<<dim3((unsigned)(a.N / 16)), dim3(64 * NW), x > slab ? x : slab, s>>>(
+      a, shift, gmask);
+  return hipGetLastError();
+}
+
+// The wave-independent kernel where it applies: fast mode, bf16 x with
+// 16-byte rows, M <= 16, N % 16 == 0, K = 16 waves x CPW chunks (CPW 1, 2
+// or 4) and the x slices within 64 KB.  Measured on the config-0 shape
+// (M = 4, 4096 x 4096, graph replays): 4.58 us against 4.90 for the stream
+// kernel's 8 waves of 4 chunks.
+static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
+                            hipError_t *err) {
+  const char *e = knob(kKnobWoqWave);  // "0" disables
+  if (e && e[0] == '0') return false;
+  if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || a.N % 16 ||
+      a.K % (16 * 128))
+    return false;
+  if (((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) ||
+      (a.M - 1) * a.ldx * 2 + a.K * 2 >= (int64_t)kOobOffset ||
+      a.N * (a.K / 2) >= (int64_t)kOobOffset || a.G * a.N * 2 >= (int64_t)kOobOffset)
+    return false;
+  const int cpw = (int)(a.K / (16 * 128));
+  if (knob(kKnobWoqDebug))
+    std::fprintf(stderr, "[zt] woq wave M=%lld N=%lld K=%lld: NW=16 CPW=%d\n", (long long)a.M,
+                 (long long)a.N, (long long)a.K, cpw);
+#define ZT_WAVE_CASE(CPW_)                                                      \
+  if (cpw == CPW_ && wave_x_bytes<16, CPW_>((int)a.M) <= 64 * 1024) {           \
+    *err = launch_wave_t<16, CPW_>(a, s, shift, gmask);                        \
+    return true;                                                               \
+  }
+  ZT_WAVE_CASE(1) ZT_WAVE_CASE(2) ZT_WAVE_CASE(4)
+#undef ZT_WAVE_CASE
+  return false;
+}
+
 static bool stream_x_dma(const WoqArgs &a, int p) {
   return (a.K / p) % 512 == 0 &&
          ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) == 0 &&
@@ -1339,6 +1478,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
   // N take the general bf16-scale mode (same weights, same results)
   if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
+  if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, err)) return true;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles, or more
   // tiles than CUs when x takes most of the LDS (one workgroup per CU)
