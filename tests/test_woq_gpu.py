@@ -211,6 +211,7 @@ def run_gate_up(M, K, I, G, seed, zp=None, x_dtype=torch.bfloat16, bias=True):
     xd, wd, sd, zd, bd = gpu(x, wp, s, z, b)
     y = C.woq_linear_gate_up(xd, wd, sd, zd, bd)
     check_close(y, y_ref)
+    return y, y_ref
 
 
 # one launch: bf16, up to 16 rows, I % 16 == 0 (one gate/up tile pair per
@@ -377,8 +378,8 @@ def test_empty_and_error_paths():
         C.woq_linear(xd, wd, torch.ones(3, 32, dtype=torch.bfloat16, device=DEV))
 
 
-# the wave-independent decode kernel (fast mode, M <= 16, N % 16 == 0,
-# K = 16 waves x 1 / 2 / 4 chunks): group sizes 128 / 256 / 1024 and per
+# the wave-independent decode kernel (fast mode, M <= 16, even N, K = 16
+# waves x 1 / 2 / 4 chunks): group sizes 128 / 256 / 1024 and per
 # channel, every M up to the LDS limit, bias and post-ops, strided x, and
 # the same result as the stream kernel it replaces on these shapes
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 13, 16])
@@ -407,3 +408,22 @@ def test_wave_kernel_strided_x():
     xd = xs.to(DEV)[:, :K]
     y = C.woq_linear(xd, wp.to(DEV), s.to(DEV))
     check_close(y, y_ref)
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 8192, 4100, 64), (2, 8192, 514, 8),
+                                     (1, 4096, 1000, 32), (3, 2048, 50, 16)])
+def test_wave_kernel_ragged_n(M, K, N, G, knobs):
+    y, _ = run_case(M, K, N, G, seed=M + N)
+    knobs.set("ZT_WOQ_WAVE", "0")
+    y_stream, _ = run_case(M, K, N, G, seed=M + N)
+    check_close(y, y_stream.cpu())
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("K,I,G", [(4096, 256, 32), (2048, 1040, 1), (8192, 64, 64)])
+def test_wave_kernel_gate_up(M, K, I, G, knobs):
+    knobs.set("ZT_WOQ_WAVE", "1")  # also below 5 rows
+    y, y_ref = run_gate_up(M, K, I, G, seed=M + I)
+    knobs.set("ZT_WOQ_WAVE", "0")
+    y_stream, _ = run_gate_up(M, K, I, G, seed=M + I)
+    check_close(y, y_stream.cpu())

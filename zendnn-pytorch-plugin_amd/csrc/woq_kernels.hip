@@ -1321,14 +1321,18 @@ constexpr size_t wave_x_bytes(int M) {
   return (size_t)NW * wave_region_bytes(M, CPW);
 }
 
-template <int NW, int CPW>
-__global__ __launch_bounds__(64 * NW) void woq_wave_kernel(WoqArgs a, int cpg_shift, int gmask) {
+template <int NW, int CPW, int TPW>
+__global__ __launch_bounds__(64 * NW) void woq_wave_kernel(WoqArgs a, int cpg_shift, int gmask,
+                                                           int gu) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
-  const int rb = blockIdx.x * 16;  // N % 16 == 0 (host-checked)
+  // tile t's first weight row: TPW consecutive 16-row tiles, or with gu > 0
+  // (merged gate_up, TPW == 2) gate rows j0.. and the up rows gu + j0..
+  const int j0 = blockIdx.x * 16;
+  auto rowbase = [&](int t) { return gu ? t * gu + j0 : (blockIdx.x * TPW + t) * 16; };
   constexpr int RB = CPW * 256;    // bytes of one token row of the wave's slice
   constexpr int UPR = RB / 16;     // 16-byte units per row
   const int c0 = wv * CPW;         // the wave's first chunk (K == NW * CPW * 128)
@@ -1345,94 +1349,138 @@ __global__ __launch_bounds__(64 * NW) void woq_wave_kernel(WoqArgs a, int cpg_sh
     const uint32_t off = u < units ? (uint32_t)(row * a.ldx * 2 + c0 * 256 + col * 16) : kOobOffset;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(xw + j * 1024), 16, off, 0, 0, 0);
   }
-  // 2. the row scales of its chunks, 3. all its weights
-  uint32_t sr[CPW];
+  // 2. the row scales of its chunks, 3. all its weights (rows past N, only
+  //    in the last workgroup of a plain call, read zeros and are not stored)
+  uint32_t sr[TPW][CPW];
+  u32x4_t wr[TPW][CPW];
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) {
-    const uint32_t g = (uint32_t)(((c0 + c) >> cpg_shift) & gmask);
-    sr[c] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, (g * (uint32_t)N + (uint32_t)(rb + lr)) * 2u,
-                                                 0, 0);
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const uint32_t g = (uint32_t)(((c0 + c) >> cpg_shift) & gmask);
+      sr[t][c] = __builtin_amdgcn_raw_buffer_load_b16(
+          s_rs, (g * (uint32_t)N + (uint32_t)(rowbase(t) + lr)) * 2u, 0, 0);
+    }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int n = rowbase(t) + lr;
+    const uint32_t row_off = n < N ? (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u : kOobOffset;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+      wr[t][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 w_rs, row_off + (uint32_t)(c0 + c) * 64u, 0, 0));
   }
-  u32x4_t wr[CPW];
-  const uint32_t row_off = (uint32_t)(rb + lr) * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
-#pragma unroll
-  for (int c = 0; c < CPW; ++c)
-    wr[c] = __builtin_bit_cast(
-        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, row_off + (uint32_t)(c0 + c) * 64u, 0, 0));
-  // the x DMA was issued first: once at most the 2 CPW later loads are
-  // outstanding it has landed in this wave's region (no other wave writes it)
-  constexpr int after = 2 * CPW > 63 ? 63 : 2 * CPW;
+  // the x DMA was issued first: once at most the later loads are outstanding
+  // it has landed in this wave's region (no other wave writes it)
+  constexpr int after = 2 * TPW * CPW > 63 ? 63 : 2 * TPW * CPW;
   __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (7 << 4) | (15 << 8));
   asm volatile("" ::: "memory");
 
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // token columns past M repeat row M-1: their sums are never stored
   const int row = min(lr, M - 1);
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
-    const float sc = __uint_as_float(sr[c] << 16);
     u32x4_t xb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       xb[i] = *reinterpret_cast<const u32x4_t *>(xw + row * RB + (c * 128 + 32 * lg + 8 * i) * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dq_word<kDecFast>(wr[c][i], sc, 0.f, 0),
-                                                    __builtin_bit_cast(bf16x8_t, xb[i]), acc, 0, 0, 0);
+    for (int t = 0; t < TPW; ++t) {
+      const float sc = __uint_as_float(sr[t][c] << 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dq_word<kDecFast>(wr[t][c][i], sc, 0.f, 0),
+                                                         __builtin_bit_cast(bf16x8_t, xb[i]), acc[t],
+                                                         0, 0, 0);
+    }
   }
-  // 4. partial D[row = 4 lg + r][token = lr] -> slab[wave] (over x, after every
-  //    wave is done with its slice), then each output adds the NW partials in
-  //    wave order
+  // 4. partial D[row = 4 lg + r][token = lr] of tile t -> slab[wave][t] (over
+  //    x, after every wave is done with its slice), then each output adds the
+  //    NW partials in wave order
   __syncthreads();
   float *slab = reinterpret_cast<float *>(smem);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) slab[(wv * 16 + 4 * lg + r) * 17 + lr] = acc[r];
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][r];
   __syncthreads();
-  for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
-    const int m = idx / 16, nr = idx - m * 16;
-    const int n = rb + nr;
+  if (gu) {
+    for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
+      const int m = idx / 16, nr = idx - m * 16;
+      const int jj = j0 + nr;
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        g += slab[((w * TPW) * 16 + nr) * 17 + m];
+        u += slab[((w * TPW + 1) * 16 + nr) * 17 + m];
+      }
+      if (a.bias) {
+        g = g + load_elem(a.bias, a.b_dt, jj);
+        u = u + load_elem(a.bias, a.b_dt, gu + jj);
+      }
+      if (a.y_dt == ZT_DT_BF16) u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+      store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + jj, unary_op(ZT_PO_SILU, g) * u);
+    }
+    return;
+  }
+  for (int idx = tid; idx < TPW * 16 * M; idx += 64 * NW) {
+    const int m = idx / (TPW * 16), nr = idx - m * (TPW * 16);
+    const int n = blockIdx.x * TPW * 16 + nr;
+    if (n >= N) continue;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) v += slab[(w * 16 + nr) * 17 + m];
+    for (int w = 0; w < NW; ++w) v += slab[((w * TPW + (nr >> 4)) * 16 + (nr & 15)) * 17 + m];
     if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
     v = apply_post_ops(v, a.post, m, n);
     store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
   }
 }
 
-template <int NW, int CPW>
-static hipError_t launch_wave_t(const WoqArgs &a, hipStream_t s, int shift, int gmask) {
-  const size_t slab = (size_t)NW * 16 * 17 * 4;
+template <int NW, int CPW, int TPW>
+static hipError_t launch_wave_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int gu) {
+  const size_t slab = (size_t)NW * TPW * 16 * 17 * 4;
   const size_t x = wave_x_bytes<NW, CPW>((int)a.M);
-  woq_wave_kernel<NW, CPW><<<dim3((unsigned)(a.N / 16)), dim3(64 * NW), x > slab ? x : slab, s>>>(
-      a, shift, gmask);
+  const unsigned blocks = gu ? (unsigned)(gu / 16) : (unsigned)((a.N + 16 * TPW - 1) / (16 * TPW));
+  woq_wave_kernel<NW, CPW, TPW><<<dim3(blocks), dim3(64 * NW), x > slab ? x : slab, s>>>(
+      a, shift, gmask, gu);
   return hipGetLastError();
 }
 
 // The wave-independent kernel where it applies: fast mode, bf16 x with
-// 16-byte rows, M <= 16, N % 16 == 0, K = 16 waves x CPW chunks (CPW 1, 2
-// or 4) and the x slices within 64 KB.  Measured on the config-0 shape
-// (M = 4, 4096 x 4096, graph replays): 4.58 us against 4.90 for the stream
-// kernel's 8 waves of 4 chunks.
+// 16-byte rows, M <= 16, K = 16 waves x CPW chunks (CPW 1, 2 or 4) and the
+// x slices within 64 KB; gu > 0 is the merged gate_up (I = gu, a multiple
+// of 16; "1" in ZT_WOQ_WAVE takes it below 5 rows too).  Measured on the config-0 shape (M = 4, 4096 x 4096,
+// graph replays): 4.92 us against 5.12 for the stream kernel's 8 waves of 4
+// chunks.
 static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
-                            hipError_t *err) {
+                            int gu, hipError_t *err) {
   const char *e = knob(kKnobWoqWave);  // "0" disables
   if (e && e[0] == '0') return false;
-  if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || a.N % 16 ||
-      a.K % (16 * 128))
+  if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || a.K % (16 * 128) ||
+      (gu ? gu % 16 : a.N % 2))
     return false;
   if (((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) ||
       (a.M - 1) * a.ldx * 2 + a.K * 2 >= (int64_t)kOobOffset ||
       a.N * (a.K / 2) >= (int64_t)kOobOffset || a.G * a.N * 2 >= (int64_t)kOobOffset)
     return false;
   const int cpw = (int)(a.K / (16 * 128));
+  // measured against the stream kernel in the same process (graph replays
+  // over rotating weights, Llama-3 8B shapes): QKV 6.3-6.4 us against
+  // 6.7-6.9 at M = 2..8, O even; the merged gate_up only from M = 5 (18.2 us
+  // against 20.0 at M = 8, but 18.2 against 17.3 at M = 1); the down
+  // projection (16 x 7 chunks, M <= 2) no faster, so CPW 7 is not used
+  if (gu && a.M < 5 && !e) return false;
   if (knob(kKnobWoqDebug))
-    std::fprintf(stderr, "[zt] woq wave M=%lld N=%lld K=%lld: NW=16 CPW=%d\n", (long long)a.M,
-                 (long long)a.N, (long long)a.K, cpw);
-#define ZT_WAVE_CASE(CPW_)                                                      \
-  if (cpw == CPW_ && wave_x_bytes<16, CPW_>((int)a.M) <= 64 * 1024) {           \
-    *err = launch_wave_t<16, CPW_>(a, s, shift, gmask);                        \
-    return true;                                                               \
+    std::fprintf(stderr, "[zt] woq wave M=%lld N=%lld K=%lld gu=%d: NW=16 CPW=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, gu, cpw);
+#define ZT_WAVE_CASE(CPW_)                                                         \
+  if (cpw == CPW_ && wave_x_bytes<16, CPW_>((int)a.M) <= 64 * 1024) {              \
+    *err = gu ? launch_wave_t<16, CPW_, 2>(a, s, shift, gmask, gu)                 \
+              : launch_wave_t<16, CPW_, 1>(a, s, shift, gmask, 0);                 \
+    return true;                                                                  \
   }
   ZT_WAVE_CASE(1) ZT_WAVE_CASE(2) ZT_WAVE_CASE(4)
 #undef ZT_WAVE_CASE
@@ -1478,7 +1526,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
   // N take the general bf16-scale mode (same weights, same results)
   if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
-  if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, err)) return true;
+  if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, 0, err)) return true;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles, or more
   // tiles than CUs when x takes most of the LDS (one workgroup per CU)
@@ -1949,6 +1997,8 @@ bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   int shift = 0;
   while (cpg > 1 && (1 << shift) < cpg) ++shift;
   const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, kDecFast, (int)I, err))
+    return true;
   const int C = (int)(a.K / 128), tiles = (int)(a.N / 16);
   const size_t x_bytes = (size_t)a.M * stream_x_pitch((int)a.K) * 2;
   // as the plain stream kernel: four tiles (two pairs) per wave once x
