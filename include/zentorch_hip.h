@@ -115,11 +115,12 @@ size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
  * round_y rounds u to y_dtype first, so y equals the two-op composition
  * u = zt_woq_linear(x, W[I:2I]) then zt_woq_linear(x, W[0:I]) with the
  * post-ops {SILU, MUL u}.  Arguments as zt_woq_linear without post-ops;
- * N even, y [M, ldy] with N/2 columns.  Up to 16 rows of bf16 x with bf16
- * scales and I % 16 == 0, and 17-64 such rows with I % 64 == 0 and
- * K % 512 == 0 where the linear needs no K split, run as one launch without
- * workspace; other calls run the full linear into fp32 in the workspace,
- * then the epilogue (zt_woq_linear_gate_up_workspace_size bytes).
+ * N even, y [M, ldy] with N/2 columns.  Pass a workspace of
+ * zt_woq_linear_gate_up_workspace_size(M, K, N, G) bytes on every call:
+ * calls the fused kernels take (bf16 x and scales, no zero points, up to 64
+ * rows, I % 16 == 0, x within the kernel's LDS, no K split) run as one
+ * launch and leave it untouched; the others run the full linear into fp32
+ * there, then the epilogue.
  */
 int zt_woq_linear_gate_up(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                           int64_t ldx, const int32_t *w_packed, int64_t N,
