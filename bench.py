@@ -568,7 +568,7 @@ def secondary_rooflines(res):
                     "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(d["frac_hbm"], 4),
                     "achieved_tops": round(d["TOPS"], 2), "frac_int8_peak": round(d["frac_int8_peak"], 4),
-                    "kernels": "dyn_quantize_bf16_kernel + s8_skinny32_kernel",
+                    "kernels": "dyn_quantize_bf16_kernel + s8_splitk_kernel",
                     "op_avg_us": round(d["s_per_call"] * 1e6, 3)})
     d = res.get("prefill_int8_m2048")
     if d:

@@ -146,7 +146,12 @@ size_t zt_woq_linear_gate_up_workspace_size(int64_t M, int64_t K, int64_t N,
  *  post     NULL for the reference op (it has no post-ops,
  *           docs/zentorch_dynamic_qlinear.md:99); non-NULL is an extension
  *  y        [M, N] in y_dtype
- *  workspace: zt_dynamic_qlinear_workspace_size(M, K) bytes
+ *  workspace: zt_dynamic_qlinear_workspace_size(M, K, N) bytes.  Its first
+ *           part holds the quantised activations and row scales; the rest
+ *           (for 64 < M <= 128, K % 256 == 0) holds the exchange of the
+ *           split-K GEMM.  A workspace holding only the first part
+ *           (zt_dynamic_qlinear_workspace_size(M, K, 0)) is accepted and runs
+ *           the unsplit kernel, with the same results.
  */
 int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                        const int8_t *w, int64_t N, const void *w_scales,
@@ -155,7 +160,7 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                        int32_t y_dtype, void *workspace, size_t workspace_bytes,
                        zt_stream_t stream);
 
-size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K);
+size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K, int64_t N);
 
 /*
  * zt_dynamic_qlinear without a workspace argument: allocates nothing.  No
@@ -164,8 +169,9 @@ size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K);
  * harnesses that forbid hipMalloc).  The quantised activations and row
  * scales go to a scratch array of ZT_DYN_SCRATCH_BYTES that each GPU holds
  * from the first call on it until the process ends, so a call is limited to
- * zt_dynamic_qlinear_workspace_size(M, K) <= ZT_DYN_SCRATCH_BYTES (about
- * M * K <= 32 Mi; larger calls return ZT_EINVAL and launch nothing).  Every
+ * zt_dynamic_qlinear_workspace_size(M, K, 0) <= ZT_DYN_SCRATCH_BYTES (about
+ * M * K <= 32 Mi; larger calls return ZT_EINVAL and launch nothing); the
+ * split-K exchange uses the rest of the array when it fits.  Every
  * call on one GPU shares that GPU's array: calls that overlap in time on one
  * GPU (different streams, or threads without ordering) race and must not be
  * issued.  Nothing in the scratch needs to start at zero; it keeps the last
@@ -218,7 +224,8 @@ int zt_s8s8s32_gemm(const int8_t *qa, const int8_t *w, int64_t M, int64_t N,
  *            computed once per weight and kept beside it
  *  y_dtype   bf16 / fp32, or ZT_DT_S32 for the corrected accumulators
  *            sum_k (q - zp) * w exactly (no scales, bias or post-ops)
- *  workspace zt_dynamic_qlinear_asym_workspace_size(M, K) bytes
+ *  workspace zt_dynamic_qlinear_asym_workspace_size(M, K, N) bytes (as for
+ *            zt_dynamic_qlinear: N = 0 gives the least that is accepted)
  * Other arguments as zt_dynamic_qlinear.
  */
 int zt_dynamic_qlinear_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
@@ -228,7 +235,7 @@ int zt_dynamic_qlinear_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K
                             void *y, int32_t y_dtype, void *workspace,
                             size_t workspace_bytes, zt_stream_t stream);
 
-size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K);
+size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K, int64_t N);
 
 /* The asymmetric quantisation stage on its own (same kernel): qx[M, K] =
  * q - 128 as int8, sx[M] fp32, azp[M] = zp - 128 int32.  No reference
@@ -260,7 +267,8 @@ int zt_dynamic_quantize_asym(const void *x, int32_t x_dtype, int64_t M, int64_t 
  *                fp32 scalar) u8 when y_zero_point (device int32) is given
  *                and s8 when not, y = clamp(rint(v * (1 / y_scale)) + zp)
  *                (the reference scales by 1 / output_scales, QLinear.cpp:163-166).
- *  workspace     zt_qlinear_workspace_size(M, K) bytes
+ *  workspace     zt_qlinear_workspace_size(M, K, N) bytes (N = 0: the least
+ *                that is accepted, without the split-K exchange)
  * Weight zero points are not an argument: the reference's matmul path leaves
  * them unused (QLinear.cpp:248-262), so weights are symmetric.
  */
@@ -271,7 +279,7 @@ int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float
                const float *y_scale, const int32_t *y_zero_point, void *workspace,
                size_t workspace_bytes, zt_stream_t stream);
 
-size_t zt_qlinear_workspace_size(int64_t M, int64_t K);
+size_t zt_qlinear_workspace_size(int64_t M, int64_t K, int64_t N);
 
 /* colsum[n] = sum_k w[n][k] of an int8 [N, K] row-major weight, exactly in
  * int32.  No reference counterpart (extension above). */
@@ -332,9 +340,9 @@ const char *zt_last_error_string(void);
  * variables on every call).  Each knob is named after the environment
  * variable that sets it when the library is loaded (ZT_WOQ_FORCE_KERNEL,
  * ZT_WOQ_DECODE_PLAN, ZT_WOQ_STREAM, ZT_WOQ_WIDE, ZT_WOQ_GEMM, ZT_WOQ_DEBUG,
- * ZT_WOQ_WAVE,
- * ZT_S8_SKINNY32, ZT_S8_SKINNY, ZT_S8_FRAG, ZT_S8_FORCE, ZT_S8_TILE,
- * ZT_S8_KIND, ZT_MOE_BN); the environment is not read again.  value NULL or
+ * ZT_WOQ_WAVE, ZT_S8_SKINNY32, ZT_S8_SKINNY, ZT_S8_FRAG, ZT_S8_FORCE,
+ * ZT_S8_TILE, ZT_S8_KIND, ZT_S8_SPLIT, ZT_MOE_BN); the environment is not
+ * read again.  value NULL or
  * "" unsets the knob.  Returns ZT_EINVAL for an unknown name.  Launches
  * already enqueued are not affected.
  */

@@ -66,7 +66,14 @@ def test_c_abi_validates_without_gpu():
     assert rc == 1 and b"K" in L.zt_last_error_string()
     rc = L.zt_woq_repack_from_int4pack(None, 10, 64, None, None)
     assert rc == 1 and b"multiple of 64" in L.zt_last_error_string()
-    assert L.zt_dynamic_qlinear_workspace_size(128, 4096) >= 128 * 4096 + 128 * 4
+    assert L.zt_dynamic_qlinear_workspace_size(128, 4096, 0) >= 128 * 4096 + 128 * 4
+    # the split-K exchange (64 < M <= 128, K % 256 == 0): int32 partials of
+    # both K halves of every 96-column tile, then the tile counters
+    base = L.zt_dynamic_qlinear_workspace_size(128, 4096, 0)
+    tiles = (11008 + 95) // 96
+    assert L.zt_dynamic_qlinear_workspace_size(128, 4096, 11008) >= base + tiles * 2 * 128 * 96 * 4
+    assert L.zt_dynamic_qlinear_workspace_size(64, 4096, 11008) == \
+        L.zt_dynamic_qlinear_workspace_size(64, 4096, 0)
     # MoE: H, I multiples of 128; E <= 1024; activations the kernels have
     rc = L.zt_woq_moe(None, 4, 100, None, None, 0, 2, 0, 4, None, None, 1, None, None, None,
                       1, None, 8, 256, None, None, 0, None)

@@ -136,6 +136,46 @@ def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, knobs):
     torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
 
 
+# 64 < M <= 128 with K % 256 == 0 runs the split-K kernel when the workspace
+# holds its exchange (two K halves per 96-column tile, the second to finish
+# adds the other's int32 partial): bit-identical to the unsplit kernel (the
+# least workspace), on ragged M, N past a tile, N % 4 != 0, one or an odd
+# number of 128-k chunks per half, every load depth.  Calls alternate two
+# inputs, so a partial left from the previous call cannot pass for the
+# current one; each call reuses the freed workspace, whose tile counters the
+# quantise kernel clears.
+@pytest.mark.parametrize("M,K,N,depth", [(65, 256, 1, None), (70, 512, 95, None),
+                                         (96, 768, 96, "3"), (97, 1024, 97, "4"),
+                                         (128, 2816, 203, None), (128, 4096, 11008, None),
+                                         (128, 4096, 11008, "3"), (100, 1536, 4100, "4")])
+def test_dynamic_qlinear_split_k(M, K, N, depth, knobs):
+    if depth:
+        knobs.set("ZT_S8_SPLIT", depth)
+    x, w, sw, b = make(M, K, N, seed=M * 7 + K + N)
+    x2 = torch.randn(M, K, generator=torch.Generator().manual_seed(K)).to(x.dtype)
+    wd, swd, bd = w.to(DEV), sw.to(DEV), b.to(DEV)
+    xs = [x.to(DEV), x2.to(DEV)]
+    y0 = [C.dynamic_qlinear(xi, wd, swd, bd, split=False).cpu() for xi in xs]
+    for i in (0, 1, 0, 1):
+        assert torch.equal(C.dynamic_qlinear(xs[i], wd, swd, bd).cpu(), y0[i])
+    torch.testing.assert_close(y0[0].float(), O.dynamic_qlinear(x, w, sw, b).float(),
+                               rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("post", [("relu",), ("add",), ("mul", "add"), ("silu",)])
+def test_dynamic_qlinear_split_k_post_ops(post):
+    M, K, N = 112, 1280, 300
+    x, w, sw, b = make(M, K, N, seed=5)
+    g = torch.Generator().manual_seed(13)
+    bufs = [torch.randn(M, N, generator=g).bfloat16() for p in post if p in ("add", "mul")]
+    args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV))
+    kw = dict(post_ops=post, post_bufs=[t.to(DEV) for t in bufs])
+    y = C.dynamic_qlinear(*args, **kw).cpu()
+    assert torch.equal(y, C.dynamic_qlinear(*args, split=False, **kw).cpu())
+    y_ref = O.dynamic_qlinear(x, w, sw, b, post_ops=post, post_bufs=bufs)
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("post", [("relu",), ("add",), ("mul", "add"), ("gelu_tanh",)])
 def test_dynamic_qlinear_fragment_kernel_post_ops(post):
     M, K, N = 48, 512, 136

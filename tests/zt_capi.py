@@ -49,14 +49,14 @@ def lib():
         L.zt_dynamic_qlinear.argtypes = [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _i32, _vp,
                                          _i32, ctypes.POINTER(PostOps), _vp, _i32, _vp,
                                          _sz, _vp]
-        L.zt_dynamic_qlinear_workspace_size.argtypes = [_i64, _i64]
+        L.zt_dynamic_qlinear_workspace_size.argtypes = [_i64, _i64, _i64]
         L.zt_dynamic_qlinear_workspace_size.restype = _sz
         L.zt_dynamic_quantize.argtypes = [_vp, _i32, _i64, _i64, _vp, _vp, _vp]
         L.zt_s8s8s32_gemm.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp]
         L.zt_dynamic_qlinear_asym.argtypes = [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _i32,
                                               _vp, _vp, _i32, ctypes.POINTER(PostOps), _vp,
                                               _i32, _vp, _sz, _vp]
-        L.zt_dynamic_qlinear_asym_workspace_size.argtypes = [_i64, _i64]
+        L.zt_dynamic_qlinear_asym_workspace_size.argtypes = [_i64, _i64, _i64]
         L.zt_dynamic_qlinear_asym_workspace_size.restype = _sz
         L.zt_dynamic_quantize_asym.argtypes = [_vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp]
         L.zt_s8_weight_colsum.argtypes = [_vp, _i64, _i64, _vp, _vp]
@@ -175,14 +175,16 @@ def woq_linear_gate_up(x, w_nk, scales, zp=None, bias=None, sync=True):
     return y
 
 
-def dynamic_qlinear(x, w, sw, bias=None, post_ops=(), post_bufs=(), sync=True):
+def dynamic_qlinear(x, w, sw, bias=None, post_ops=(), post_bufs=(), sync=True, split=True):
+    """split=False passes the least workspace (no room for the split-K
+    exchange), which runs the unsplit kernel."""
     K = x.shape[-1]
     x2 = x.reshape(-1, K).contiguous()
     M = x2.shape[0]
     N = w.shape[0]
     y = torch.empty(M, N, dtype=x.dtype, device=x.device)
     po, keep = make_post(post_ops, post_bufs, N)
-    ws_bytes = lib().zt_dynamic_qlinear_workspace_size(M, K)
+    ws_bytes = lib().zt_dynamic_qlinear_workspace_size(M, K, N if split else 0)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     rc = lib().zt_dynamic_qlinear(
         _p(x2), DT[x2.dtype], M, K, _p(w), N, _p(sw), DT[sw.dtype], _p(bias),
@@ -230,14 +232,14 @@ def dynamic_quantize_asym(x):
 
 
 def dynamic_qlinear_asym(x, w, sw, colsum, bias=None, out_dtype=None, post_ops=(),
-                         post_bufs=()):
+                         post_bufs=(), split=True):
     K = x.shape[-1]
     x2 = x.reshape(-1, K).contiguous()
     M = x2.shape[0]
     N = w.shape[0]
     y = torch.empty(M, N, dtype=out_dtype or x.dtype, device=x.device)
     po, keep = make_post(post_ops, post_bufs, N)
-    ws_bytes = lib().zt_dynamic_qlinear_asym_workspace_size(M, K)
+    ws_bytes = lib().zt_dynamic_qlinear_asym_workspace_size(M, K, N if split else 0)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     rc = lib().zt_dynamic_qlinear_asym(
         _p(x2), DT[x2.dtype], M, K, _p(w), N, _p(sw), DT[sw.dtype], _p(colsum), _p(bias),

@@ -112,7 +112,7 @@ constexpr const char *kKnobNames[kKnobCount] = {
     "ZT_WOQ_FORCE_KERNEL", "ZT_WOQ_DECODE_PLAN", "ZT_WOQ_STREAM", "ZT_WOQ_WIDE",
     "ZT_WOQ_GEMM",         "ZT_WOQ_DEBUG",       "ZT_WOQ_WAVE",    "ZT_S8_SKINNY32", "ZT_S8_SKINNY",
     "ZT_S8_FRAG",          "ZT_S8_FORCE",        "ZT_S8_TILE",     "ZT_S8_KIND",
-    "ZT_MOE_BN"};
+    "ZT_S8_SPLIT",         "ZT_MOE_BN"};
 
 // Values are interned copies that are never freed: a reader may hold an old
 // pointer while another thread replaces the value.
@@ -425,9 +425,28 @@ static size_t dyn_qx_bytes(int64_t M, int64_t K) {
   return ((size_t)((M + 31) / 32 * 32) * (size_t)K + 255) & ~(size_t)255;
 }
 
-size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K) {
+// Bytes of qx, the row scales and (asym) the row offsets, rounded to 256:
+// the least workspace a dynamic or static qlinear call takes.  The split-K
+// exchange of the skinny int8 GEMM (zt::s8_split_bytes) follows it; a call
+// whose workspace has no room for it runs the unsplit kernel.
+static size_t dyn_base_bytes(int64_t M, int64_t K, bool asym) {
+  return (dyn_qx_bytes(M, K) + (size_t)M * 4 * (asym ? 2 : 1) + 255) & ~(size_t)255;
+}
+
+size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K, int64_t N) {
   if (M <= 0 || K <= 0) return 0;
-  return dyn_qx_bytes(M, K) + (size_t)M * sizeof(float);
+  return dyn_base_bytes(M, K, false) + zt::s8_split_bytes(M, K, N);
+}
+
+// Points a at the split-K exchange when the workspace holds it; returns the
+// tile-counter count the quantise kernel must clear (0: no split).
+static int attach_split(zt::DynArgs &a, char *ws, size_t ws_bytes, size_t base) {
+  const size_t sb = zt::s8_split_bytes(a.M, a.K, a.N);
+  if (!sb || ws_bytes < base + sb) return 0;
+  const int nc = zt::s8_split_counters(a.N);
+  a.split_part = reinterpret_cast<int32_t *>(ws + base);
+  a.split_cnt = reinterpret_cast<int32_t *>(ws + base + sb - (((size_t)nc * 4 + 255) & ~(size_t)255));
+  return nc;
 }
 
 int zt_dynamic_quantize(const void *x, int32_t x_dtype, int64_t M, int64_t K,
@@ -476,8 +495,7 @@ static int dynamic_qlinear_common(const char *op, const void *x, int32_t x_dtype
   if (!x || !w || !w_scales || !y) return fail(ZT_EINVAL, "%s: null pointer", op);
   if (asym && (reinterpret_cast<uintptr_t>(colsum) & 15u))
     return fail(ZT_EINVAL, "%s: weight_colsum must be 16-byte aligned", op);
-  const size_t need = asym ? zt_dynamic_qlinear_asym_workspace_size(M, K)
-                           : zt_dynamic_qlinear_workspace_size(M, K);
+  const size_t need = dyn_base_bytes(M, K, asym);
   if (!workspace || workspace_bytes < need)
     return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op,
                 need, workspace ? workspace_bytes : (size_t)0);
@@ -494,8 +512,11 @@ static int dynamic_qlinear_common(const char *op, const void *x, int32_t x_dtype
   int32_t *azp = asym ? reinterpret_cast<int32_t *>(ws + dyn_qx_bytes(M, K) + M * 4) : nullptr;
   a.qx = qx, a.sx = sx, a.azp = azp, a.colsum = colsum;
   a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
+  const int nc = a.qx_frag ? attach_split(a, ws, workspace_bytes, need) : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s, azp), op);
+  rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s, azp,
+                                          a.split_cnt, nc),
+                  op);
   if (rc) return rc;
   return hip_status(zt::launch_s8_gemm(a, s), op);
 }
@@ -511,8 +532,8 @@ int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                                 workspace, workspace_bytes, stream);
 }
 
-size_t zt_qlinear_workspace_size(int64_t M, int64_t K) {
-  return zt_dynamic_qlinear_asym_workspace_size(M, K);
+size_t zt_qlinear_workspace_size(int64_t M, int64_t K, int64_t N) {
+  return zt_dynamic_qlinear_asym_workspace_size(M, K, N);
 }
 
 int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float *x_scale,
@@ -548,7 +569,7 @@ int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float
                 op);
   if (offset && (reinterpret_cast<uintptr_t>(w_colsum) & 15u))
     return fail(ZT_EINVAL, "%s: weight_colsum must be 16-byte aligned", op);
-  const size_t need = zt_qlinear_workspace_size(M, K);
+  const size_t need = dyn_base_bytes(M, K, true);
   if (!workspace || workspace_bytes < need)
     return fail(ZT_EINVAL, "%s: workspace of %zu bytes needed, %zu given", op, need,
                 workspace ? workspace_bytes : (size_t)0);
@@ -565,17 +586,18 @@ int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float
   int32_t *azp = offset ? reinterpret_cast<int32_t *>(ws + dyn_qx_bytes(M, K) + M * 4) : nullptr;
   a.qx = qx, a.sx = sx, a.azp = azp, a.colsum = offset ? w_colsum : nullptr;
   a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
+  const int nc = a.qx_frag ? attach_split(a, ws, workspace_bytes, need) : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   rc = hip_status(zt::launch_static_quantize(x, x_dtype, M, K, qx, a.qx_frag != 0, x_scale,
-                                             x_zero_point, sx, azp, s),
+                                             x_zero_point, sx, azp, s, a.split_cnt, nc),
                   op);
   if (rc) return rc;
   return hip_status(zt::launch_s8_gemm(a, s), op);
 }
 
-size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K) {
+size_t zt_dynamic_qlinear_asym_workspace_size(int64_t M, int64_t K, int64_t N) {
   if (M <= 0 || K <= 0) return 0;
-  return dyn_qx_bytes(M, K) + (size_t)M * (sizeof(float) + sizeof(int32_t));
+  return dyn_base_bytes(M, K, true) + zt::s8_split_bytes(M, K, N);
 }
 
 int zt_dynamic_quantize_asym(const void *x, int32_t x_dtype, int64_t M, int64_t K,
@@ -662,7 +684,7 @@ int zt_dynamic_qlinear_scratch(const void *x, int32_t x_dtype, int64_t M, int64_
   static const char *op = "zt_dynamic_qlinear_scratch";
   if (M < 0 || N < 0 || K < 1) return fail(ZT_EINVAL, "%s: bad sizes", op);
   if (M == 0 || N == 0) return ZT_OK;
-  const size_t need = zt_dynamic_qlinear_workspace_size(M, K);
+  const size_t need = dyn_base_bytes(M, K, false);
   if (need > (size_t)ZT_DYN_SCRATCH_BYTES)
     return fail(ZT_EINVAL, "%s: M=%lld x K=%lld needs %zu bytes of scratch, more than the "
                 "%zu this entry point holds (use zt_dynamic_qlinear with a workspace)",

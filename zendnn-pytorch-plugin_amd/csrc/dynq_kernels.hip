@@ -79,12 +79,21 @@ __device__ __forceinline__ void block_minmax(float &lo, float &hi, float *red, i
   hi = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
 }
 
+// The quantise kernels also clear the tile counters of the split-K GEMM that
+// follows them on the stream (workgroup 0, 256 threads).
+__device__ __forceinline__ void zero_counters(int32_t *zero, int nzero, int tid) {
+  if (blockIdx.x == 0)
+    for (int i = tid; i < nzero; i += 256) zero[i] = 0;
+}
+
 template <bool ASYM>
 __global__ __launch_bounds__(256) void dyn_quantize_kernel(
-    const void *x, int x_dt, int64_t K, int8_t *qx, float *sx, int frag, int32_t *azp) {
+    const void *x, int x_dt, int64_t K, int8_t *qx, float *sx, int frag, int32_t *azp,
+    int32_t *zero, int nzero) {
   __shared__ float red[8];
   const int tid = threadIdx.x;
   const int64_t m = blockIdx.x;
+  zero_counters(zero, nzero, tid);
   const int64_t base = m * K;
   float lo = 0.f, hi = 0.f;
   for (int64_t k = tid; k < K; k += 256) {
@@ -116,10 +125,12 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(
 template <int VPT, bool FRAG, bool ASYM>
 __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *x, int64_t K,
                                                                  int8_t *qx, float *sx,
-                                                                 int32_t *azp) {
+                                                                 int32_t *azp, int32_t *zero,
+                                                                 int nzero) {
   __shared__ float red[8];
   const int tid = threadIdx.x;
   const int64_t m = blockIdx.x;
+  zero_counters(zero, nzero, tid);
   const u32x4_t *row = reinterpret_cast<const u32x4_t *>(x + m * K);
   const int nv = (int)(K / 8);
   u32x4_t v[VPT];
@@ -175,9 +186,10 @@ __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *
 // zp = 0 when absent).  sx[m] = scale; azp[m] = the offset, when azp is set.
 __global__ __launch_bounds__(256) void static_quantize_kernel(
     const void *x, int x_dt, int64_t K, int8_t *qx, int frag, const float *scale,
-    const int32_t *zp, float *sx, int32_t *azp) {
+    const int32_t *zp, float *sx, int32_t *azp, int32_t *zero, int nzero) {
   const int tid = threadIdx.x;
   const int64_t m = blockIdx.x, base = m * K;
+  zero_counters(zero, nzero, tid);
   const float s = *scale;
   const int32_t z = zp ? *zp : 0;
   const bool u8 = x_dt == ZT_DT_U8 || ((x_dt == ZT_DT_F32 || x_dt == ZT_DT_BF16) && zp);
@@ -1071,66 +1083,93 @@ constexpr size_t s8_skinny_lds() {
 // Sum of the four K-partial slabs [4][ROWS][16*TPW + pad] int32 and the
 // dequantising epilogue, for the skinny kernels (ROWS tokens, TPW 16-row
 // weight tiles from n0, 64*NW threads).
+// Epilogue of a ROWS x COLS int32 tile (rows 0.., columns n0..) over NT
+// threads.  Thread t < T = RP * Q (Q = COLS / 4 column quads, RP = NT / Q
+// rows per pass) keeps quad t % Q for rows t / Q + k RP, so its weight
+// scales, bias and column sums and its rows' scales and offsets are loaded
+// once, by prefetch(), which the kernels call before their final reductions
+// so that those loads are in flight meanwhile.  Same arithmetic as
+// dyn_epilogue4; post-ops, requantised or int32 outputs and a row length
+// that is not a multiple of 4 take dyn_epilogue4 itself.
+template <int ROWS, int COLS, int NT>
+struct QuadEpi {
+  static constexpr int Q = COLS / 4, RP = NT / Q, T = RP * Q, KR = (ROWS + RP - 1) / RP;
+  bool fast;
+  int c4, r0;
+  float sw[4], b[4], sx[KR];
+  int32_t cs[4], az[KR];
+
+  __device__ __forceinline__ void prefetch(const DynArgs &a, int n0, int tid) {
+    const int M = (int)a.M, N = (int)a.N;
+    fast = (a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32) && a.post.count == 0 && (N & 3) == 0;
+    c4 = (tid % Q) * 4;
+    r0 = tid / Q;
+    if (!fast || tid >= T || n0 + c4 >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sw[r] = wscale(a, n0 + c4 + r);
+      b[r] = a.bias ? load_elem(a.bias, a.b_dt, n0 + c4 + r) : 0.f;
+      cs[r] = a.azp ? a.colsum[n0 + c4 + r] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+      const int m = r0 + k * RP;
+      sx[k] = m < M && m < ROWS ? a.sx[m] : 0.f;
+      az[k] = a.azp && m < M && m < ROWS ? a.azp[m] : 0;
+    }
+  }
+
+  // v(m, c) returns the int32 sums of row m, columns c .. c + 3
+  template <typename V>
+  __device__ __forceinline__ void finish(const DynArgs &a, int n0, int tid, V v) {
+    const int M = (int)a.M, N = (int)a.N;
+    if (!fast) {
+      for (int idx = tid; idx < ROWS * Q; idx += NT) {
+        const int m = idx / Q, c = (idx % Q) * 4;
+        if (m < M && n0 + c < N) dyn_epilogue4(a, m, n0 + c, v(m, c));
+      }
+      return;
+    }
+    const int n = n0 + c4;
+    if (tid >= T || n >= N) return;
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+      const int m = r0 + k * RP;
+      if (m >= M || m >= ROWS) break;
+      i32x4_t s = v(m, c4);
+      if (a.azp) s -= i32x4_t{cs[0], cs[1], cs[2], cs[3]} * az[k];
+      float f[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = (float)s[r] * sx[k];
+        t = t * sw[r];
+        f[r] = a.bias ? t + b[r] : t;
+      }
+      if (a.y_dt == ZT_DT_BF16) {
+        u32x2_t pk;
+        pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
+        pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+        *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
+      } else {
+        *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
+            f32x4_t{f[0], f[1], f[2], f[3]};
+      }
+    }
+  }
+};
+
+// Epilogue of the skinny kernels: the four K-partial slabs [4][ROWS][P] are
+// added and finished by ep (prefetched by the kernel).
 template <int ROWS, int TPW, int NW>
 __device__ __forceinline__ void skinny_epilogue(const DynArgs &a, const int32_t *slab, int n0,
-                                                int tid) {
-  const int M = (int)a.M, N = (int)a.N;
+                                                int tid, QuadEpi<ROWS, 16 * TPW, 64 * NW> &ep) {
   constexpr int P = 16 * TPW + kSkPitchPad;
-  // 4*TPW four-column groups divide the 64*NW threads: a thread keeps its
-  // columns, so their weight scales and bias are loaded once
-  constexpr int G4 = 4 * TPW;
-  if ((64 * NW) % G4 != 0) {  // groups do not divide the threads: general loop
-    for (int idx = tid; idx < ROWS * G4; idx += 64 * NW) {
-      const int m = idx / G4, cc = (idx % G4) * 4;
-      if (m >= M || n0 + cc >= N) continue;
-      i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + cc);
+  ep.finish(a, n0, tid, [&](int m, int c) {
+    i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + c);
 #pragma unroll
-      for (int w = 1; w < 4; ++w)
-        v += *reinterpret_cast<const i32x4_t *>(slab + (w * ROWS + m) * P + cc);
-      dyn_epilogue4(a, m, n0 + cc, v);
-    }
-    return;
-  }
-  const int c4 = (tid % G4) * 4, n = n0 + c4;
-  if (n >= N) return;
-  const bool fast =
-      (a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32) && a.post.count == 0 && (N & 3) == 0;
-  float sw[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
-  if (fast) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sw[r] = wscale(a, n + r);
-      if (a.bias) b[r] = load_elem(a.bias, a.b_dt, n + r);
-    }
-  }
-  for (int m = tid / G4; m < M && m < ROWS; m += (64 * NW) / G4) {
-    i32x4_t v = *reinterpret_cast<const i32x4_t *>(slab + m * P + c4);
-#pragma unroll
-    for (int w = 1; w < 4; ++w)
-      v += *reinterpret_cast<const i32x4_t *>(slab + (w * ROWS + m) * P + c4);
-    if (!fast) {
-      dyn_epilogue4(a, m, n, v);
-      continue;
-    }
-    if (a.azp) v = asym_fix4(a, m, n, v);
-    const float sxm = a.sx[m];
-    float f[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float t = (float)v[r] * sxm;
-      t = t * sw[r];
-      f[r] = a.bias ? t + b[r] : t;
-    }
-    if (a.y_dt == ZT_DT_BF16) {
-      u32x2_t pk;
-      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
-      *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
-    } else {
-      *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
-          f32x4_t{f[0], f[1], f[2], f[3]};
-    }
-  }
+    for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const i32x4_t *>(slab + (w * ROWS + m) * P + c);
+    return v;
+  });
 }
 
 template <int MT, int TPW, int PF, int NW>
@@ -1185,6 +1224,9 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunk
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[t][j] = i32x4_t{0, 0, 0, 0};
 
+  // the epilogue's per-column and per-row values, in flight with the chunks
+  QuadEpi<16 * MT, 16 * TPW, 64 * NW> ep;
+  ep.prefetch(a, n0, tid);
 #pragma unroll
   for (int p = 0; p < PF; ++p) load(p, p);
   for (int c = 0; c < nch; c += PF) {
@@ -1224,7 +1266,7 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunk
       }
   }
   __syncthreads();
-  skinny_epilogue<16 * MT, TPW, NW>(a, slab, n0, tid);
+  skinny_epilogue<16 * MT, TPW, NW>(a, slab, n0, tid, ep);
 }
 
 // The skinny GEMM on v_mfma_i32_32x32x32_i8 (twice the int8 rate of the
@@ -1293,6 +1335,9 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny32_kernel(DynArgs a, int chu
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[g][j][r] = 0;
 
+  // the epilogue's per-column and per-row values, in flight with the chunks
+  QuadEpi<32 * MT, 16 * TPW, 64 * NW> ep;
+  ep.prefetch(a, n0, tid);
 #pragma unroll
   for (int p = 0; p < PF; ++p) load(p, p);
   for (int c = 0; c < nch; c += PF) {
@@ -1343,7 +1388,7 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny32_kernel(DynArgs a, int chu
   if (NW == 8) __syncthreads();
   if (wv < 4) put(wv, NW == 8);
   __syncthreads();
-  skinny_epilogue<ROWS, TPW, NW>(a, slab, n0, tid);
+  skinny_epilogue<ROWS, TPW, NW>(a, slab, n0, tid, ep);
 }
 
 template <int MT, int TPW, int PF, int NW>
@@ -1369,6 +1414,248 @@ hipError_t launch_s8_skinny32(const DynArgs &a, hipStream_t s) {
   ZT_SK(4, 3, 4, 4) ZT_SK(4, 4, 4, 4)
 #undef ZT_SK
   return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------- split-K skinny
+// Skinny int8 GEMM for 64 < M <= 128 tokens with K split in two halves
+// across workgroups (qx in fragment order, K % 256 == 0).  The
+// weight-streaming kernels above give each workgroup all of K, so every CU
+// pulls the whole of qx through its vector memory path (at M = 128, 2.7 x
+// the weight bytes it streams); here a CU pulls half of it.
+//
+// Workgroup (tile, half) takes 96 weight rows (three 32-row groups) over K
+// half `half`; its eight waves are (token tile j = w % 4, chunk parity
+// h = w / 4).  A step covers two 128-k chunks, one per parity:
+//  * the weight slab [2][96][128 B] moves into LDS by DMA, three 1 KB
+//    instructions per wave, each eight whole 128-byte rows (the 16-byte
+//    blocks of row r are XOR-swizzled by (r >> 1) & 7, so the 32-row
+//    fragment reads hit each bank once);
+//  * a wave loads the qx fragments of its token tile and chunk straight to
+//    registers;
+//  * a wave runs 12 v_mfma_i32_32x32x32_i8 (3 row groups x 4 32-k steps):
+//    W is A (row 32g + l%32, k block f + 2 (l/32) of each 64-k half, the
+//    blocks qx fragment f pairs with), qx is B.
+// PD steps of loads are in flight (PD + 1 LDS stages, one barrier a step;
+// steps past the half read zeros).  The two parities meet in LDS.  Both
+// halves of a tile write their int32 partial tile to the workspace; the
+// second workgroup of the tile to finish (a per-tile counter) adds the
+// other half's partial and runs the epilogue.  The partials are written and
+// read with device-scope (sc1) accesses, the memory instructions of relaxed
+// device-scope atomic stores and loads, and the writer waits for its stores
+// to complete before the counter's atomic add: the exchange needs neither an
+// L2 writeback nor an invalidate (a release / acquire fence pair makes every
+// workgroup write back its XCD's whole dirty L2).  The sums are integers, so the result does not depend on which
+// half finishes last.  Workgroups b and b + 8 of every 16 are the two
+// halves of one tile (the same XCD under round-robin dispatch).
+constexpr int kSpBN = 96;                 // weight rows per workgroup
+constexpr int kSpChunk = kSpBN * 128;     // LDS bytes of one 128-k weight chunk
+constexpr int kSpStep = 2 * kSpChunk;     // one chunk per parity
+constexpr int kSpPart = 128 * kSpBN;      // int32 partials of a workgroup
+constexpr int kSpTileP = kSpBN + 4;       // row pitch of the staged output tile
+constexpr int kSpSlabB = 4 * 48 * 64 * 4;  // the parity-1 waves' accumulators
+constexpr int kSpFlagOff = kSpSlabB + 128 * kSpTileP * 4;
+constexpr int kSc1 = 16;  // cache-policy bit of device-scope accesses (sc1)
+
+template <int PD>
+constexpr size_t s8_splitk_lds() {
+  const size_t stages = (size_t)(PD + 1) * kSpStep;
+  const size_t tail = (size_t)kSpFlagOff + 16;
+  return stages > tail ? stages : tail;
+}
+
+template <int PD>
+__global__ __launch_bounds__(512) void s8_splitk_kernel(DynArgs a, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+  constexpr int NS = PD + 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x;
+  const int tile = (b >> 4) * 8 + (b & 7), half = (b >> 3) & 1;
+  if (tile >= tiles_n) return;  // the grid is a whole number of 16-blocks
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int n0 = tile * kSpBN;
+  const int tiles_m = (M + 31) >> 5;
+  const int nch = K >> 8;  // 128-k chunks per half
+  const int kc0 = half * nch;
+  const int nsteps = (((nch + 1) >> 1) + PD - 1) / PD * PD;
+  const int j = wv & 3, h = wv >> 2;
+  const auto q_rs = make_rsrc(a.qx, (uint32_t)(tiles_m * 32 * K));
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+
+  // DMA instruction 3 wv + u of a step: rows 8 (q % 12) .. + 7 of chunk
+  // parity q / 12 (= h); lane l takes 16-byte block (l % 8) ^ swz of row
+  // 8 (q % 12) + l / 8 (N * K < 2^31, host-checked)
+  uint32_t w_src[3];
+  int w_dst[3];
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int rb = (3 * wv + u) % 12;
+    const int lr = 8 * rb + (lane >> 3), n = n0 + lr;
+    const int blk = (lane & 7) ^ ((lr >> 1) & 7);
+    w_src[u] = n < N ? (uint32_t)(n * K + blk * 16) : kOobOffset;
+    w_dst[u] = h * kSpChunk + rb * 1024;
+  }
+  auto dma = [&](int st) {
+    int8_t *stage = s8_smem + (st % NS) * kSpStep;
+    const int c = 2 * st + h;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const uint32_t off = (w_src[u] == kOobOffset || c >= nch)
+                               ? kOobOffset : w_src[u] + (uint32_t)((kc0 + c) * 128);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (lds_ptr_t)(stage + w_dst[u]), 16, off, 0, 0,
+                                               0);
+    }
+  };
+  // qx fragment (tile j, 64-k chunk c64, f) at ((j (K/64) + c64) 2 + f) KB
+  const uint32_t q_base = j < tiles_m ? (uint32_t)(j * (K >> 6) * 2048) + 16u * lane : kOobOffset;
+  i32x4_t qf[PD][2][2];
+  auto ldq = [&](int st, int slot) {
+    const int c = 2 * st + h;
+    const bool in = q_base != kOobOffset && c < nch;
+    const uint32_t base = in ? q_base + (uint32_t)((kc0 + c) * 4096) : 0u;
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        qf[slot][e][f] = __builtin_bit_cast(
+            i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         q_rs, in ? base + (uint32_t)(e * 2048 + f * 1024) : kOobOffset, 0, 0));
+  };
+
+  i32x16_t acc[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[g][r] = 0;
+  const int swz = ((lane & 31) >> 1) & 7;
+  const int a_row = (lane & 31) * 128;
+  auto compute = [&](int st, int slot) {
+    const int8_t *stage = s8_smem + (st % NS) * kSpStep + h * kSpChunk + a_row;
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int pos = ((4 * e + f + 2 * (lane >> 5)) ^ swz) << 4;
+        i32x4_t wa[3];
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+          wa[g] = *reinterpret_cast<const i32x4_t *>(stage + g * 32 * 128 + pos);
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+          acc[g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[g], qf[slot][e][f], acc[g], 0, 0, 0);
+      }
+  };
+
+  // the epilogue's per-column and per-row values, loaded first: a step's
+  // wait below then counts only the loads issued after its own
+  QuadEpi<128, kSpBN, 512> ep;
+  ep.prefetch(a, n0, tid);
+#pragma unroll
+  for (int p = 0; p < PD; ++p) {
+    dma(p);
+    ldq(p, p);
+  }
+  for (int st0 = 0; st0 < nsteps; st0 += PD) {
+#pragma unroll
+    for (int p = 0; p < PD; ++p) {
+      const int st = st0 + p;
+      // this step's 3 DMA + 4 qx loads are the oldest of the PD steps in flight
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait_imm(7 * (PD - 1)));
+      asm volatile("s_barrier" ::: "memory");
+      dma(st + PD);  // into the stage of step st - 1, which every wave has finished
+      compute(st, p);
+      ldq(st + PD, p);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_wait_imm(0));  // the zero-filling DMA past the end
+  __syncthreads();
+
+  // the parities meet: slab[j][g][r][lane]
+  int32_t *slab = reinterpret_cast<int32_t *>(s8_smem);
+  if (h == 1) {
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) slab[((j * 3 + g) * 16 + r) * 64 + lane] = acc[g][r];
+  }
+  __syncthreads();
+  if (h == 0) {
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[g][r] += slab[((j * 3 + g) * 16 + r) * 64 + lane];
+    const auto mine = make_rsrc(a.split_part + ((size_t)tile * 2 + half) * kSpPart, kSpPart * 4);
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4_t{(uint32_t)acc[g][4 * q], (uint32_t)acc[g][4 * q + 1],
+                    (uint32_t)acc[g][4 * q + 2], (uint32_t)acc[g][4 * q + 3]},
+            mine, (uint32_t)((((j * 3 + g) * 4 + q) * 64 + lane) * 16), 0, kSc1);
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait_imm(0));  // the partial is at device scope
+  }
+  // count the halves done; the first to finish leaves
+  __syncthreads();
+  int32_t *flag = reinterpret_cast<int32_t *>(s8_smem + kSpFlagOff);
+  if (tid == 0) *flag = atomicAdd(a.split_cnt + tile, 1);
+  __syncthreads();
+  if (*flag == 0) return;
+  int32_t *tl = reinterpret_cast<int32_t *>(s8_smem + kSpSlabB);
+  if (h == 0) {
+    const auto other =
+        make_rsrc(a.split_part + ((size_t)tile * 2 + (half ^ 1)) * kSpPart, kSpPart * 4);
+    // D[n][m]: register r of lane l holds row 32g + 8 (r/4) + 4 (l/32) + r%4
+    // of the tile and token 32 j + l%32
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const i32x4_t o = __builtin_bit_cast(
+            i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         other, (uint32_t)((((j * 3 + g) * 4 + q) * 64 + lane) * 16), 0, kSc1));
+        *reinterpret_cast<i32x4_t *>(tl + (32 * j + (lane & 31)) * kSpTileP + 32 * g + 8 * q +
+                                     4 * (lane >> 5)) =
+            i32x4_t{acc[g][4 * q] + o[0], acc[g][4 * q + 1] + o[1], acc[g][4 * q + 2] + o[2],
+                    acc[g][4 * q + 3] + o[3]};
+      }
+  }
+  __syncthreads();
+  ep.finish(a, n0, tid, [&](int m, int c) {
+    return *reinterpret_cast<const i32x4_t *>(tl + m * kSpTileP + c);
+  });
+}
+
+template <int PD>
+hipError_t launch_s8_splitk_t(const DynArgs &a, hipStream_t s) {
+  const int tiles_n = s8_split_counters(a.N);
+  const unsigned blocks = (unsigned)((tiles_n + 7) / 8 * 16);
+  s8_splitk_kernel<PD><<<dim3(blocks), dim3(512), s8_splitk_lds<PD>(), s>>>(a, tiles_n);
+  return hipGetLastError();
+}
+
+bool s8_split_shape(int64_t M, int64_t K, int64_t N) {
+  const int64_t rows = (M + 31) / 32 * 32;
+  return M > 64 && M <= 128 && K % 256 == 0 && N > 0 && N * K < (int64_t)kOobOffset &&
+         rows * K < (int64_t)kOobOffset;
+}
+
+bool s8_split_ok(const DynArgs &a) {
+  const char *e = knob(kKnobS8Split);
+  if (e && e[0] == '0') return false;
+  return a.qx_frag && a.split_part && a.split_cnt && s8_split_shape(a.M, a.K, a.N) &&
+         ((reinterpret_cast<uintptr_t>(a.split_part) | reinterpret_cast<uintptr_t>(a.w) |
+           reinterpret_cast<uintptr_t>(a.qx)) & 15u) == 0;
+}
+
+hipError_t launch_s8_splitk(const DynArgs &a, hipStream_t s) {
+  // "2" .. "4": steps of loads in flight (2 measured fastest at M = 128,
+  // N = 11008, K = 4096: 19.6 us against 20.8 for 3)
+  const char *e = knob(kKnobS8Split);
+  const int pd = e && e[0] >= '2' && e[0] <= '4' ? e[0] - '0' : 2;
+  if (pd == 3) return launch_s8_splitk_t<3>(a, s);
+  if (pd == 4) return launch_s8_splitk_t<4>(a, s);
+  return launch_s8_splitk_t<2>(a, s);
 }
 
 template <int MT, int TPW, int PF, int NW>
@@ -1410,7 +1697,7 @@ hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
 
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                                int8_t *qx, float *sx, bool frag, hipStream_t s,
-                               int32_t *azp) {
+                               int32_t *azp, int32_t *zero, int nzero) {
   if (M == 0) return hipSuccess;
   if (frag && K % 64 != 0) return hipErrorInvalidValue;
   const bool vec = x_dt == ZT_DT_BF16 && K % 8 == 0 &&
@@ -1422,30 +1709,32 @@ hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
 #define ZT_QB(V_)                                                                          \
   if (per <= V_) {                                                                         \
     if (azp)                                                                               \
-      frag ? dyn_quantize_bf16_kernel<V_, true, true><<<grid, block, 0, s>>>(xb, K, qx, sx, azp) \
-           : dyn_quantize_bf16_kernel<V_, false, true><<<grid, block, 0, s>>>(xb, K, qx, sx, azp); \
+      frag ? dyn_quantize_bf16_kernel<V_, true, true><<<grid, block, 0, s>>>(xb, K, qx, sx, azp, zero, nzero) \
+           : dyn_quantize_bf16_kernel<V_, false, true><<<grid, block, 0, s>>>(xb, K, qx, sx, azp, zero, nzero); \
     else                                                                                   \
-      frag ? dyn_quantize_bf16_kernel<V_, true, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp) \
-           : dyn_quantize_bf16_kernel<V_, false, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp); \
+      frag ? dyn_quantize_bf16_kernel<V_, true, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp, zero, nzero) \
+           : dyn_quantize_bf16_kernel<V_, false, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp, zero, nzero); \
     return hipGetLastError();                                                              \
   }
     ZT_QB(2) ZT_QB(4) ZT_QB(8)
 #undef ZT_QB
   }
   if (azp)
-    dyn_quantize_kernel<true><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp);
+    dyn_quantize_kernel<true><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp,
+                                                    zero, nzero);
   else
-    dyn_quantize_kernel<false><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp);
+    dyn_quantize_kernel<false><<<grid, block, 0, s>>>(x, x_dt, K, qx, sx, (int)frag, azp,
+                                                     zero, nzero);
   return hipGetLastError();
 }
 
 hipError_t launch_static_quantize(const void *x, int x_dt, int64_t M, int64_t K, int8_t *qx,
                                   bool frag, const float *scale, const int32_t *zp, float *sx,
-                                  int32_t *azp, hipStream_t s) {
+                                  int32_t *azp, hipStream_t s, int32_t *zero, int nzero) {
   if (M == 0) return hipSuccess;
   if (frag && K % 64 != 0) return hipErrorInvalidValue;
   static_quantize_kernel<<<dim3((unsigned)M), dim3(256), 0, s>>>(x, x_dt, K, qx, (int)frag, scale,
-                                                                 zp, sx, azp);
+                                                                 zp, sx, azp, zero, nzero);
   return hipGetLastError();
 }
 
@@ -1483,6 +1772,14 @@ hipError_t launch_s8_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *cols
   return hipGetLastError();
 }
 
+int s8_split_counters(int64_t N) { return (int)((N + kSpBN - 1) / kSpBN); }
+
+size_t s8_split_bytes(int64_t M, int64_t K, int64_t N) {
+  if (!s8_split_shape(M, K, N)) return 0;
+  const size_t tiles = (size_t)s8_split_counters(N);
+  return tiles * 2 * kSpPart * 4 + ((tiles * 4 + 255) & ~(size_t)255);
+}
+
 bool s8_frag_ok(const DynArgs &a) {
   // 17..128 tokens: the 32x32 kernel's tiles are at least half full there
   // (one 16-token tile is cheaper on the 16x16 kernel)
@@ -1496,7 +1793,10 @@ bool s8_frag_ok(const DynArgs &a) {
 
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
-  if (a.qx_frag) return s8_frag_ok(a) ? launch_s8_skinny32(a, s) : hipErrorInvalidValue;
+  if (a.qx_frag) {
+    if (!s8_frag_ok(a)) return hipErrorInvalidValue;
+    return s8_split_ok(a) ? launch_s8_splitk(a, s) : launch_s8_skinny32(a, s);
+  }
   const bool aligned = ((reinterpret_cast<uintptr_t>(a.qx) |
                          reinterpret_cast<uintptr_t>(a.w)) & 15u) == 0;
   if (a.K % 16 != 0 || !aligned) {

@@ -470,14 +470,14 @@ at::Tensor dynamic_qlinear_impl(const at::Tensor &input, const at::Tensor &weigh
   const zt_stream_t st = reinterpret_cast<zt_stream_t>(current_stream());
   int rc;
   if (cs.defined()) {
-    const size_t ws_bytes = zt_dynamic_qlinear_asym_workspace_size(M, K);
+    const size_t ws_bytes = zt_dynamic_qlinear_asym_workspace_size(M, K, N);
     const at::Tensor ws = call_workspace(input, ws_bytes);
     rc = zt_dynamic_qlinear_asym(x2.data_ptr(), zt_dtype_of(x2), M, K, wp, N, sc.data_ptr(),
                                  zt_dtype_of(sc), cs.data_ptr<int32_t>(), bp, bdt,
                                  post.count ? &post : nullptr, result.data_ptr(),
                                  zt_dtype_of(result), ws.data_ptr(), ws_bytes, st);
   } else {
-    const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K);
+    const size_t ws_bytes = zt_dynamic_qlinear_workspace_size(M, K, N);
     const at::Tensor ws = call_workspace(input, ws_bytes);
     rc = zt_dynamic_qlinear(x2.data_ptr(), zt_dtype_of(x2), M, K, wp, N, sc.data_ptr(),
                             zt_dtype_of(sc), bp, bdt, post.count ? &post : nullptr,
@@ -710,7 +710,7 @@ void qlinear_into(at::Tensor &result, const at::Tensor &input, const at::Tensor 
   }
   // the result may be a strided .out tensor: compute into a contiguous one
   at::Tensor y = result.is_contiguous() ? result : at::empty_like(result, at::MemoryFormat::Contiguous);
-  const size_t ws_bytes = zt_qlinear_workspace_size(M, K);
+  const size_t ws_bytes = zt_qlinear_workspace_size(M, K, N);
   const at::Tensor ws = call_workspace(input, ws_bytes);
   const int rc = zt_qlinear(
       x2.data_ptr(), zt_dtype_of(x2), M, K, sx.data_ptr<float>(),

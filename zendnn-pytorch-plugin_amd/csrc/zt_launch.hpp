@@ -104,25 +104,37 @@ struct DynArgs {
   // + *out_zp) (out_zp null = 0)
   const float *out_scale;
   const int32_t *out_zp;
+  // split-K exchange of s8_splitk_kernel (both null: not used): int32
+  // partials of both K halves of every tile, then one counter per tile that
+  // the quantise kernel of the same call clears
+  int32_t *split_part;
+  int32_t *split_cnt;
 };
 
 // frag: write qx in the fragment order (K % 64 == 0; the buffer holds
 // ceil(M / 32) * 32 rows)
 // azp non-null: per-token asymmetric uint8 (qx = q_u8 - 128, azp = zp - 128)
+// zero[0, nzero): the split-K tile counters, cleared by the same launch
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                                int8_t *qx, float *sx, bool frag, hipStream_t s,
-                               int32_t *azp = nullptr);
+                               int32_t *azp = nullptr, int32_t *zero = nullptr, int nzero = 0);
 // Static per-tensor quantisation of zentorch_qlinear's activations into qx
 // (fragment order when frag), with sx[m] = *scale and, when azp is set,
 // azp[m] = the offset o with q - zp = qx - o (see static_quantize_kernel).
 hipError_t launch_static_quantize(const void *x, int x_dt, int64_t M, int64_t K, int8_t *qx,
                                   bool frag, const float *scale, const int32_t *zp, float *sx,
-                                  int32_t *azp, hipStream_t s);
+                                  int32_t *azp, hipStream_t s, int32_t *zero = nullptr,
+                                  int nzero = 0);
 // colsum[n] = sum_k w[n][k] of an int8 [N, K] weight
 hipError_t launch_s8_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *colsum,
                             hipStream_t s);
 // whether launch_s8_gemm takes qx in fragment order for this call (a.qx set)
 bool s8_frag_ok(const DynArgs &a);
+// Workspace bytes of the split-K exchange for an [M, K] x [N, K] call whose
+// shape s8_splitk_kernel takes (0 otherwise), and its tile-counter count;
+// the counters follow split_bytes - 4 * counters bytes of partials.
+size_t s8_split_bytes(int64_t M, int64_t K, int64_t N);
+int s8_split_counters(int64_t N);
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);
 
 // Grouped int4 MoE (moe_kernels.hip).  Device scratch of one call.
