@@ -8,18 +8,26 @@
 // (test/unittests/op_tests/test_woq_linear.py:118-128) and that its 1e-3
 // tolerance pins; an exact sum_g s_g sum_k x q fails that test.
 //
-//  * woq_decode_kernel  M <= 32: the decode GEMV / skinny GEMM.  Packed int4
-//    weights stream from HBM in 16-byte loads straight into the registers
-//    that are the MFMA A operands; the activations stay in registers for
-//    every row tile a wave visits.  Waves split K inside a workgroup
-//    (reduced through LDS); long K is split across workgroups too, and the
-//    last workgroup of a row block reduces the fp32 partials and runs the
-//    epilogue.
-//  * woq_gemm_kernel    M > 32: tiled bf16 MFMA GEMM; weight tiles are
-//    dequantised into LDS.
-//  * woq_generic_kernel any shape/dtype the two above do not take (fp32
-//    activations, K not a multiple of 64, odd group sizes): one wave per
-//    output element.
+// Kernels, in the order zt_woq_linear (capi.hip) tries them:
+//  * woq_wide_kernel     17..64 rows with large N * K: row tiles of 32 or 64
+//    tokens, K split over workgroups (fp32 partials in the workspace,
+//    woq_splitk_reduce_kernel adds them in split order).
+//  * woq_wave_kernel / woq_stream_kernel  1..16 rows (and up to 64 on
+//    smaller weights): the decode GEMV / skinny GEMM.  Packed int4 weights
+//    stream from HBM in 16-byte loads straight into the registers that are
+//    the MFMA A operands; x sits in LDS; the waves split K and their partials
+//    meet in LDS.  The wave kernel gives every wave its own x slice and no
+//    barrier before the reduction; the stream kernel shares one x copy.
+//    Rows past what one launch holds go in blocks of 16.
+//  * woq_decode_kernel   the older decode kernel for shapes the two above do
+//    not take (long K split over workgroups, general dequant modes).
+//  * woq_gemm32_kernel / woq_gemm_dma_kernel  prefill (more rows): LDS tiles
+//    moved by DMA, int4 dequantised in registers after the LDS read, bf16
+//    MFMA (32x32x16 for signed int4 with bf16 scales, 16x16x32 for the
+//    other modes); woq_gemm_kernel for group sizes that are not multiples
+//    of 128.
+//  * woq_generic_kernel  what none of the above takes (K not a multiple of
+//    64, odd group sizes): one wave per output element.
 //
 // Weight layout: [N, K/8] int32, nibble i of word (n, c) is element
 // (n, 8c+i) -- the storage of the [K/8, N] view zentorch_woq_linear takes
