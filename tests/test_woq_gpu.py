@@ -427,3 +427,44 @@ def test_wave_kernel_gate_up(M, K, I, G, knobs):
     knobs.set("ZT_WOQ_WAVE", "0")
     y_stream, _ = run_gate_up(M, K, I, G, seed=M + I)
     check_close(y, y_stream.cpu())
+
+
+# the persistent decode kernel (fast mode, M <= 16, K = 8 or 16 waves x
+# CPW chunks; forced by ZT_WOQ_PERSIST: "1" 8 waves, "2" 16 waves): every
+# workgroup loops over row units with the next units' weights in flight;
+# units past N (ragged last unit), more units than workgroups, group sizes
+# and per channel, bias and post-ops, and the merged gate_up
+@pytest.mark.parametrize("variant", ["1", "2"])
+@pytest.mark.parametrize("M", [1, 4, 9, 16])
+@pytest.mark.parametrize("K,N,G", [(2048, 16, 16), (4096, 4096, 32), (4096, 12304, 32),
+                                   (2048, 9000, 1), (4096, 496, 16)])
+def test_persist_kernel_vs_oracle(variant, M, K, N, G, knobs):
+    knobs.set("ZT_WOQ_PERSIST", variant)
+    y, y_ref = run_case(M, K, N, G, seed=M * 5 + N + G)
+
+
+@pytest.mark.parametrize("post,nbuf", [(("relu",), 0), (("add",), 1), (("mul", "add"), 2)])
+def test_persist_kernel_post_ops(post, nbuf, knobs):
+    knobs.set("ZT_WOQ_PERSIST", "1")
+    run_case(8, 4096, 8200, 32, post=post, nbuf=nbuf, seed=6, bias=True)
+
+
+# None: the library's choice, the persistent kernel from 9 rows
+@pytest.mark.parametrize("variant", ["1", "2", None])
+@pytest.mark.parametrize("M", [1, 5, 12, 16])
+@pytest.mark.parametrize("K,I,G", [(4096, 256, 32), (2048, 4112, 1), (4096, 14336, 32)])
+def test_persist_kernel_gate_up(variant, M, K, I, G, knobs):
+    if variant:
+        knobs.set("ZT_WOQ_PERSIST", variant)
+    run_gate_up(M, K, I, G, seed=M + I + 1)
+
+
+def test_persist_kernel_gate_up_strided_x():
+    M, K, I, G = 12, 4096, 1040, 32
+    x, q, wp, s, z, b = make_case(M, K, 2 * I, G, seed=3, bias=True)
+    xs = torch.randn(M, K + 64).bfloat16()
+    xs[:, :K] = x
+    xd, wd, sd, bd = gpu(x, wp, s, b)
+    y0 = C.woq_linear_gate_up(xd, wd, sd, None, bd).cpu()
+    y = C.woq_linear_gate_up(xs.to(DEV)[:, :K], wd, sd, None, bd).cpu()
+    assert torch.equal(y, y0)

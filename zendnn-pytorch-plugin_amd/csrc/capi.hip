@@ -110,7 +110,8 @@ namespace {
 
 constexpr const char *kKnobNames[kKnobCount] = {
     "ZT_WOQ_FORCE_KERNEL", "ZT_WOQ_DECODE_PLAN", "ZT_WOQ_STREAM", "ZT_WOQ_WIDE",
-    "ZT_WOQ_GEMM",         "ZT_WOQ_DEBUG",       "ZT_WOQ_WAVE",    "ZT_S8_SKINNY32", "ZT_S8_SKINNY",
+    "ZT_WOQ_GEMM",         "ZT_WOQ_DEBUG",       "ZT_WOQ_WAVE",    "ZT_WOQ_PERSIST",
+    "ZT_S8_SKINNY32",      "ZT_S8_SKINNY",
     "ZT_S8_FRAG",          "ZT_S8_FORCE",        "ZT_S8_TILE",     "ZT_S8_KIND",
     "ZT_S8_SPLIT",         "ZT_MOE_BN"};
 

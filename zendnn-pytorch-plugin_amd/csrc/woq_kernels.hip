@@ -19,6 +19,9 @@
 //    meet in LDS.  The wave kernel gives every wave its own x slice and no
 //    barrier before the reduction; the stream kernel shares one x copy.
 //    Rows past what one launch holds go in blocks of 16.
+//  * woq_persist_kernel  the merged gate_up at 9..16 rows: one workgroup
+//    per CU loops over row units with x in registers and the next units'
+//    weights in flight.
 //  * woq_decode_kernel   the older decode kernel for shapes the two above do
 //    not take (long K split over workgroups, general dequant modes).
 //  * woq_gemm32_kernel / woq_gemm_dma_kernel  prefill (more rows): LDS tiles
@@ -1495,6 +1498,198 @@ static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmas
   return false;
 }
 
+// ------------------------------------------------ persistent decode
+// The wave kernel's split of K (NW waves of CPW 128-wide chunks, no barrier
+// before the reduction) with each workgroup looping over many row units:
+// TPW 16-row tiles, or with gu the gate tile and its up tile.  A wave's x
+// slice is loaded once into registers as its B operands and serves every
+// unit; the weights and scales of the next D units are in flight while a
+// unit is computed.  Unit i's partial tiles meet in LDS slab i % 2 after
+// one barrier, and its reduction and epilogue run while the next units'
+// weights land (slab i % 2 is written again only after the barrier of unit
+// i + 1, which every thread reaches after reducing unit i).  Grid: at most
+// one workgroup per CU, units dealt round robin, so per-workgroup set-up
+// (x, launch) is paid once per CU rather than once per unit.  Fast mode
+// only: signed int4, bf16 scales, bf16 x, M <= 16, K == NW * CPW * 128.
+template <int NW, int CPW, int TPW>
+struct PersistSet {
+  u32x4_t w[TPW][CPW];
+  uint32_t s[TPW][CPW];
+};
+
+template <int NW, int CPW, int TPW, int D>
+__global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg_shift, int gmask,
+                                                              int gu, int units) {
+  extern __shared__ __attribute__((aligned(16))) float pslab[];  // [2][NW][TPW][16][17]
+  constexpr int SLAB = NW * TPW * 16 * 17;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
+  const int c0 = wv * CPW;
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
+  // B operands: token column lr (columns past M repeat row M - 1, whose
+  // sums are never stored), elements 32 lg + 8 i .. + 7 of each chunk
+  const int xrow = min(lr, M - 1);
+  u32x4_t xb[CPW][4];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xb[c][i] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                       x_rs, (uint32_t)(xrow * a.ldx * 2 + ((c0 + c) * 128 + 32 * lg + 8 * i) * 2),
+                       0, 0));
+  const int G0 = (int)gridDim.x;
+  // units of this workgroup: blockIdx.x + i G0, i < nu
+  const int nu = (units - (int)blockIdx.x + G0 - 1) / G0;  // >= 1: the grid is <= units
+  auto rowbase = [&](int u, int t) { return gu ? t * gu + u * 16 : (u * TPW + t) * 16; };
+  // unconditional loads (a load under a lane condition becomes a branch,
+  // and the compiler then drains every load in flight at it): a unit index
+  // past nu re-reads the workgroup's last unit into a set nothing uses, and
+  // rows past N (plain calls' last unit) re-read row N - 1, never stored
+  auto issue = [&](int i, PersistSet<NW, CPW, TPW> &S) {
+    const int u = (int)blockIdx.x + min(i, nu - 1) * G0;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int n = min(rowbase(u, t) + lr, N - 1);
+      const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) {
+        S.w[t][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    w_rs, row_off + (uint32_t)(c0 + c) * 64u, 0, 0));
+        const uint32_t g = (uint32_t)(((c0 + c) >> cpg_shift) & gmask);
+        S.s[t][c] = __builtin_amdgcn_raw_buffer_load_b16(
+            s_rs, (g * (uint32_t)N + (uint32_t)n) * 2u, 0, 0);
+      }
+    }
+  };
+  auto unit = [&](int i, const PersistSet<NW, CPW, TPW> &S) {
+    f32x4_t acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float sc = __uint_as_float(S.s[t][c] << 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              dq_word<kDecFast>(S.w[t][c][q], sc, 0.f, 0), __builtin_bit_cast(bf16x8_t, xb[c][q]),
+              acc[t], 0, 0, 0);
+      }
+    // D[row = 4 lg + r][token = lr] of tile t -> slab (i % 2)[wave][t]
+    float *slab = pslab + (i & 1) * SLAB;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][r];
+    __syncthreads();
+    const int u = (int)blockIdx.x + i * G0;
+    if (gu) {
+      for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
+        const int m = idx / 16, nr = idx - m * 16;
+        const int jj = u * 16 + nr;
+        float g = 0.f, up = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          g += slab[((w * TPW) * 16 + nr) * 17 + m];
+          up += slab[((w * TPW + 1) * 16 + nr) * 17 + m];
+        }
+        if (a.bias) {
+          g = g + load_elem(a.bias, a.b_dt, jj);
+          up = up + load_elem(a.bias, a.b_dt, gu + jj);
+        }
+        if (a.y_dt == ZT_DT_BF16) up = bf16_bits_to_f32(f32_to_bf16_bits(up));
+        store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + jj, unary_op(ZT_PO_SILU, g) * up);
+      }
+      return;
+    }
+    for (int idx = tid; idx < TPW * 16 * M; idx += 64 * NW) {
+      const int m = idx / (TPW * 16), nr = idx - m * (TPW * 16);
+      const int n = u * TPW * 16 + nr;
+      if (n >= N) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v += slab[((w * TPW + (nr >> 4)) * 16 + (nr & 15)) * 17 + m];
+      if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
+      v = apply_post_ops(v, a.post, m, n);
+      store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
+    }
+  };
+
+  PersistSet<NW, CPW, TPW> S[D + 1];
+#pragma unroll
+  for (int p = 0; p < D; ++p) issue(p, S[p]);
+  // whole rounds of D + 1 units (fixed register sets), then the rest
+  int i0 = 0;
+  for (; i0 + D + 1 <= nu; i0 += D + 1) {
+#pragma unroll
+    for (int p = 0; p <= D; ++p) {
+      issue(i0 + p + D, S[(p + D) % (D + 1)]);
+      unit(i0 + p, S[p]);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < D; ++p)
+    if (i0 + p < nu) {
+      issue(i0 + p + D, S[(p + D) % (D + 1)]);
+      unit(i0 + p, S[p]);
+    }
+}
+
+template <int NW, int CPW, int TPW, int D>
+static hipError_t launch_persist_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int gu,
+                                   int units) {
+  const unsigned grid = (unsigned)(units < 256 ? units : 256);
+  const size_t lds = (size_t)2 * NW * TPW * 16 * 17 * 4;
+  woq_persist_kernel<NW, CPW, TPW, D><<<dim3(grid), dim3(64 * NW), lds, s>>>(a, shift, gmask, gu,
+                                                                           units);
+  return hipGetLastError();
+}
+
+// The persistent kernel where it applies: fast mode, bf16 x with 16-byte
+// rows, M <= 16, K = NW waves x CPW chunks, gu > 0 the merged gate_up (I =
+// gu, a multiple of 16).  Taken by default for the merged gate_up from
+// M = 9 with 16 waves (measured in HIP-graph replays over rotating weights,
+// 28672 x 4096: 19.3 / 20.2 us at M = 12 / 16 against 25.1 / 25.8 for the
+// wave kernel, whose per-workgroup x copy then fills the LDS; within 0.6 us
+// of it at M <= 8).  ZT_WOQ_PERSIST: "0" never, "1" / "2" force 8 / 16
+// waves wherever the shape allows.
+static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
+                               int gu, hipError_t *err) {
+  const char *e = knob(kKnobWoqPersist);
+  if (e && e[0] == '0') return false;
+  if (!e && !(gu && a.M >= 9)) return false;
+  if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || (gu && gu % 16))
+    return false;
+  if (((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) ||
+      (a.M - 1) * a.ldx * 2 + a.K * 2 >= (int64_t)kOobOffset ||
+      a.N * (a.K / 2) >= (int64_t)kOobOffset || a.G * a.N * 2 >= (int64_t)kOobOffset)
+    return false;
+  const int nw = e && e[0] == '1' ? 8 : 16;
+  if (a.K % (nw * 128)) return false;
+  const int cpw = (int)(a.K / (nw * 128));
+  const int units = gu ? (int)(gu / 16) : (int)((a.N + 31) / 32);  // rows past N read row N - 1
+  if (knob(kKnobWoqDebug))
+    std::fprintf(stderr, "[zt] woq persist M=%lld N=%lld K=%lld gu=%d: NW=%d CPW=%d units=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, gu, nw, cpw, units);
+  // register budgets: 16 waves hold 128 VGPRs, 8 waves 256 (x slices of
+  // 16 CPW, D + 1 sets of 20 TPW CPW)
+#define ZT_PERSIST_CASE(NW_, CPW_, D_)                                              \
+  if (nw == NW_ && cpw == CPW_) {                                                   \
+    *err = launch_persist_t<NW_, CPW_, 2, D_>(a, s, shift, gmask, gu, units);       \
+    return true;                                                                    \
+  }
+  ZT_PERSIST_CASE(8, 2, 2) ZT_PERSIST_CASE(8, 4, 1) ZT_PERSIST_CASE(16, 1, 2)
+  ZT_PERSIST_CASE(16, 2, 1)
+#undef ZT_PERSIST_CASE
+  return false;
+}
+
 static bool stream_x_dma(const WoqArgs &a, int p) {
   return (a.K / p) % 512 == 0 &&
          ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) == 0 &&
@@ -1534,6 +1729,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
   // N take the general bf16-scale mode (same weights, same results)
   if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
+  // the persistent kernel only when forced: no faster on the plain Llama shapes
+  if (!knob(kKnobWoqStream) && try_launch_persist(a, s, shift, gmask, mode, 0, err)) return true;
   if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, 0, err)) return true;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles, or more
@@ -2005,6 +2202,8 @@ bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   int shift = 0;
   while (cpg > 1 && (1 << shift) < cpg) ++shift;
   const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  if (!knob(kKnobWoqStream) && try_launch_persist(a, s, shift, gmask, kDecFast, (int)I, err))
+    return true;
   if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, kDecFast, (int)I, err))
     return true;
   const int C = (int)(a.K / 128), tiles = (int)(a.N / 16);

@@ -17,6 +17,7 @@ enum Knob {
   kKnobWoqGemm,         // ZT_WOQ_GEMM: "old" takes the 16x16 kernel, "128" 128x128 tiles
   kKnobWoqDebug,        // ZT_WOQ_DEBUG: print each launch shape to stderr
   kKnobWoqWave,         // ZT_WOQ_WAVE: "0" disables the wave-independent decode kernel
+  kKnobWoqPersist,      // ZT_WOQ_PERSIST: "0" never, "1" / "2" force the persistent decode kernel (8 / 16 waves)
   kKnobS8Skinny32,      // ZT_S8_SKINNY32: "TPW,PF,NW" of the 32-token skinny kernel
   kKnobS8Skinny,        // ZT_S8_SKINNY: "TPW,PF,NW" of the 16-token skinny kernel
   kKnobS8Frag,          // ZT_S8_FRAG: "0" never, "1" from M = 1 (fragment-order qx)
