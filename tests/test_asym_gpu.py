@@ -33,7 +33,7 @@ def _x(M, K, seed, dtype=torch.bfloat16):
 
 
 @pytest.mark.parametrize("M,K", [(1, 8), (5, 12), (16, 4096), (7, 11008), (130, 1024),
-                                 (3, 33), (64, 20000)])
+                                 (3, 33), (64, 20000), (1500, 4096), (1025, 14336)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_asym_quantize_bit_exact(M, K, dtype):
     x = _x(M, K, seed=M * 7 + K, dtype=dtype)

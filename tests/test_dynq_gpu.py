@@ -31,8 +31,10 @@ def make(M, K, N, seed, x_dtype=torch.bfloat16, sw_dtype=torch.float32, bias=Tru
     return x, w, sw, b
 
 
+# long rows (7 vectors per thread), a partial last 16-byte vector per
+# thread, odd row counts
 @pytest.mark.parametrize("M,K", [(1, 4), (3, 12), (16, 16), (128, 4096), (7, 11008),
-                                 (2048, 4096), (5, 1)])
+                                 (2048, 4096), (5, 1), (1025, 14336), (3001, 2056), (1024, 8)])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
 def test_quantize_bit_exact(M, K, x_dtype):
     g = torch.Generator().manual_seed(M * 31 + K)
