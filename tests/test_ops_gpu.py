@@ -241,11 +241,18 @@ def test_dynamic_qlinear_op_under_graph_capture():
     with torch.cuda.graph(graph):
         y_graph = dyn_op(xd, wd, sd, bd)
     x2 = dyn_case(2 * M, N, K, seed=42)
-    for _ in range(3):
+    # new activations in the captured input before each replay (M = 128 runs
+    # the split-K kernel, whose tile counters the captured quantise kernel
+    # clears on every replay): each replay equals an eager call on them
+    for i in range(3):
         dyn_op(x2[0].to(DEV), wd, sd, bd)
+        xi = x if i == 2 else dyn_case(M, N, K, seed=50 + i)[0]
+        xd.copy_(xi.to(DEV))
+        ref = dyn_op(xd.clone(), wd, sd, bd)
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(y_graph, eager)
+        assert torch.equal(y_graph, ref)
+    assert torch.equal(y_graph, eager)
     torch.testing.assert_close(eager.cpu().float(), O.dynamic_qlinear(x, w, sw, b).float(), **TOL)
 
 
