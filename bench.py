@@ -546,7 +546,7 @@ def main():
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(c0["GBps"] / HBM_PEAK_GBS, 4),
                             "traffic": read_traffic(),
-                            "kernel": "woq_wave_kernel",
+                            "kernel": "woq_stream_kernel",
                             "kernel_avg_us": round(c0["s_per_call"] * 1e6, 3),
                             "rocprof_kernel_avg_us": read_profile_avg(CONFIG0_TRACE_FILE),
                             "algorithmic_bytes": c0["bytes_per_call"]}

@@ -379,14 +379,16 @@ def test_empty_and_error_paths():
 
 
 # the wave-independent decode kernel (fast mode, M <= 16, even N, K = 16
-# waves x 1 / 2 / 4 chunks): group sizes 128 / 256 / 1024 and per
-# channel, every M up to the LDS limit, bias and post-ops, strided x, and
-# the same result as the stream kernel it replaces on these shapes
+# waves x 1 / 2 / 4 chunks; forced, as the library keeps it for more than
+# 4096 rows): group sizes 128 / 256 / 1024 and per channel, every M up to
+# the LDS limit, bias and post-ops, strided x, and the same result as the
+# stream kernel on these shapes
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 13, 16])
 @pytest.mark.parametrize("K,N,G", [(2048, 16, 16), (4096, 4096, 32), (4096, 496, 16),
                                    (8192, 256, 8), (8192, 112, 1)])
 def test_wave_kernel_vs_oracle(M, K, N, G, knobs):
     knobs.set("ZT_WOQ_DEBUG", None)
+    knobs.set("ZT_WOQ_WAVE", "1")  # also on 4096 rows or fewer
     y, y_ref = run_case(M, K, N, G, seed=M * 3 + G)
     knobs.set("ZT_WOQ_WAVE", "0")
     y_stream, _ = run_case(M, K, N, G, seed=M * 3 + G)
@@ -395,11 +397,13 @@ def test_wave_kernel_vs_oracle(M, K, N, G, knobs):
 
 @pytest.mark.parametrize("post,nbuf", [(("relu",), 0), (("gelu_erf",), 0), (("add",), 1),
                                        (("mul", "add"), 2)])
-def test_wave_kernel_post_ops(post, nbuf):
+def test_wave_kernel_post_ops(post, nbuf, knobs):
+    knobs.set("ZT_WOQ_WAVE", "1")
     run_case(4, 4096, 512, 32, post=post, nbuf=nbuf, seed=5, bias=True)
 
 
-def test_wave_kernel_strided_x():
+def test_wave_kernel_strided_x(knobs):
+    knobs.set("ZT_WOQ_WAVE", "1")
     M, K, N, G = 4, 4096, 256, 32
     x, q, wp, s, z, b = make_case(M, K, N, G, seed=78)
     xs = torch.randn(M, K + 64).bfloat16()
@@ -413,6 +417,7 @@ def test_wave_kernel_strided_x():
 @pytest.mark.parametrize("M,K,N,G", [(1, 8192, 4100, 64), (2, 8192, 514, 8),
                                      (1, 4096, 1000, 32), (3, 2048, 50, 16)])
 def test_wave_kernel_ragged_n(M, K, N, G, knobs):
+    knobs.set("ZT_WOQ_WAVE", "1")
     y, _ = run_case(M, K, N, G, seed=M + N)
     knobs.set("ZT_WOQ_WAVE", "0")
     y_stream, _ = run_case(M, K, N, G, seed=M + N)

@@ -1462,10 +1462,9 @@ static hipError_t launch_wave_t(const WoqArgs &a, hipStream_t s, int shift, int 
 
 // The wave-independent kernel where it applies: fast mode, bf16 x with
 // 16-byte rows, M <= 16, K = 16 waves x CPW chunks (CPW 1, 2 or 4) and the
-// x slices within 64 KB; gu > 0 is the merged gate_up (I = gu, a multiple
-// of 16; "1" in ZT_WOQ_WAVE takes it below 5 rows too).  Measured on the config-0 shape (M = 4, 4096 x 4096,
-// graph replays): 4.92 us against 5.12 for the stream kernel's 8 waves of 4
-// chunks.
+// x slices within 64 KB, more than 4096 rows unless forced; gu > 0 is the
+// merged gate_up (I = gu, a multiple of 16; "1" in ZT_WOQ_WAVE takes it
+// below 5 rows and on 4096 rows or fewer too).
 static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                             int gu, hipError_t *err) {
   const char *e = knob(kKnobWoqWave);  // "0" disables
@@ -1484,6 +1483,12 @@ static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmas
   // against 20.0 at M = 8, but 18.2 against 17.3 at M = 1); the down
   // projection (16 x 7 chunks, M <= 2) no faster, so CPW 7 is not used
   if (gu && a.M < 5 && !e) return false;
+  // at most one tile per CU (N <= 4096), the stream kernel's 8 waves did as
+  // well or better on every box measured but one (4096 x 4096 at M = 1..8:
+  // 4.96-5.38 us against 5.21-5.42), and its rocprof kernel durations agree
+  // with the graph-replay time per call where the wave kernel's run 14 %
+  // longer under the tracer
+  if (!gu && a.N <= 4096 && !e) return false;
   if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq wave M=%lld N=%lld K=%lld gu=%d: NW=16 CPW=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, gu, cpw);
