@@ -439,12 +439,14 @@ def test_wave_kernel_gate_up(M, K, I, G, knobs):
 # workgroup loops over row units with the next units' weights in flight;
 # units past N (ragged last unit), more units than workgroups, group sizes
 # and per channel, bias and post-ops, and the merged gate_up
-@pytest.mark.parametrize("variant", ["1", "2"])
+# None: the library's choice, the persistent kernel from 12288 rows
+@pytest.mark.parametrize("variant", ["1", "2", None])
 @pytest.mark.parametrize("M", [1, 4, 9, 16])
 @pytest.mark.parametrize("K,N,G", [(2048, 16, 16), (4096, 4096, 32), (4096, 12304, 32),
-                                   (2048, 9000, 1), (4096, 496, 16)])
+                                   (2048, 9000, 1), (4096, 496, 16), (4096, 14336, 32)])
 def test_persist_kernel_vs_oracle(variant, M, K, N, G, knobs):
-    knobs.set("ZT_WOQ_PERSIST", variant)
+    if variant:
+        knobs.set("ZT_WOQ_PERSIST", variant)
     y, y_ref = run_case(M, K, N, G, seed=M * 5 + N + G)
 
 

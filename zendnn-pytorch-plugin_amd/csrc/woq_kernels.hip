@@ -19,9 +19,9 @@
 //    meet in LDS.  The wave kernel gives every wave its own x slice and no
 //    barrier before the reduction; the stream kernel shares one x copy.
 //    Rows past what one launch holds go in blocks of 16.
-//  * woq_persist_kernel  the merged gate_up at 9..16 rows: one workgroup
-//    per CU loops over row units with x in registers and the next units'
-//    weights in flight.
+//  * woq_persist_kernel  the merged gate_up at 9..16 rows and plain calls
+//    of 12288 rows or more: one workgroup per CU loops over row units with
+//    x in registers and the next units' weights in flight.
 //  * woq_decode_kernel   the older decode kernel for shapes the two above do
 //    not take (long K split over workgroups, general dequant modes).
 //  * woq_gemm32_kernel / woq_gemm_dma_kernel  prefill (more rows): LDS tiles
@@ -1658,17 +1658,21 @@ static hipError_t launch_persist_t(const WoqArgs &a, hipStream_t s, int shift, i
 
 // The persistent kernel where it applies: fast mode, bf16 x with 16-byte
 // rows, M <= 16, K = NW waves x CPW chunks, gu > 0 the merged gate_up (I =
-// gu, a multiple of 16).  Taken by default for the merged gate_up from
-// M = 9 with 16 waves (measured in HIP-graph replays over rotating weights,
-// 28672 x 4096: 19.3 / 20.2 us at M = 12 / 16 against 25.1 / 25.8 for the
-// wave kernel, whose per-workgroup x copy then fills the LDS; within 0.6 us
-// of it at M <= 8).  ZT_WOQ_PERSIST: "0" never, "1" / "2" force 8 / 16
-// waves wherever the shape allows.
+// gu, a multiple of 16; units of a gate/up tile pair), else units of one
+// 16-row tile.  Taken by default with 16 waves where it measured faster (HIP-graph
+// replays over rotating weights): the merged gate_up from M = 9 (28672 x
+// 4096: 19.3 / 20.2 us at M = 12 / 16 against 25.1 / 25.8 for the wave
+// kernel, whose per-workgroup x copy then fills the LDS; within 0.6 us of
+// it at M <= 8), and plain calls from 12288 rows, three or more units per
+// CU (14336 x 4096: 10.2 / 10.7 / 12.6 us at M = 1 / 8 / 16 against 10.9 /
+// 11.9 / 13.5 for the stream kernel); QKV- and O-sized calls (1.5 and 1
+// unit per CU) are slower on it.  ZT_WOQ_PERSIST: "0" never, "1" / "2"
+// force 8 / 16 waves wherever the shape allows.
 static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                                int gu, hipError_t *err) {
   const char *e = knob(kKnobWoqPersist);
   if (e && e[0] == '0') return false;
-  if (!e && !(gu && a.M >= 9)) return false;
+  if (!e && !(gu ? a.M >= 9 : a.N >= 12288)) return false;
   if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || (gu && gu % 16))
     return false;
   if (((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) ||
@@ -1678,7 +1682,8 @@ static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int g
   const int nw = e && e[0] == '1' ? 8 : 16;
   if (a.K % (nw * 128)) return false;
   const int cpw = (int)(a.K / (nw * 128));
-  const int units = gu ? (int)(gu / 16) : (int)((a.N + 31) / 32);  // rows past N read row N - 1
+  // units: gate/up tile pairs, or single 16-row tiles of a plain call
+  const int units = gu ? (int)(gu / 16) : (int)((a.N + 15) / 16);  // rows past N read row N - 1
   if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq persist M=%lld N=%lld K=%lld gu=%d: NW=%d CPW=%d units=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, gu, nw, cpw, units);
@@ -1686,7 +1691,8 @@ static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int g
   // 16 CPW, D + 1 sets of 20 TPW CPW)
 #define ZT_PERSIST_CASE(NW_, CPW_, D_)                                              \
   if (nw == NW_ && cpw == CPW_) {                                                   \
-    *err = launch_persist_t<NW_, CPW_, 2, D_>(a, s, shift, gmask, gu, units);       \
+    *err = gu ? launch_persist_t<NW_, CPW_, 2, D_>(a, s, shift, gmask, gu, units)   \
+              : launch_persist_t<NW_, CPW_, 1, D_>(a, s, shift, gmask, 0, units);   \
     return true;                                                                    \
   }
   ZT_PERSIST_CASE(8, 2, 2) ZT_PERSIST_CASE(8, 4, 1) ZT_PERSIST_CASE(16, 1, 2)
@@ -1734,7 +1740,6 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
   // N take the general bf16-scale mode (same weights, same results)
   if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
-  // the persistent kernel only when forced: no faster on the plain Llama shapes
   if (!knob(kKnobWoqStream) && try_launch_persist(a, s, shift, gmask, mode, 0, err)) return true;
   if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, 0, err)) return true;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
