@@ -115,10 +115,12 @@ def test_qlinear_out_forms(variant):
                                   output_dtype=torch.int8)
 
 
-# (M, N, K): each row reaches another int8 GEMM kernel (skinny 16/32-token,
-# 16x16, load-wave, generic)
-@pytest.mark.parametrize("M,N,K", [(1, 264, 512), (16, 130, 256), (100, 520, 1024),
-                                   (200, 264, 512), (2048, 512, 1024), (5, 33, 12)])
+# (M, N, K): each row reaches another int8 GEMM kernel (skinny 16-token,
+# split-K 32-token (twice: a ragged last tile), 32-token, 16x16, load-wave,
+# generic)
+@pytest.mark.parametrize("M,N,K", [(1, 264, 512), (100, 520, 1024), (128, 1000, 2048),
+                                   (40, 130, 256), (200, 264, 512), (2048, 512, 1024),
+                                   (5, 33, 12)])
 @pytest.mark.parametrize("kind", ["u8_in_u8_out", "f32_zp_s8_out", "bf16_sym_bf16_out"])
 def test_qlinear_kernels(M, N, K, kind):
     in_dtype = {"u8_in_u8_out": torch.uint8, "f32_zp_s8_out": torch.float32,
