@@ -5,6 +5,8 @@
 * zentorch/_C.so -- TORCH_LIBRARY(zentorch) registration and the AOTInductor
   shims of include/shim_cuda_zentorch.h, linked against the library above and
   PyTorch-ROCm.
+* tests/native/bf16_rne_check -- a GPU program that checks the kernels' bf16
+  rounding on every fp32 bit pattern (run by tests/test_bf16_rne_gpu.py).
 
 Run ``python zendnn-pytorch-plugin_amd/build.py`` (or __graft_entry__.build()).
 Every call compiles; objects go to zendnn-pytorch-plugin_amd/_build/.
@@ -102,6 +104,10 @@ def build(verbose=False, jobs=8):
     clib = os.path.join(PKG, "_C.so")
     _run(["g++", "-shared", "-o", clib + ".tmp"] + torch_objs + ldflags, verbose)
     os.replace(clib + ".tmp", clib)
+    # the GPU test of the library's bf16 rounding (tests/test_bf16_rne_gpu.py)
+    check = os.path.join(ROOT, "tests", "native", "bf16_rne_check")
+    _run([HIPCC] + HIP_FLAGS + ["-o", check + ".tmp", check + ".hip"], verbose)
+    os.replace(check + ".tmp", check)
     return hiplib, clib
 
 

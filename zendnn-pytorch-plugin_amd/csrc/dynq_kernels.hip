@@ -385,8 +385,8 @@ __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i3
     }
     if (a.y_dt == ZT_DT_BF16) {
       u32x2_t p;
-      p[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-      p[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      p[0] = pack_bf16x2(f[0], f[1]);
+      p[1] = pack_bf16x2(f[2], f[3]);
       *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = p;
       return;
     }
@@ -437,8 +437,8 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
       }
       if (a.y_dt == ZT_DT_BF16) {
         u32x2_t pk;
-        pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-        pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+        pk[0] = pack_bf16x2(f[0], f[1]);
+        pk[1] = pack_bf16x2(f[2], f[3]);
         *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
       } else {
         *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =
@@ -1147,8 +1147,8 @@ struct QuadEpi {
       }
       if (a.y_dt == ZT_DT_BF16) {
         u32x2_t pk;
-        pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-        pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+        pk[0] = pack_bf16x2(f[0], f[1]);
+        pk[1] = pack_bf16x2(f[2], f[3]);
         *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * N + n) = pk;
       } else {
         *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(a.y) + (int64_t)m * N + n) =

@@ -365,8 +365,8 @@ __device__ __forceinline__ void moe_tile(const MoeGemm &g, int e, int r0, int r_
 #pragma unroll
     for (int r = 0; r < 4; ++r) f[r] = GATED ? unary_op(g.act, t[r]) * t[COLS + r] : t[r];
     u32x2_t pk;
-    pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-    pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+    pk[0] = pack_bf16x2(f[0], f[1]);
+    pk[1] = pack_bf16x2(f[2], f[3]);
     *reinterpret_cast<u32x2_t *>(g.out + (size_t)(r0 + row) * g.ldo + n) = pk;
   }
 }
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *y, int
     u32x4_t o;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      o[i] = (uint32_t)f32_to_bf16_bits(acc[2 * i]) | ((uint32_t)f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+      o[i] = pack_bf16x2(acc[2 * i], acc[2 * i + 1]);
     *reinterpret_cast<u32x4_t *>(out + (size_t)t * H + h) = o;
   }
 }

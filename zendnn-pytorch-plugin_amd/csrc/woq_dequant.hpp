@@ -36,11 +36,6 @@ __device__ __forceinline__ float f16_hi(uint32_t p) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(p >> 16));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});
-}
-
 constexpr uint32_t kNibLo = 0x000F000Fu;   // nibbles at bits 0-3 of each half
 constexpr uint32_t kNibHi = 0x00F000F0u;   // nibbles at bits 4-7 of each half
 constexpr uint32_t kExpLo = 0x64006400u;   // fp16 1024 in both halves
@@ -57,10 +52,10 @@ __device__ __forceinline__ u32x4_t dq8_s4_bf16scale(uint32_t w, float s, float s
   const uint32_t p2 = and_xor(w8, kNibLo, kExpLo | kXorLo);  // elements 2, 6
   const uint32_t p3 = and_xor(w8, kNibHi, kExpLo | kXorHi);  // elements 3, 7
   u32x4_t r;
-  r[0] = pack_bf16(fmaf(f16_lo(p0), s, c0), fmaf(f16_lo(p1), s16, c1));
-  r[1] = pack_bf16(fmaf(f16_lo(p2), s, c0), fmaf(f16_lo(p3), s16, c1));
-  r[2] = pack_bf16(fmaf(f16_hi(p0), s, c0), fmaf(f16_hi(p1), s16, c1));
-  r[3] = pack_bf16(fmaf(f16_hi(p2), s, c0), fmaf(f16_hi(p3), s16, c1));
+  r[0] = pack_bf16x2(fmaf(f16_lo(p0), s, c0), fmaf(f16_lo(p1), s16, c1));
+  r[1] = pack_bf16x2(fmaf(f16_lo(p2), s, c0), fmaf(f16_lo(p3), s16, c1));
+  r[2] = pack_bf16x2(fmaf(f16_hi(p0), s, c0), fmaf(f16_hi(p1), s16, c1));
+  r[3] = pack_bf16x2(fmaf(f16_hi(p2), s, c0), fmaf(f16_hi(p3), s16, c1));
   return r;
 }
 
@@ -102,10 +97,10 @@ __device__ __forceinline__ u32x4_t dq8_general(uint32_t w, const DqGeneral &d) {
   auto q0 = [&](float h) { return dq_general_one(fmaf(h, 1.f, d.o0), d); };
   auto q1 = [&](float h) { return dq_general_one(fmaf(h, 0.0625f, d.o1), d); };
   u32x4_t r;
-  r[0] = pack_bf16(q0(f16_lo(p0)), q1(f16_lo(p1)));
-  r[1] = pack_bf16(q0(f16_lo(p2)), q1(f16_lo(p3)));
-  r[2] = pack_bf16(q0(f16_hi(p0)), q1(f16_hi(p1)));
-  r[3] = pack_bf16(q0(f16_hi(p2)), q1(f16_hi(p3)));
+  r[0] = pack_bf16x2(q0(f16_lo(p0)), q1(f16_lo(p1)));
+  r[1] = pack_bf16x2(q0(f16_lo(p2)), q1(f16_lo(p3)));
+  r[2] = pack_bf16x2(q0(f16_hi(p0)), q1(f16_hi(p1)));
+  r[3] = pack_bf16x2(q0(f16_hi(p2)), q1(f16_hi(p3)));
   return r;
 }
 

@@ -683,8 +683,8 @@ __device__ __forceinline__ void woq_tile_epilogue(const WoqArgs &a, const float 
     }
     if (a.y_dt == ZT_DT_BF16 && n + 3 < N && (a.ldy & 3) == 0) {
       u32x2_t pk;
-      pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-      pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+      pk[0] = pack_bf16x2(f[0], f[1]);
+      pk[1] = pack_bf16x2(f[2], f[3]);
       *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * a.ldy + n) = pk;
     } else {
 #pragma unroll
@@ -2077,8 +2077,8 @@ __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const
   }
   if (a.y_dt == ZT_DT_BF16 && (a.ldy & 3) == 0) {
     u32x2_t pk;
-    pk[0] = (uint32_t)f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16);
-    pk[1] = (uint32_t)f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16);
+    pk[0] = pack_bf16x2(f[0], f[1]);
+    pk[1] = pack_bf16x2(f[2], f[3]);
     *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(a.y) + (int64_t)m * a.ldy + n) = pk;
   } else {
 #pragma unroll

@@ -31,12 +31,18 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
-// fp32 -> bf16 bits, IEEE round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16, IEEE round to nearest even; a NaN keeps its sign and top
+// payload bits and becomes quiet ((bits >> 16) | 0x40).  gfx950's
+// v_cvt_pk_bf16_f32 does exactly this for every fp32 bit pattern
+// (tests/native/bf16_rne_check.hip compares it with the integer form
+// ((bits + 0x7fff + lsb) >> 16) on all 2^32 of them), and converts two
+// values in one instruction.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float load_elem(const void *p, int dt, int64_t i) {
