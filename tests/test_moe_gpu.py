@@ -92,6 +92,19 @@ def test_moe_one_expert_takes_every_pair_and_idle_experts():
     torch.testing.assert_close(y.float(), ref.float(), **TOL)
 
 
+# routing past one 1024-pair chunk, with many experts (up to 64 distinct
+# ones in a wave) and with few: every pair must land on its own row
+@pytest.mark.parametrize("T,E,k", [(700, 96, 2), (1500, 3, 1), (513, 1024, 2)])
+def test_moe_routing_chunks_and_many_experts(T, E, k):
+    H, I = 256, 128
+    experts = make_experts(E, H, I, seed=T + E)
+    ids, wts = route(T, E, k, seed=T + E)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(14)).bfloat16()
+    y = run_gpu(x, ids, wts, experts)
+    ref = O.woq_moe(x, ids, wts, *experts[:4])
+    torch.testing.assert_close(y.float(), ref.float(), **TOL)
+
+
 def test_moe_decode_single_token():
     T, H, I, E, k = 1, 1024, 512, 8, 2
     experts = make_experts(E, H, I, seed=5)

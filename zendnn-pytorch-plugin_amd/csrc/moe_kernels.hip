@@ -8,7 +8,8 @@
 // GPU without a host round trip (so the op can be captured in a HIP graph):
 //
 //  * moe_route_kernel   one workgroup: per-expert counts, a stable order of
-//    the pairs by expert (the token of each row in that order: pair_token),
+//    the pairs by expert (the token of each row in that order: pair_token;
+//    ranks from wave ballots),
 //    each pair's row in that order (pair_pos, -1 for ids outside [0, E)),
 //    expert row offsets, and a table of (expert, first row, end row) for
 //    every BM-row tile of the grouped GEMMs.
@@ -41,12 +42,18 @@ constexpr int kMoeDepth = 2;  // K steps of weights loaded ahead
 constexpr int kMoeComputeWaves = 4;
 constexpr int kMoeThreads = 64 * (kMoeComputeWaves + 1);  // + the x producer
 
+// Ranks are stable: pair i's row is its expert's offset plus the number of
+// earlier pairs with the same expert.  The pairs go in chunks of 1024, one
+// per thread; inside a wave a ballot per distinct expert gives each lane its
+// rank among the wave's lanes of that expert and the wave's count of it
+// (wcnt[wave][e], dynamic LDS of 16 E ints), the waves before it add theirs,
+// and base[e] carries the counts of earlier chunks.
 __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int P, int E,
                                                           int topk, MoeWork w) {
   __shared__ int cnt[1024];
   __shared__ int base[1024];
-  __shared__ int chunk_e[1024];
-  const int tid = threadIdx.x;
+  extern __shared__ int wcnt[];  // [16][E]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < E; e += 1024) cnt[e] = 0;
   __syncthreads();
   for (int i = tid; i < P; i += 1024) {
@@ -71,30 +78,41 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int32_t *ids, int
     w.expert_off[E] = off;
     w.num_mt[0] = nt;
   }
-  __syncthreads();
-  // stable positions: rank of pair i among the earlier pairs of its expert
+  const uint64_t lt = (1ull << lane) - 1;
   for (int c0 = 0; c0 < P; c0 += 1024) {
+    for (int j = tid; j < 16 * E; j += 1024) wcnt[j] = 0;
+    __syncthreads();  // also orders base[] after tid 0 or the previous chunk
     const int i = c0 + tid;
     int e = i < P ? ids[i] : -1;
     if (e >= E) e = -1;
-    chunk_e[tid] = e;
-    __syncthreads();
+    // rank among this wave's lanes of the same expert, one ballot per
+    // distinct expert of the wave (the loop is wave-uniform)
     int rank = 0;
-    bool last = true;
-    if (e >= 0) {
-      for (int j = 0; j < tid; ++j) rank += chunk_e[j] == e;
-      for (int j = tid + 1; j < 1024 && c0 + j < P; ++j)
-        if (chunk_e[j] == e) { last = false; break; }
+    uint64_t todo = __ballot(e >= 0);
+    while (todo) {
+      const int ee = __shfl(e, __ffsll((unsigned long long)todo) - 1);
+      const uint64_t m = __ballot(e == ee);
+      if (e == ee) {
+        rank = __popcll(m & lt);
+        if (rank == 0) wcnt[wave * E + e] = __popcll(m);
+      }
+      todo &= ~m;
     }
+    __syncthreads();
     int pos = -1;
     if (e >= 0) {
+      for (int v = 0; v < wave; ++v) rank += wcnt[v * E + e];
       pos = base[e] + rank;
       w.pair_token[pos] = i / topk;
     }
     if (i < P) w.pair_pos[i] = pos;
-    __syncthreads();
-    if (e >= 0 && last) base[e] += rank + 1;
-    __syncthreads();
+    __syncthreads();  // every base[] read of this chunk is done
+    for (int ee = tid; ee < E; ee += 1024) {
+      int n = 0;
+      for (int v = 0; v < 16; ++v) n += wcnt[v * E + ee];
+      base[ee] += n;
+    }
+    __syncthreads();  // before the next chunk clears wcnt
   }
 }
 
@@ -451,7 +469,7 @@ int moe_max_tiles(int64_t P, int64_t E) { return (int)((P + kMoeBM - 1) / kMoeBM
 hipError_t launch_woq_moe(const MoeArgs &a, const MoeWork &w, hipStream_t s) {
   const int P = (int)(a.T * a.topk);
   const int mt_max = moe_max_tiles(P, a.E);
-  moe_route_kernel<<<1, 1024, 0, s>>>(a.ids, P, (int)a.E, (int)a.topk, w);
+  moe_route_kernel<<<1, 1024, (size_t)16 * a.E * sizeof(int), s>>>(a.ids, P, (int)a.E, (int)a.topk, w);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
 
