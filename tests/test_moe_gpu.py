@@ -92,6 +92,23 @@ def test_moe_one_expert_takes_every_pair_and_idle_experts():
     torch.testing.assert_close(y.float(), ref.float(), **TOL)
 
 
+# both tile widths of each GEMM (ZT_MOE_BN="gate_up,down"): 128 (four
+# compute waves and an A producer wave) and 256 (the wide form: four waves
+# of two tiles, A moved by the compute waves); H = 384 leaves the last
+# 256-column down tile half empty
+@pytest.mark.parametrize("bn", ["128,128", "256,256", "256,128", "128,256"])
+@pytest.mark.parametrize("T,H,I,E,k", [(8, 256, 128, 4, 2), (70, 512, 256, 8, 2),
+                                       (64, 1024, 2048, 8, 2), (5, 384, 384, 3, 3)])
+def test_moe_tile_widths(T, H, I, E, k, bn, knobs):
+    knobs.set("ZT_MOE_BN", bn)
+    experts = make_experts(E, H, I, seed=T + H + 1, bias=T == 70)
+    ids, wts = route(T, E, k, seed=T + 1)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(15)).bfloat16()
+    y = run_gpu(x, ids, wts, experts)
+    ref = O.woq_moe(x, ids, wts, *experts[:4], w13_bias=experts[4], w2_bias=experts[5])
+    torch.testing.assert_close(y.float(), ref.float(), **TOL)
+
+
 # routing past one 1024-pair chunk, with many experts (up to 64 distinct
 # ones in a wave) and with few: every pair must land on its own row
 @pytest.mark.parametrize("T,E,k", [(700, 96, 2), (1500, 3, 1), (513, 1024, 2)])

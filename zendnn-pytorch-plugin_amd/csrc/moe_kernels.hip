@@ -13,8 +13,9 @@
 //    each pair's row in that order (pair_pos, -1 for ids outside [0, E)),
 //    expert row offsets, and a table of (expert, first row, end row) for
 //    every BM-row tile of the grouped GEMMs.
-//  * woq_moe_gemm_kernel<GATED, BN>  an int4 GEMM over that tile table on
-//    32x32x16 bf16 MFMAs.  A rows are gathered (w13: the input row of the
+//  * woq_moe_gemm_kernel<GATED, BN> / woq_moe_gemm_wide_kernel<GATED, BN>
+//    an int4 GEMM over that tile table on 32x32x16 bf16 MFMAs (the wide
+//    form, 256 weight rows per workgroup, runs the gate_up GEMM).  A rows are gathered (w13: the input row of the
 //    pair's token; w2: the pair's row of the intermediate), the weight
 //    pointer is the tile's expert.  GATED tiles pair gate rows n with their
 //    up rows I + n, so the epilogue writes act(g) * u directly.
@@ -389,6 +390,240 @@ __device__ __forceinline__ void moe_tile(const MoeGemm &g, int e, int r0, int r_
   }
 }
 
+// Wide form of moe_tile: BN = 128 WTN weight rows per workgroup, four
+// waves that each own WTN 32-column tiles (tile t = 4 j + wave), so every
+// A fragment read from LDS feeds WTN MFMAs instead of one.  There is no
+// producer wave (its registers would cost the second workgroup per CU):
+// each wave moves a quarter of the A rows by DMA together with its own
+// weights, both two K steps ahead.  A wave's loads retire in issue order
+// and the A rows and weights of a step are issued together, so one vmcnt
+// wait per step covers both, and the barrier after it publishes every
+// wave's share of the A tile.  Past the last step the DMA still issues,
+// out of range (zeros into a stage no one reads), so that every step
+// leaves the same number of loads in flight.  The epilogue goes through
+// LDS one tile column j at a time (128 fp32 columns, so two workgroups fit
+// a CU).
+template <bool GATED, int BN, int NB>
+__device__ __forceinline__ void moe_tile_wide(const MoeGemm &g, int e, int r0, int r_end, int tn,
+                                              unsigned char *smem) {
+  constexpr int WTN = BN / 128;  // 32-column tiles per wave
+  constexpr int XL = 2 * NB;     // 1 KB A loads (4 rows each) per wave per step
+  static_assert(WTN >= 2, "the wide form owns at least two tiles per wave");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lc = lane & 31, kb = lane >> 5;
+  const int K = g.K, KW = K / 8, N = g.N;
+  const int n0 = GATED ? tn * (BN / 2) : tn * BN;
+  const int nk = K / 128;
+  constexpr int kLgkm0 = 15 | (3 << 14) | (7 << 4);  // s_waitcnt lgkmcnt(0) alone
+
+  // A rows 4 q' .. 4 q' + 3, q' = XL wv + q, 16 bytes per lane; rows past
+  // the expert's last pair read 0
+  const auto a_rs = make_rsrc(g.a, (uint32_t)((int64_t)g.a_rows * g.lda * 2));
+  uint32_t a_off[XL];
+#pragma unroll
+  for (int q = 0; q < XL; ++q) {
+    const int row = 4 * (XL * wv + q) + (lane >> 4);
+    const int gr = r0 + row;
+    const int src = GATED ? g.w.pair_token[min(gr, r_end - 1)] : gr;
+    a_off[q] = (uint32_t)(src * (2 * g.lda) + (((lane & 15) ^ (row & 15)) * 16)) |
+               (gr < r_end ? 0u : kOobOffset);
+  }
+  auto issue_x = [&](int step) {
+    unsigned char *st = smem + (step % kXStages) * kXStage;
+    const uint32_t past = step < nk ? 0u : kOobOffset;
+#pragma unroll
+    for (int q = 0; q < XL; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_ptr_t)(st + 4 * (XL * wv + q) * kXRowB),
+                                               16, a_off[q] | past, step * kXRowB, 0, 0);
+  };
+
+  const uint32_t *wexp = g.w_packed + (size_t)e * N * KW;
+  const uint16_t *sexp = g.scales + (size_t)e * g.G * N;
+  const auto w_rs = make_rsrc(wexp, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(sexp, (uint32_t)(g.G * N * 2));
+  uint32_t srow2[WTN], woff[WTN];
+#pragma unroll
+  for (int j = 0; j < WTN; ++j) {
+    const int t = 4 * j + wv;
+    int n = GATED ? (lc < 16 ? n0 : g.I + n0) + t * 16 + (lc & 15) : n0 + t * 32 + lc;
+    n = min(n, N - 1);
+    srow2[j] = 2u * (uint32_t)n;
+    woff[j] = (uint32_t)n * (uint32_t)(KW * 4) + 32u * (uint32_t)kb;
+  }
+  auto issue_w = [&](int step, u32x4_t (&w)[WTN][2], uint32_t (&s)[WTN]) {
+    step = min(step, nk - 1);  // past the end: an L2 hit into a set no one reads
+    const int sb = ((step >> g.cpg_shift) & g.gmask) * N * 2;
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        w[j][h] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[j] + 16u * h,
+                                                           step * kWRowB, 0));
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+      s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, srow2[j], sb, 0);
+  };
+
+  f32x16_t acc[NB][WTN];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  auto dequant = [&](const u32x4_t (&w)[WTN][2], const uint32_t (&s)[WTN], int sub,
+                     bf16x8_t (&B)[WTN]) {
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const float sc = __uint_as_float(s[j] << 16);
+      B[j] = __builtin_bit_cast(bf16x8_t, dq8_s4_bf16scale(w[j][sub >> 2][sub & 3], sc,
+                                                            sc * 0.0625f, -1032.f * sc,
+                                                            -72.f * sc));
+    }
+  };
+  auto read_x = [&](const unsigned char *st, int sub, u32x4_t (&xf)[NB]) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      xf[i] = *reinterpret_cast<const u32x4_t *>(st + (32 * i + lc) * kXRowB +
+                                                 (((8 * kb + sub) ^ (lc & 15)) * 16));
+  };
+  auto mfmas = [&](const u32x4_t (&xf)[NB], const bf16x8_t (&B)[WTN]) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, xf[i]), B[j], acc[i][j], 0, 0, 0);
+  };
+  auto interleave = [&](bool reads) {
+    constexpr int M = NB * WTN;
+    constexpr int V = (16 * WTN + M - 1) / M;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+      if (reads && m < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+
+  constexpr int D = kMoeDepth;
+  static_assert(D == 2 && kXStages == 3, "A rows and weights travel two steps ahead");
+  u32x4_t wq[D + 1][WTN][2];
+  uint32_t sq[D + 1][WTN];
+  bf16x8_t Bn[WTN];
+#pragma unroll
+  for (int p = 0; p < D; ++p) {
+    issue_x(p);
+    issue_w(p, wq[p], sq[p]);
+  }
+  // step ks: x(ks) and w(ks) landed once only step ks + 1's loads (XL A
+  // loads, 2 WTN weight loads, WTN scale loads) are still in flight
+  constexpr int kAfter = XL + 3 * WTN;
+  dequant(wq[0], sq[0], 0, Bn);
+  auto step = [&](int ks, const u32x4_t (&wc)[WTN][2], const uint32_t (&sc)[WTN],
+                  const u32x4_t (&wx)[WTN][2], const uint32_t (&sx)[WTN],
+                  u32x4_t (&wn)[WTN][2], uint32_t (&sn)[WTN]) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfter));
+    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's reads of step ks - 1 are done
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char *st = smem + (ks % kXStages) * kXStage;
+    u32x4_t xa[NB], xb[NB];
+    read_x(st, 0, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_x(ks + D);
+    issue_w(ks + D, wn, sn);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int sub = 0; sub < 8; ++sub) {
+      bf16x8_t Bc[WTN];
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) Bc[j] = Bn[j];
+      if (sub < 7) {
+        read_x(st, sub + 1, sub & 1 ? xa : xb);
+        dequant(wc, sc, sub + 1, Bn);
+      } else {
+        dequant(wx, sx, 0, Bn);
+      }
+      mfmas(sub & 1 ? xb : xa, Bc);
+      interleave(sub < 7);
+    }
+  };
+  int k0 = 0;
+  for (; k0 + D + 1 <= nk; k0 += D + 1) {
+#pragma unroll
+    for (int p = 0; p <= D; ++p)
+      step(k0 + p, wq[p], sq[p], wq[(p + 1) % (D + 1)], sq[(p + 1) % (D + 1)],
+           wq[(p + D) % (D + 1)], sq[(p + D) % (D + 1)]);
+  }
+#pragma unroll
+  for (int p = 0; p < D; ++p)
+    if (k0 + p < nk)
+      step(k0 + p, wq[p], sq[p], wq[(p + 1) % (D + 1)], sq[(p + 1) % (D + 1)],
+           wq[(p + D) % (D + 1)], sq[(p + D) % (D + 1)]);
+
+  // epilogue, one tile column j (the waves' tiles 4 j .. 4 j + 3, i.e. 128
+  // consecutive weight rows) at a time through an fp32 LDS tile; the
+  // in-flight out-of-range DMA must land before the stages are reused
+  constexpr int COLS = GATED ? 64 : 128;              // output columns per j
+  constexpr int TPF = (GATED ? 2 * COLS : COLS) + 4;  // fp32 pitch
+  float *tile = reinterpret_cast<float *>(smem);
+  const int NO = GATED ? g.I : N;
+  const uint16_t *bexp = g.bias ? g.bias + (size_t)e * N : nullptr;
+  const int rows = min(32 * NB, r_end - r0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < WTN; ++j) {
+    if (j) __syncthreads();  // the previous column's reads are done
+    const int oc = GATED ? wv * 16 + (lc & 15) : wv * 32 + lc;  // within this j
+    const int c = GATED && lc >= 16 ? COLS + oc : oc;
+    const int n = n0 + j * COLS + oc;
+    float b = 0.f;
+    if (bexp && n < NO) b = bf16_bits_to_f32(bexp[GATED && lc >= 16 ? g.I + n : n]);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        tile[(32 * i + 8 * (r >> 2) + 4 * kb + (r & 3)) * TPF + c] = acc[i][j][r] + b;
+    __syncthreads();
+    for (int idx = tid; idx < rows * (COLS / 4); idx += 256) {
+      const int row = idx / (COLS / 4), c4 = (idx % (COLS / 4)) * 4;
+      const int nn = n0 + j * COLS + c4;
+      if (nn >= NO) continue;
+      const float *tp = tile + row * TPF + c4;
+      float f[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) f[r] = GATED ? unary_op(g.act, tp[r]) * tp[COLS + r] : tp[r];
+      u32x2_t pk;
+      pk[0] = pack_bf16x2(f[0], f[1]);
+      pk[1] = pack_bf16x2(f[2], f[3]);
+      *reinterpret_cast<u32x2_t *>(g.out + (size_t)(r0 + row) * g.ldo + nn) = pk;
+    }
+  }
+}
+
+template <bool GATED, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void woq_moe_gemm_wide_kernel(MoeGemm g, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int live = g.w.num_mt[0] * tiles_n;
+  if ((int)blockIdx.x >= live) return;  // uniform: the whole workgroup leaves
+  const int t = xcd_contiguous_tile(blockIdx.x, live);
+  const int mt = t / tiles_n, tn = t - mt * tiles_n;
+  const i32x4_t info = reinterpret_cast<const i32x4_t *>(g.w.mt_info)[mt];
+  const int e = info[0], r0 = info[1], r_end = info[2];
+  switch ((r_end - r0 + 31) >> 5) {
+    case 1: moe_tile_wide<GATED, BN, 1>(g, e, r0, r_end, tn, smem); break;
+    case 2: moe_tile_wide<GATED, BN, 2>(g, e, r0, r_end, tn, smem); break;
+    default: moe_tile_wide<GATED, BN, 3>(g, e, r0, r_end, tn, smem); break;
+  }
+}
+
 // Grid: mt_max * tiles_n workgroups (the route kernel's tile count is only
 // known on the device).  The first num_mt * tiles_n blocks take the live
 // tiles, XCD-contiguously (consecutive column tiles of one row tile share
@@ -443,17 +678,26 @@ template <bool GATED, int BN>
 hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s) {
   const int cols = GATED ? BN / 2 : BN;
   const int tiles_n = (GATED ? g.I : g.N + cols - 1) / cols;
-  const size_t tile = (size_t)kMoeBM * (BN + 4) * 4;  // fp32 epilogue tile
-  const size_t lds = tile > (size_t)kXStages * kXStage ? tile : (size_t)kXStages * kXStage;
-  woq_moe_gemm_kernel<GATED, BN><<<dim3((unsigned)(g.mt_max * tiles_n)), dim3(kMoeThreads), lds, s>>>(
-      g, tiles_n);
-  return hipGetLastError();
+  const dim3 grid((unsigned)(g.mt_max * tiles_n));
+  if constexpr (BN > 128) {  // the wide form: 128-column epilogue tiles, no producer wave
+    const size_t tile = (size_t)kMoeBM * (128 + 4) * 4;
+    const size_t lds = tile > (size_t)kXStages * kXStage ? tile : (size_t)kXStages * kXStage;
+    woq_moe_gemm_wide_kernel<GATED, BN><<<grid, dim3(256), lds, s>>>(g, tiles_n);
+    return hipGetLastError();
+  } else {
+    const size_t tile = (size_t)kMoeBM * (BN + 4) * 4;  // fp32 epilogue tile
+    const size_t lds = tile > (size_t)kXStages * kXStage ? tile : (size_t)kXStages * kXStage;
+    woq_moe_gemm_kernel<GATED, BN><<<grid, dim3(kMoeThreads), lds, s>>>(g, tiles_n);
+    return hipGetLastError();
+  }
 }
 
 // weight rows per workgroup of the gate_up and down GEMMs; ZT_MOE_BN="g,d"
-// (each 128 or 256) overrides them for tuning
+// (each 128 or 256) overrides them for tuning.  Measured on the Mixtral
+// layer (256 tokens): gate_up 218 -> 199 us with the wide form; the down
+// GEMM (4096 rows) would leave half the CUs idle with 256-row tiles.
 void moe_tile_widths(int &bn1, int &bn2) {
-  bn1 = 128, bn2 = 128;
+  bn1 = 256, bn2 = 128;
   if (const char *v = knob(kKnobMoeBn)) {
     int a = 0, b = 0;
     if (std::sscanf(v, "%d,%d", &a, &b) == 2 && (a == 128 || a == 256) &&
