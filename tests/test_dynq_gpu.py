@@ -47,6 +47,26 @@ def test_quantize_bit_exact(M, K, x_dtype):
     assert torch.equal(qx.cpu(), qr)
 
 
+# quotients x / s that are exactly half-integers (ties, rounded to even) or
+# within an ulp of one: rows whose amax is 127 * 2^e make s = 2^e exact
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_quantize_ties_bit_exact(x_dtype):
+    rows = []
+    for e in (0, -3, 5):
+        h = (torch.arange(-127, 127, dtype=torch.float32) + 0.5) * 2.0 ** e
+        row = torch.cat([torch.tensor([127.0 * 2.0 ** e]), h, -h[:1]])
+        rows.append(row)
+        # one ulp either side of every half-integer (fp32 rows only keep it)
+        rows.append(torch.cat([torch.tensor([127.0 * 2.0 ** e]), torch.nextafter(h, h + 1),
+                               torch.nextafter(h, h - 1)])[:256])
+    K = 256
+    x = torch.stack([torch.nn.functional.pad(r, (0, K - r.numel()))[:K] for r in rows]).to(x_dtype)
+    qx, sx = C.dynamic_quantize(x.to(DEV))
+    qr, sr = O.dynamic_quantize(x)
+    assert torch.equal(sx.cpu(), sr)
+    assert torch.equal(qx.cpu(), qr)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 8, 16), (5, 33, 48), (64, 96, 256), (128, 11008, 4096),
                                    (300, 130, 512), (2048, 256, 1024), (4, 17, 12),
                                    # large-M tiled kernel: ragged M, N and K % 128 != 0

@@ -56,11 +56,26 @@ __device__ __forceinline__ void row_qparams(float lo, float hi, float &s, float 
   }
 }
 
+// rint(x / s) with x / s the correctly rounded quotient, |x / s| < 256,
+// given inv = 1 / s correctly rounded.  y = x * inv is within 2 ulp of the
+// exact quotient (two roundings of relative size 2^-24) and the rounded
+// quotient within 0.5 ulp of it: 2.5 ulp <= 2.5 * 2^-16 < 2^-14 below 256.
+// So unless y lies within 2^-14 of a half-integer, both have the same
+// nearest integer and neither is a tie; only those rare elements take the
+// IEEE division.  (A product that underflows leaves |x / s| far below 0.5:
+// 0 either way; NaN and infinite inputs give NaN or 0 in both forms.)
+__device__ __forceinline__ float rint_div(float x, float s, float inv) {
+  const float y = x * inv;
+  const float r = rintf(y);
+  if (fabsf(y - r) > 0.5f - 0x1p-14f) return rintf(__fdiv_rn(x, s));
+  return r;
+}
+
 // q as stored in qx: clamp(rint(x / s) + zp) in [-128, 127] (symmetric) or
-// [0, 255] (asymmetric, stored minus 128)
+// [0, 255] (asymmetric, stored minus 128); inv = 1 / s correctly rounded
 template <bool ASYM>
-__device__ __forceinline__ int quant_one(float x, float s, float zp) {
-  float r = rintf(__fdiv_rn(x, s));
+__device__ __forceinline__ int quant_one(float x, float s, float inv, float zp) {
+  float r = rint_div(x, s, inv);
   if (ASYM) return (int)fminf(fmaxf(r + zp, 0.f), 255.f) - 128;
   return (int)fminf(fmaxf(r, -128.f), 127.f);
 }
@@ -112,9 +127,10 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(
     sx[m] = s;
     if (ASYM) azp[m] = (int32_t)zp - 128;
   }
+  const float inv = __fdiv_rn(1.0f, s);
   for (int64_t k = tid; k < K; k += 256)
     qx[frag ? qx_frag_offset(m, k, K) : base + k] =
-        (int8_t)quant_one<ASYM>(load_elem(x, x_dt, base + k), s, zp);
+        (int8_t)quant_one<ASYM>(load_elem(x, x_dt, base + k), s, inv, zp);
 }
 
 // The same per-row quantisation for bf16 rows with K % 8 == 0, 16-byte
@@ -158,7 +174,8 @@ __global__ __launch_bounds__(256) void dyn_quantize_bf16_kernel(const uint16_t *
     sx[m] = s;
     if (ASYM) azp[m] = (int32_t)zp - 128;
   }
-  auto q1 = [&](float f) { return (uint32_t)(uint8_t)(int8_t)quant_one<ASYM>(f, s, zp); };
+  const float inv = __fdiv_rn(1.0f, s);
+  auto q1 = [&](float f) { return (uint32_t)(uint8_t)(int8_t)quant_one<ASYM>(f, s, inv, zp); };
   u32x2_t *out = reinterpret_cast<u32x2_t *>(qx + m * K);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
