@@ -210,14 +210,17 @@ def test_dynamic_qlinear_fragment_kernel_post_ops(post):
     torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
 
 
-# the large-M kernels by name: the load-wave kernel (default) and the
-# 32x32 DMA kernel it replaced, on ragged shapes (M, N past a tile, K not a
-# multiple of the 128-byte step)
-@pytest.mark.parametrize("kind", ["w", "n"])
+# the large-M kernels by name: the load-wave kernel (default, also with its
+# 128 x 128 tiles: ZT_S8_TILE 1 / 0) and the kernels it replaced (n: 32x32
+# DMA, r: register-staged, 2 / 3: 16x16 DMA with 2 / 3 stages), on ragged
+# shapes (M, N past a tile, K not a multiple of the 128-byte step)
+@pytest.mark.parametrize("kind", ["w", "w1", "w0", "n", "r", "2", "3"])
 @pytest.mark.parametrize("M,N,K", [(257, 200, 144), (520, 4160, 272), (2100, 130, 2064),
                                    (512, 384, 4096)])
 def test_s8_large_m_kernels_bit_exact(kind, M, N, K, knobs):
-    knobs.set("ZT_S8_KIND", kind)
+    knobs.set("ZT_S8_KIND", kind[0])
+    if len(kind) > 1:
+        knobs.set("ZT_S8_TILE", kind[1])
     g = torch.Generator().manual_seed(M * 3 + N + K)
     a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
     w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
