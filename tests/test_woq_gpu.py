@@ -475,3 +475,20 @@ def test_persist_kernel_gate_up_strided_x():
     y0 = C.woq_linear_gate_up(xd, wd, sd, None, bd).cpu()
     y = C.woq_linear_gate_up(xs.to(DEV)[:, :K], wd, sd, None, bd).cpu()
     assert torch.equal(y, y0)
+
+
+# every prefill GEMM variant by name (ZT_WOQ_GEMM): "1" the 32x32 kernel with
+# 128 x 128 tiles (256 x 128 is the default at this size), "d" the 16x16
+# DMA kernel, "2" its 256 x 128 tiles, "o" the 16x16 kernel without DMA;
+# ragged M and N, two scale dtypes
+@pytest.mark.parametrize("variant", ["1", "d", "2", "o"])
+@pytest.mark.parametrize("M,K,N,G,s_dtype", [(300, 1024, 264, 8, torch.bfloat16),
+                                             (520, 2048, 520, 16, torch.bfloat16),
+                                             (97, 512, 136, 4, torch.float32)])
+def test_prefill_gemm_variants(variant, M, K, N, G, s_dtype):
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=M + N, bias=True, s_dtype=s_dtype)
+    y_ref = O.woq_linear(x, wp, s, bias=b)
+    xd, wd, sd, bd = gpu(x, wp, s, b)
+    with C.tuning(ZT_WOQ_FORCE_KERNEL="gemm", ZT_WOQ_GEMM=variant):
+        y = C.woq_linear(xd, wd, sd, None, bd)
+    check_close(y, y_ref)
