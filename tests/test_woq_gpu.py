@@ -478,10 +478,11 @@ def test_persist_kernel_gate_up_strided_x():
 
 
 # every prefill GEMM variant by name (ZT_WOQ_GEMM): "1" the 32x32 kernel with
-# 128 x 128 tiles (256 x 128 is the default at this size), "d" the 16x16
-# DMA kernel, "2" its 256 x 128 tiles, "o" the 16x16 kernel without DMA;
-# ragged M and N, two scale dtypes
-@pytest.mark.parametrize("variant", ["1", "d", "2", "o"])
+# 128 x 128 tiles (256 x 128 is the default at this size), "w" / "v" its
+# load-wave form with 4 / 3 stages, "d" the 16x16 DMA kernel, "2" its
+# 256 x 128 tiles, "o" the 16x16 kernel without DMA; ragged M and N, two
+# scale dtypes
+@pytest.mark.parametrize("variant", ["1", "w", "v", "d", "2", "o"])
 @pytest.mark.parametrize("M,K,N,G,s_dtype", [(300, 1024, 264, 8, torch.bfloat16),
                                              (520, 2048, 520, 16, torch.bfloat16),
                                              (97, 512, 136, 4, torch.float32)])
@@ -491,4 +492,15 @@ def test_prefill_gemm_variants(variant, M, K, N, G, s_dtype):
     xd, wd, sd, bd = gpu(x, wp, s, b)
     with C.tuning(ZT_WOQ_FORCE_KERNEL="gemm", ZT_WOQ_GEMM=variant):
         y = C.woq_linear(xd, wd, sd, None, bd)
+    check_close(y, y_ref)
+
+
+# the default prefill dispatch at one round of 256 x 128 tiles (128 tiles
+# here) takes the load-wave kernel
+def test_prefill_one_round_default_kernel():
+    M, K, N, G = 2048, 256, 2048, 2
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=11, bias=True)
+    y_ref = O.woq_linear(x, wp, s, bias=b)
+    xd, wd, sd, bd = gpu(x, wp, s, b)
+    y = C.woq_linear(xd, wd, sd, None, bd)
     check_close(y, y_ref)

@@ -24,11 +24,12 @@
 //    x in registers and the next units' weights in flight.
 //  * woq_decode_kernel   the older decode kernel for shapes the two above do
 //    not take (long K split over workgroups, general dequant modes).
-//  * woq_gemm32_kernel / woq_gemm_dma_kernel  prefill (more rows): LDS tiles
-//    moved by DMA, int4 dequantised in registers after the LDS read, bf16
-//    MFMA (32x32x16 for signed int4 with bf16 scales, 16x16x32 for the
-//    other modes); woq_gemm_kernel for group sizes that are not multiples
-//    of 128.
+//  * woq_gemm32_kernel / woq_gemm_ws_kernel / woq_gemm_dma_kernel  prefill
+//    (more rows): LDS tiles moved by DMA, int4 dequantised in registers
+//    after the LDS read, bf16 MFMA (32x32x16 for signed int4 with bf16
+//    scales -- with load waves of their own when one round of tiles covers
+//    the matrix -- 16x16x32 for the other modes); woq_gemm_kernel for group
+//    sizes that are not multiples of 128.
 //  * woq_generic_kernel  what none of the above takes (K not a multiple of
 //    64, odd group sizes): one wave per output element.
 //
@@ -660,13 +661,13 @@ constexpr size_t woq_dma_lds() {
 
 // Epilogue of ROWS x BN fp32 outputs staged in LDS (row pitch BN + 4) for
 // rows m0.. and columns n0..: bias, post-ops, then rows of four columns per
-// thread (8-byte bf16 stores where the row allows), 256 threads.
-template <int ROWS, int BN>
+// thread (8-byte bf16 stores where the row allows), NT threads.
+template <int ROWS, int BN, int NT = 256>
 __device__ __forceinline__ void woq_tile_epilogue(const WoqArgs &a, const float *tile, int m0,
                                                   int n0, int tid) {
   constexpr int TP = BN + 4;
   const int M = (int)a.M, N = (int)a.N;
-  for (int idx = tid; idx < ROWS * (BN / 4); idx += 256) {
+  for (int idx = tid; idx < ROWS * (BN / 4); idx += NT) {
     const int row = idx / (BN / 4), c4 = (idx % (BN / 4)) * 4;
     const int m = m0 + row, n = n0 + c4;
     if (m >= M || n >= N) continue;
@@ -854,6 +855,12 @@ void woq_gemm_dma_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int c
 // the tile (the rows of the waves with wm == h) as fp32 [m][n] at a time.
 constexpr int kW32BK = 64;
 
+// s_waitcnt immediate that waits for at most n outstanding vector-memory
+// operations (n < 64) and nothing else
+__host__ __device__ constexpr int vmcnt_imm_woq(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
 template <int BM, int BN>
 constexpr size_t woq_gemm32_stage() {
   return (size_t)BM * 128 + (size_t)BN * 32 + 1024;
@@ -1000,6 +1007,175 @@ void woq_gemm32_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg
     woq_tile_epilogue<BM / 2, BN>(a, tile, m0 + h * (BM / 2), n0, tid);
     __syncthreads();
   }
+}
+
+// The same tile with the loads in waves of their own (as s8_gemm_ws_kernel
+// does for int8): four compute waves (128 x 64 each) only read LDS, dequantise
+// and issue MFMAs; four load waves move the S-stage [x | W | scales] slabs
+// by DMA, S - 1 steps ahead, one workgroup per CU.  A load wave waits only
+// for its own loads (in-order vmcnt); one s_barrier per step.  Every load
+// wave issues the same number of loads per step (the last ones out of range
+// into a spare 1 KB of LDS), so the wait count is one immediate.
+template <int BM, int BN, int S>
+constexpr size_t woq_gemm_ws_lds() {
+  const size_t stages = (size_t)S * woq_gemm32_stage<BM, BN>() + 1024;
+  const size_t half = (size_t)(BM / 2) * (BN + 4) * 4;
+  return stages > half ? stages : half;
+}
+
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void woq_gemm_ws_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg_shift,
+                        int gmask) {
+  constexpr int WTM = BM / 64, WTN = BN / 64;  // 32 x 32 tiles per compute wave
+  constexpr int STAGE = (int)woq_gemm32_stage<BM, BN>();
+  constexpr int XI = BM / 8;          // 1 KB x loads (8 rows) per stage
+  constexpr int WI = BN / 32;         // 1 KB weight loads (32 rows)
+  constexpr int LOADS = XI + WI + 1;  // + the scale row
+  constexpr int LPW = (LOADS + 3) / 4;
+  static_assert((S - 2) * LPW <= 63 && S >= 2 && BN % 64 == 0 && BM % 64 == 0, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = xcd_contiguous_tile(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group, tg = t - g * per_group;
+  const int gm = min(group_m, tiles_m - g * group_m);
+  const int tm = g * group_m + tg % gm, tn = tg / gm;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = K / kW32BK;
+
+  f32x16_t acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  if (wv >= 4) {
+    // load wave dw issues loads li = dw + 4 q (q < LPW): x rows, weight
+    // rows, the scale row, then out-of-range fillers into the spare 1 KB
+    const int dw = wv - 4;
+    const int ldx2 = (int)a.ldx * 2, KB = K / 2;
+    const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)M * ldx2));
+    const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KB));
+    const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
+    auto dma = [&](int step) {
+      const int k0 = step * kW32BK;
+      const bool in = step < nk;
+      unsigned char *stage = smem + (step % S) * STAGE;
+#pragma unroll
+      for (int q = 0; q < LPW; ++q) {
+        const int li = dw + 4 * q;
+        if (li < XI) {
+          const int row = li * 8 + (lane >> 3);
+          const int chunk = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+          const uint32_t off = in && m0 + row < M
+                                   ? (uint32_t)((m0 + row) * ldx2 + k0 * 2 + chunk * 16) : kOobOffset;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(stage + li * 1024), 16, off, 0, 0, 0);
+        } else if (li < XI + WI) {
+          const int wi = li - XI;
+          const int row = wi * 32 + (lane >> 1);
+          const int half = (lane & 1) ^ ((row >> 3) & 1);
+          const uint32_t off = in && n0 + row < N
+                                   ? (uint32_t)((n0 + row) * KB + k0 / 2 + half * 16) : kOobOffset;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (lds_ptr_t)(stage + BM * 128 + wi * 1024), 16,
+                                                   off, 0, 0, 0);
+        } else if (li == XI + WI) {
+          // N % 8 == 0 (host-checked): a lane's 8 scales lie wholly inside or past N
+          const uint32_t grp = (uint32_t)(((k0 >> 7) >> cpg_shift) & gmask);
+          const uint32_t off = in && lane < BN / 8 && n0 + 8 * lane < N
+                                   ? (grp * (uint32_t)N + (uint32_t)(n0 + 8 * lane)) * 2u
+                                   : kOobOffset;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rs, (lds_ptr_t)(stage + BM * 128 + BN * 32), 16,
+                                                   off, 0, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rs, (lds_ptr_t)(smem + S * STAGE), 16,
+                                                   kOobOffset, 0, 0, 0);
+        }
+      }
+    };
+#pragma unroll
+    for (int p = 0; p < S - 1; ++p) dma(p);
+    for (int ks = 0; ks < nk; ++ks) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm_woq((S - 2) * LPW));  // this wave's loads of step ks
+      asm volatile("s_barrier" ::: "memory");
+      dma(ks + S - 1);  // into the stage step ks - 1 used; past the end: zeros
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  } else {
+    const int wm = wv >> 1, wn = wv & 1;
+    const int hl = lane >> 5, l32 = lane & 31;
+    for (int ks = 0; ks < nk; ++ks) {
+      asm volatile("s_barrier" ::: "memory");
+      const unsigned char *stage = smem + (ks % S) * STAGE;
+      u32x4_t wq[WTN];
+      float sc[WTN];
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        const int row = wn * (BN / 2) + j * 32 + l32;
+        wq[j] = *reinterpret_cast<const u32x4_t *>(stage + BM * 128 + row * 32 +
+                                                   ((hl ^ ((row >> 3) & 1)) * 16));
+        sc[j] = bf16_bits_to_f32(
+            *reinterpret_cast<const uint16_t *>(stage + BM * 128 + BN * 32 + row * 2));
+      }
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int chunk = 4 * hl + sub;
+        bf16x8_t xb[WTM];
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+          const int row = wm * (BM / 2) + i * 32 + l32;
+          xb[i] = *reinterpret_cast<const bf16x8_t *>(stage + row * 128 +
+                                                      ((chunk ^ ((row ^ (row >> 3)) & 7)) * 16));
+        }
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+          const bf16x8_t wb = dq_word<kDecFast>(wq[j][sub], sc[j], 0.f, 0);
+#pragma unroll
+          for (int i = 0; i < WTM; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb, xb[i], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // epilogue in two halves of BM/2 rows, all eight waves
+  __syncthreads();
+  constexpr int TP = BN + 4;
+  float *tile = reinterpret_cast<float *>(smem);
+  const int wm = wv >> 1, wn = wv & 1, hl = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (wv < 4 && wm == h) {
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4_t *>(tile + (i * 32 + l32) * TP + wn * (BN / 2) + j * 32 + 8 * q +
+                                         4 * hl) =
+                f32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+    woq_tile_epilogue<BM / 2, BN, 512>(a, tile, m0 + h * (BM / 2), n0, tid);
+    __syncthreads();
+  }
+}
+
+template <int BM, int BN, int S>
+static hipError_t launch_woq_gemm_ws_t(const WoqArgs &a, hipStream_t s, int shift, int gmask) {
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int group_m = tiles_m < 4 ? tiles_m : 4;
+  woq_gemm_ws_kernel<BM, BN, S><<<dim3((unsigned)(tiles_m * tiles_n)), dim3(512),
+                                  woq_gemm_ws_lds<BM, BN, S>(), s>>>(a, tiles_m, tiles_n, group_m,
+                                                                     shift, gmask);
+  return hipGetLastError();
 }
 
 template <int BM, int BN>
@@ -1842,9 +2018,6 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
 // of the wave's 32 and token 32*j + l%32.  With one K split the workgroup
 // applies the epilogue; with several it writes fp32 partials
 // [split][M][N], which woq_splitk_reduce_kernel adds in split order.
-__host__ __device__ constexpr int vmcnt_imm_woq(int n) {
-  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
-}
 
 constexpr int kWideKP = 512;    // k per phase
 constexpr int kWideRows = 128;  // weight rows per workgroup
@@ -2316,7 +2489,7 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
                     (a.G == 1 || (gs % 128 == 0 && (cpg & (cpg - 1)) == 0)) &&
                     a.M * a.ldx * 2 < (int64_t)kOobOffset &&
                     a.N * (a.K / 2) < (int64_t)kOobOffset;
-    const char *e = knob(kKnobWoqGemm);  // "old" disables, "128" forces 128x128
+    const char *e = knob(kKnobWoqGemm);  // o: 16x16, d: 16x16 DMA, 1: 128x128, 2, w / v: load waves
     if (ok && !(e && e[0] == 'o')) {
       int shift = 0;
       while (cpg > 1 && (1 << shift) < cpg) ++shift;
@@ -2327,7 +2500,16 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
       // 16-byte pieces
       if (mode == kDecFast && a.N % 8 == 0 && !(e && e[0] == 'd') &&
           (int64_t)a.G * a.N * 2 < (int64_t)kOobOffset) {
+        // one round of 256 x 128 tiles (at most one per CU): the load-wave
+        // kernel, whose deeper prefetch is then not paid for by an epilogue
+        // that a second workgroup per CU would hide (O and down at M = 2048:
+        // 104 -> 81 and 327 -> 255 us); more rounds: two workgroups per CU
+        // (QKV 141 against 149, gate_up 508 against 549 us)
         const bool big32 = e ? e[0] != '1' : t256 >= 128;
+        const bool ws = e ? e[0] == 'w' || e[0] == 'v' : t256 >= 128 && t256 <= 256;
+        if (ws)
+          return e && e[0] == 'w' ? launch_woq_gemm_ws_t<256, 128, 4>(a, s, shift, gmask)
+                                  : launch_woq_gemm_ws_t<256, 128, 3>(a, s, shift, gmask);
         return big32 ? launch_woq_gemm32_t<256, 128>(a, s, shift, gmask)
                      : launch_woq_gemm32_t<128, 128>(a, s, shift, gmask);
       }
