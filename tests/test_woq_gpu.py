@@ -479,10 +479,11 @@ def test_persist_kernel_gate_up_strided_x():
 
 # every prefill GEMM variant by name (ZT_WOQ_GEMM): "1" the 32x32 kernel with
 # 128 x 128 tiles (256 x 128 is the default at this size), "w" / "v" its
-# load-wave form with 4 / 3 stages, "d" the 16x16 DMA kernel, "2" its
+# load-wave form with 4 / 3 stages, "x" with 256 x 192 tiles (ragged in N
+# here), "d" the 16x16 DMA kernel, "2" its
 # 256 x 128 tiles, "o" the 16x16 kernel without DMA; ragged M and N, two
 # scale dtypes
-@pytest.mark.parametrize("variant", ["1", "w", "v", "d", "2", "o"])
+@pytest.mark.parametrize("variant", ["1", "w", "v", "x", "d", "2", "o"])
 @pytest.mark.parametrize("M,K,N,G,s_dtype", [(300, 1024, 264, 8, torch.bfloat16),
                                              (520, 2048, 520, 16, torch.bfloat16),
                                              (97, 512, 136, 4, torch.float32)])
@@ -500,6 +501,17 @@ def test_prefill_gemm_variants(variant, M, K, N, G, s_dtype):
 def test_prefill_one_round_default_kernel():
     M, K, N, G = 2048, 256, 2048, 2
     x, q, wp, s, z, b = make_case(M, K, N, G, seed=11, bias=True)
+    y_ref = O.woq_linear(x, wp, s, bias=b)
+    xd, wd, sd, bd = gpu(x, wp, s, b)
+    y = C.woq_linear(xd, wd, sd, None, bd)
+    check_close(y, y_ref)
+
+
+# 256 x 192 tiles by default where they make one round and 256 x 128 do not:
+# 9 x 24 = 216 tiles of 256 x 192 against 9 x 36 = 324 of 256 x 128 (ragged M)
+def test_prefill_one_round_192_default_kernel():
+    M, K, N, G = 2100, 256, 4608, 2
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=12, bias=True)
     y_ref = O.woq_linear(x, wp, s, bias=b)
     xd, wd, sd, bd = gpu(x, wp, s, b)
     y = C.woq_linear(xd, wd, sd, None, bd)

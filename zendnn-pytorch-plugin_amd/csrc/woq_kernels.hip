@@ -2489,7 +2489,7 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
                     (a.G == 1 || (gs % 128 == 0 && (cpg & (cpg - 1)) == 0)) &&
                     a.M * a.ldx * 2 < (int64_t)kOobOffset &&
                     a.N * (a.K / 2) < (int64_t)kOobOffset;
-    const char *e = knob(kKnobWoqGemm);  // o: 16x16, d: 16x16 DMA, 1: 128x128, 2, w / v: load waves
+    const char *e = knob(kKnobWoqGemm);  // o: 16x16, d: 16x16 DMA, 1: 128x128, 2, w / v / x: load waves
     if (ok && !(e && e[0] == 'o')) {
       int shift = 0;
       while (cpg > 1 && (1 << shift) < cpg) ++shift;
@@ -2503,10 +2503,14 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
         // one round of 256 x 128 tiles (at most one per CU): the load-wave
         // kernel, whose deeper prefetch is then not paid for by an epilogue
         // that a second workgroup per CU would hide (O and down at M = 2048:
-        // 104 -> 81 and 327 -> 255 us); more rounds: two workgroups per CU
-        // (QKV 141 against 149, gate_up 508 against 549 us)
+        // 104 -> 81 and 327 -> 255 us); when 256 x 192 tiles make one round
+        // where 256 x 128 do not, those (QKV: 152 -> 112 us); more rounds:
+        // two workgroups per CU (gate_up 508 against 549 us with 256 x 128)
         const bool big32 = e ? e[0] != '1' : t256 >= 128;
         const bool ws = e ? e[0] == 'w' || e[0] == 'v' : t256 >= 128 && t256 <= 256;
+        const int64_t t192 = ((a.M + 255) / 256) * ((a.N + 191) / 192);
+        const bool ws192 = e ? e[0] == 'x' : t256 > 256 && t192 <= 256;
+        if (ws192) return launch_woq_gemm_ws_t<256, 192, 3>(a, s, shift, gmask);
         if (ws)
           return e && e[0] == 'w' ? launch_woq_gemm_ws_t<256, 128, 4>(a, s, shift, gmask)
                                   : launch_woq_gemm_ws_t<256, 128, 3>(a, s, shift, gmask);

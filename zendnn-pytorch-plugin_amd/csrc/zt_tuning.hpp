@@ -14,7 +14,7 @@ enum Knob {
   kKnobWoqDecodePlan,   // ZT_WOQ_DECODE_PLAN: "NK,NT,CPW,TPW" of the decode kernel
   kKnobWoqStream,       // ZT_WOQ_STREAM: "0" disables, "NW,CPW,TPW" forces a shape
   kKnobWoqWide,         // ZT_WOQ_WIDE: "0" disables, "KS" forces the K-split count
-  kKnobWoqGemm,         // ZT_WOQ_GEMM: "o" 16x16 kernel, "d" 16x16 DMA, "1" 128x128, "w" / "v" load-wave kernel (4 / 3 stages)
+  kKnobWoqGemm,         // ZT_WOQ_GEMM: "o" 16x16 kernel, "d" 16x16 DMA, "1" 128x128, "w" / "v" / "x" load-wave kernel (4 / 3 stages, 256x192)
   kKnobWoqDebug,        // ZT_WOQ_DEBUG: print each launch shape to stderr
   kKnobWoqWave,         // ZT_WOQ_WAVE: "0" disables the wave-independent decode kernel
   kKnobWoqPersist,      // ZT_WOQ_PERSIST: "0" never, "1" / "2" force the persistent decode kernel (8 / 16 waves)
