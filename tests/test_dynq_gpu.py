@@ -211,12 +211,15 @@ def test_dynamic_qlinear_fragment_kernel_post_ops(post):
 
 
 # the large-M kernels by name: the load-wave kernel (default, also with its
-# 128 x 128 tiles: ZT_S8_TILE 1 / 0) and the kernels it replaced (n: 32x32
+# 128 x 128 tiles: ZT_S8_TILE 1 / 0, and 256 x 192: 9) and the kernels it replaced (n: 32x32
 # DMA, r: register-staged, 2 / 3: 16x16 DMA with 2 / 3 stages), on ragged
 # shapes (M, N past a tile, K not a multiple of the 128-byte step)
-@pytest.mark.parametrize("kind", ["w", "w1", "w0", "n", "r", "2", "3"])
+@pytest.mark.parametrize("kind", ["w", "w1", "w0", "w9", "n", "r", "2", "3"])
 @pytest.mark.parametrize("M,N,K", [(257, 200, 144), (520, 4160, 272), (2100, 130, 2064),
-                                   (512, 384, 4096)])
+                                   (512, 384, 4096),
+                                   # 216 tiles of 256 x 192, 324 of 256 x 128: the
+                                   # default takes 256 x 192
+                                   (2100, 4608, 272)])
 def test_s8_large_m_kernels_bit_exact(kind, M, N, K, knobs):
     knobs.set("ZT_S8_KIND", kind[0])
     if len(kind) > 1:

@@ -429,18 +429,21 @@ __device__ __forceinline__ void s8_tile_epilogue(const DynArgs &a, const int32_t
                                                  const float *sx_l, int m0, int n0, int tid) {
   constexpr int AP = acc_pitch<BN>();
   constexpr int G4 = BN / 4;
-  static_assert(NT % G4 == 0, "four-column groups must divide the threads");
+  // the first NTE threads keep the same four columns for all their rows
+  // (NT / G4 rows at a time); the rest of the threads sit this loop out
+  constexpr int NTE = NT / G4 * G4;
+  static_assert(NTE > 0, "four-column groups must fit the threads");
   const int M = (int)a.M, N = (int)a.N;
   const int c4 = (tid % G4) * 4, n = n0 + c4;
   if ((a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32) && a.post.count == 0 && (N & 3) == 0) {
-    if (n >= N) return;
+    if (n >= N || tid >= NTE) return;
     float sw[4], b[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       sw[r] = wscale(a, n + r);
       b[r] = a.bias ? load_elem(a.bias, a.b_dt, n + r) : 0.f;
     }
-    for (int row = tid / G4; row < BM && m0 + row < M; row += NT / G4) {
+    for (int row = tid / G4; row < BM && m0 + row < M; row += NTE / G4) {
       const int m = m0 + row;
       i32x4_t v = *reinterpret_cast<const i32x4_t *>(tile + row * AP + c4);
       if (a.azp) v = asym_fix4(a, m, n, v);
@@ -941,10 +944,16 @@ hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
 // threads finish it (s8_tile_epilogue).
 constexpr int kWsBK = 128;
 
+// tiles wider than 128 columns stage their int32 epilogue tile in two halves
+// of BM/2 rows
+template <int BN>
+constexpr bool s8_ws_half() { return BN > 128; }
+
 template <int BM, int BN, int S>
 constexpr size_t s8_ws_lds() {
   const size_t stages = (size_t)S * (BM + BN) * kWsBK;
-  const size_t tile = (size_t)BM * acc_pitch<BN>() * 4 + (size_t)BM * 4;
+  constexpr int R = s8_ws_half<BN>() ? BM / 2 : BM;
+  const size_t tile = (size_t)R * acc_pitch<BN>() * 4 + (size_t)R * 4;
   return stages > tile ? stages : tile;
 }
 
@@ -968,27 +977,26 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
   const int m0 = tm * BM, n0 = tn * BN;
   const int nk = (K + kWsBK - 1) / kWsBK;
+  // the accumulators are set (zeroed) only on the compute waves' path, so
+  // the load waves' loop does not hold their registers
   i32x16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
   const int wm = wv / WN, wn = wv % WN;
   if (wv >= NC) {
     // load wave: rows (dw * LPW + q) * 8 + lane / 8 of the [A | B] slab
     const int dw = wv - NC;
     const auto a_rs = make_rsrc(a.qx, (uint32_t)((int64_t)M * K));
     const auto b_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+    // the 16-byte chunk of row (dw * LPW + q) * 8 + lane / 8 this lane moves
+    auto chunk = [&](int q) {
+      const int row = (dw * LPW + q) * 8 + (lane >> 3);
+      return ((lane & 7) ^ ((row >> 1) & 7)) * 16;
+    };
     uint32_t src[LPW];
-    int chunk[LPW];
 #pragma unroll
     for (int q = 0; q < LPW; ++q) {
       const int row = (dw * LPW + q) * 8 + (lane >> 3);
-      chunk[q] = ((lane & 7) ^ ((row >> 1) & 7)) * 16;
-      if (row < BM) src[q] = m0 + row < M ? (uint32_t)((m0 + row) * K + chunk[q]) : kOobOffset;
-      else src[q] = n0 + row - BM < N ? (uint32_t)((n0 + row - BM) * K + chunk[q]) : kOobOffset;
+      if (row < BM) src[q] = m0 + row < M ? (uint32_t)((m0 + row) * K + chunk(q)) : kOobOffset;
+      else src[q] = n0 + row - BM < N ? (uint32_t)((n0 + row - BM) * K + chunk(q)) : kOobOffset;
     }
     auto dma = [&](int step) {
       const int k0 = step * kWsBK;
@@ -996,7 +1004,7 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
 #pragma unroll
       for (int q = 0; q < LPW; ++q) {
         // K % 16 == 0: a 16-byte chunk lies wholly inside or past its row
-        const uint32_t off = (src[q] == kOobOffset || step >= nk || k0 + chunk[q] >= K)
+        const uint32_t off = (src[q] == kOobOffset || step >= nk || k0 + chunk(q) >= K)
                                  ? kOobOffset : src[q] + (uint32_t)k0;
         lds_ptr_t dst = (lds_ptr_t)(stage + (dw * LPW + q) * 1024);
         if ((dw * LPW + q) * 8 < BM)  // whole loads lie in A or in B
@@ -1016,6 +1024,12 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
   } else {
     // compute wave: fragments of row R = lane % 32 (+ tile offsets), k
     // block 2 * sub + lane / 32 of the 128-byte step
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
     const int fsw = (lane >> 1) & 7;
     const int a_base = (wm * (BM / WM) + (lane & 31)) * kWsBK;
     const int b_base = (BM + wn * (BN / WN) + (lane & 31)) * kWsBK;
@@ -1030,6 +1044,41 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
       for (int j = 0; j < TN; ++j)
         Fb[buf][j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kWsBK + pos);
     };
+    if constexpr (TN > 2) {
+      // twelve accumulator tiles leave registers for one set of B
+      // fragments: B[j] of the next sub-step is read as soon as the TM
+      // MFMAs of this sub-step that use it are issued, under the MFMAs of
+      // the following j; A stays double-buffered
+      auto read_a = [&](const int8_t *stage, int sub, int buf) {
+        const int pos = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          Fa[buf][i] = *reinterpret_cast<const i32x4_t *>(stage + a_base + i * 32 * kWsBK + pos);
+      };
+      auto read_b = [&](const int8_t *stage, int sub, int j) {
+        const int pos = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
+        Fb[0][j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kWsBK + pos);
+      };
+      for (int ks = 0; ks < nk; ++ks) {
+        asm volatile("s_barrier" ::: "memory");
+        const int8_t *stage = s8_smem + (ks % S) * STAGE;
+        read_a(stage, 0, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) read_b(stage, 0, j);
+#pragma unroll
+        for (int sub = 0; sub < kWsBK / 32; ++sub) {
+          if (sub + 1 < kWsBK / 32) read_a(stage, sub + 1, (sub + 1) & 1);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+              acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Fb[0][j], Fa[sub & 1][i],
+                                                                acc[i][j], 0, 0, 0);
+            if (sub + 1 < kWsBK / 32) read_b(stage, sub + 1, j);
+          }
+        }
+      }
+    } else
     for (int ks = 0; ks < nk; ++ks) {
       asm volatile("s_barrier" ::: "memory");
       read(ks, 0, 0);
@@ -1050,23 +1099,31 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
   // tile), then every thread finishes four columns of its rows
   __syncthreads();
   constexpr int AP = acc_pitch<BN>();
+  constexpr bool HALF = s8_ws_half<BN>();
+  static_assert(!HALF || WM == 2, "half-tile epilogue: one row half per wm");
+  constexpr int R = HALF ? BM / 2 : BM;  // rows staged at a time
   int32_t *tile = reinterpret_cast<int32_t *>(s8_smem);
-  float *sx_l = reinterpret_cast<float *>(tile + BM * AP);
-  if (wv < NC) {
+  float *sx_l = reinterpret_cast<float *>(tile + R * AP);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int h = 0; h < (HALF ? 2 : 1); ++h) {
+    if (h) __syncthreads();  // the first half's reads are done
+    if (wv < NC && (!HALF || wm == h)) {
+      const int rb = HALF ? 0 : wm * (BM / WM);
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<i32x4_t *>(tile + (wm * (BM / WM) + i * 32 + (lane & 31)) * AP +
-                                       wn * (BN / WN) + j * 32 + 8 * q + 4 * (lane >> 5)) =
-              i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                      acc[i][j][4 * q + 3]};
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<i32x4_t *>(tile + (rb + i * 32 + (lane & 31)) * AP +
+                                         wn * (BN / WN) + j * 32 + 8 * q + 4 * (lane >> 5)) =
+                i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]};
+    }
+    s8_stage_row_scales<R, NT>(a, sx_l, m0 + h * R, tid);
+    __syncthreads();
+    s8_tile_epilogue<R, BN, NT>(a, tile, sx_l, m0 + h * R, n0, tid);
   }
-  s8_stage_row_scales<BM, NT>(a, sx_l, m0, tid);
-  __syncthreads();
-  s8_tile_epilogue<BM, BN, NT>(a, tile, sx_l, m0, n0, tid);
 }
 
 template <int BM, int BN, int WM, int WN, int ND, int S>
@@ -1839,6 +1896,12 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
       // stages (two workgroups per CU)
       if (tile && tile[0] == '1') return launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s);
       if (tile && tile[0] == '0') return launch_s8_ws<128, 128, 2, 2, 4, 2>(a, s);
+      // 256 x 192 tiles (six compute waves of 128 x 64, two load waves, two
+      // stages) where they make one round and 256 x 128 tiles do not: QKV at
+      // M = 2048, 256 against 384 tiles, 69 -> 58.5 us
+      const int64_t t192 = ((a.M + 255) / 256) * ((a.N + 191) / 192);
+      const bool w192 = tile ? tile[0] == '9' : t256 > 256 && t192 <= 256;
+      if (w192) return launch_s8_ws<256, 192, 2, 3, 2, 2>(a, s);
       return launch_s8_ws<256, 128, 2, 2, 4, 3>(a, s);
     }
     if (kind[0] == 'n') {  // 32x32x32 kernel, S stages

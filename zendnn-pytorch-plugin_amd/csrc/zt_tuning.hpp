@@ -22,7 +22,7 @@ enum Knob {
   kKnobS8Skinny,        // ZT_S8_SKINNY: "TPW,PF,NW" of the 16-token skinny kernel
   kKnobS8Frag,          // ZT_S8_FRAG: "0" never, "1" from M = 1 (fragment-order qx)
   kKnobS8Force,         // ZT_S8_FORCE: t tiled, s skinny, o 16x16 kernel
-  kKnobS8Tile,          // ZT_S8_TILE: "2" 256 x 128 tiles, "1" 128 x 128, "0" 128 x 128 in 2 stages
+  kKnobS8Tile,          // ZT_S8_TILE: "2" 256 x 128 tiles, "9" 256 x 192, "1" 128 x 128, "0" 128 x 128 in 2 stages
   kKnobS8Kind,          // ZT_S8_KIND: w load-wave kernel (default), n 32x32 DMA kernel, r / 2 / 3 older kernels
   kKnobS8Split,         // ZT_S8_SPLIT: "0" disables the split-K skinny kernel, "2"-"4" its load depth
   kKnobMoeBn,           // ZT_MOE_BN: column tile of the MoE GEMMs
