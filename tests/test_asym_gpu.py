@@ -63,6 +63,7 @@ KERNEL_CASES = [
     (96, 1000, 768, {"ZT_S8_SPLIT": "3"}), (128, 11008, 4096, {"ZT_S8_SPLIT": "4"}),
     (200, 264, 512, {}),                                                # 16x16 kernel
     (300, 130, 144, {}), (2048, 512, 1024, {}), (1500, 600, 272, {}),   # load-wave kernel
+    (1500, 600, 272, {"ZT_S8_TILE": "9"}),                              # 256 x 192 tiles
     (2048, 512, 1024, {"ZT_S8_KIND": "n"}),                             # 32x32 DMA kernel
     (64, 100, 48, {"ZT_S8_FORCE": "o"}),                                # 16x16 kernel
     (5, 33, 12, {}),                                                     # generic (K % 16)

@@ -120,7 +120,10 @@ def test_qlinear_out_forms(variant):
 # generic)
 @pytest.mark.parametrize("M,N,K", [(1, 264, 512), (100, 520, 1024), (128, 1000, 2048),
                                    (40, 130, 256), (200, 264, 512), (2048, 512, 1024),
-                                   (5, 33, 12)])
+                                   (5, 33, 12),
+                                   # 216 tiles of 256 x 192: requantised outputs
+                                   # through the half-tile epilogue
+                                   (2100, 4608, 272)])
 @pytest.mark.parametrize("kind", ["u8_in_u8_out", "f32_zp_s8_out", "bf16_sym_bf16_out"])
 def test_qlinear_kernels(M, N, K, kind):
     in_dtype = {"u8_in_u8_out": torch.uint8, "f32_zp_s8_out": torch.float32,
