@@ -582,7 +582,8 @@ def secondary_rooflines(res):
         out.append({"workload": "config 3 int4: WOQ linear over the Llama-3-8B layer, M=2048",
                     "bound": "mfma", "achieved": round(d["TFLOPS"], 2), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(d["frac_bf16_peak"], 4),
-                    "kernels": "woq_gemm32_kernel", "layer_avg_us": round(d["s_per_layer"] * 1e6, 3)})
+                    "kernels": "woq_gemm_ws_kernel (qkv, o, down) + woq_gemm32_kernel (gate_up)",
+                    "layer_avg_us": round(d["s_per_layer"] * 1e6, 3)})
     for d in res.get("decode_layer", []):
         out.append({"workload": f"config 2: Llama-3-8B decode layer, M={d['M']}",
                     "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
@@ -593,7 +594,8 @@ def secondary_rooflines(res):
         out.append({"workload": "config 4: Mixtral int4 MoE FFN, 256 tokens, top-2",
                     "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(d["frac_hbm"], 4),
-                    "kernels": "moe_route + woq_moe_gemm x2 + moe_combine",
+                    "kernels": "moe_route + woq_moe_gemm_wide (gate_up) + woq_moe_gemm (down)"
+                               " + moe_combine",
                     "layer_avg_us": round(d["s_per_layer"] * 1e6, 3)})
     return out
 
