@@ -256,6 +256,45 @@ def test_dynamic_qlinear_op_under_graph_capture():
     torch.testing.assert_close(eager.cpu().float(), O.dynamic_qlinear(x, w, sw, b).float(), **TOL)
 
 
+# the prefill GEMM kernels under graph capture: int8 256 x 192 and 256 x 128
+# load-wave tiles, int4 load-wave 256 x 192 / 256 x 128 and the two-workgroup
+# 32x32 kernel; each replay runs on new activations copied into the captured
+# input and must equal an eager call on them, with other eager calls between
+@pytest.mark.parametrize("path,M,N,K", [("int8", 2100, 4608, 256), ("int8", 2048, 512, 1024),
+                                        ("int4", 2100, 4608, 256), ("int4", 2048, 2048, 256),
+                                        ("int4", 2100, 8192, 128)])
+def test_prefill_kernels_under_graph_capture(path, M, N, K):
+    if path == "int8":
+        x, w, sw, b = dyn_case(M, N, K, seed=N + K)
+        wd, sd, bd = w.to(DEV), sw.to(DEV), b.to(DEV)
+        op = lambda xx: dyn_op(xx, wd, sd, bd)
+        ref0 = O.dynamic_qlinear(x, w, sw, b)
+    else:
+        x, q, wp, s = woq_case(M, N, K, K // 128, seed=N + K)
+        wd, sd = wp.to(DEV).t(), s.to(DEV)
+        op = lambda xx: torch.ops.zentorch.zentorch_woq_linear(xx, wd, sd, None)
+        ref0 = O.woq_linear(x, wp, s)
+    xd = x.to(DEV)
+    eager = op(xd)
+    torch.testing.assert_close(eager.cpu().float(), ref0.float(), **TOL)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        op(xd)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_graph = op(xd)
+    for i in range(3):
+        xi = torch.randn(M, K, generator=torch.Generator().manual_seed(60 + i)).bfloat16()
+        xd.copy_(xi.to(DEV))
+        ref = op(xd.clone())
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, ref)
+
+
 # extension ops: dynamic qlinear with a fused silu * mul or residual add
 @pytest.mark.parametrize("M,N,K", [(4, 96, 256), (128, 11008, 4096), (300, 136, 1024),
                                    (2048, 512, 1024)])
