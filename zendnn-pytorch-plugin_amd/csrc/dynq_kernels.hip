@@ -940,8 +940,11 @@ hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
 // previous step's reads, so its stage can be refilled.
 // LDS rows are 128 B; the 16-byte chunk c of tile row R sits at
 // c ^ ((R >> 1) & 7), so the 16 rows one read pass touches hit 16 distinct
-// bank groups.  The epilogue stages the whole int32 tile in LDS and all
-// threads finish it (s8_tile_epilogue).
+// bank groups.  The epilogue stages the int32 tile in LDS (whole, or one
+// half of the rows at a time for tiles wider than 128 columns) and all
+// threads finish it (s8_tile_epilogue).  Waves three tiles wide (12
+// accumulator tiles) keep one set of B fragments, each reloaded right after
+// the MFMAs that use it.
 constexpr int kWsBK = 128;
 
 // tiles wider than 128 columns stage their int32 epilogue tile in two halves
