@@ -942,9 +942,7 @@ hipError_t launch_s8_dma(const DynArgs &a, hipStream_t s) {
 // c ^ ((R >> 1) & 7), so the 16 rows one read pass touches hit 16 distinct
 // bank groups.  The epilogue stages the int32 tile in LDS (whole, or one
 // half of the rows at a time for tiles wider than 128 columns) and all
-// threads finish it (s8_tile_epilogue).  Waves three tiles wide (12
-// accumulator tiles) keep one set of B fragments, each reloaded right after
-// the MFMAs that use it.
+// threads finish it (s8_tile_epilogue).
 constexpr int kWsBK = 128;
 
 // tiles wider than 128 columns stage their int32 epilogue tile in two halves
@@ -1047,41 +1045,6 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
       for (int j = 0; j < TN; ++j)
         Fb[buf][j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kWsBK + pos);
     };
-    if constexpr (TN > 2) {
-      // twelve accumulator tiles leave registers for one set of B
-      // fragments: B[j] of the next sub-step is read as soon as the TM
-      // MFMAs of this sub-step that use it are issued, under the MFMAs of
-      // the following j; A stays double-buffered
-      auto read_a = [&](const int8_t *stage, int sub, int buf) {
-        const int pos = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          Fa[buf][i] = *reinterpret_cast<const i32x4_t *>(stage + a_base + i * 32 * kWsBK + pos);
-      };
-      auto read_b = [&](const int8_t *stage, int sub, int j) {
-        const int pos = ((2 * sub + (lane >> 5)) ^ fsw) * 16;
-        Fb[0][j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kWsBK + pos);
-      };
-      for (int ks = 0; ks < nk; ++ks) {
-        asm volatile("s_barrier" ::: "memory");
-        const int8_t *stage = s8_smem + (ks % S) * STAGE;
-        read_a(stage, 0, 0);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) read_b(stage, 0, j);
-#pragma unroll
-        for (int sub = 0; sub < kWsBK / 32; ++sub) {
-          if (sub + 1 < kWsBK / 32) read_a(stage, sub + 1, (sub + 1) & 1);
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-              acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Fb[0][j], Fa[sub & 1][i],
-                                                                acc[i][j], 0, 0, 0);
-            if (sub + 1 < kWsBK / 32) read_b(stage, sub + 1, j);
-          }
-        }
-      }
-    } else
     for (int ks = 0; ks < nk; ++ks) {
       asm volatile("s_barrier" ::: "memory");
       read(ks, 0, 0);
