@@ -59,6 +59,7 @@ def test_colsum_exact():
 KERNEL_CASES = [
     (1, 264, 512, {}), (8, 258, 512, {}), (16, 512, 1024, {}),          # skinny 16-token
     (17, 264, 512, {}), (100, 520, 1024, {"ZT_S8_SPLIT": "0"}),         # skinny 32-token
+    (20, 64, 8192, {}), (45, 96, 1600, {}),
     (100, 520, 1024, {}), (128, 1032, 4096, {}), (65, 97, 256, {}),     # split-K
     (96, 1000, 768, {"ZT_S8_SPLIT": "3"}), (128, 11008, 4096, {"ZT_S8_SPLIT": "4"}),
     (200, 264, 512, {}),                                                # 16x16 kernel

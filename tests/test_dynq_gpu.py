@@ -130,10 +130,10 @@ def test_prefill_shape_accumulator_checksum():
 # 17..128 tokens run on the 32x32x32 skinny kernel over qx in fragment
 # order: ragged M inside the last 32-token tile, N not a multiple of the
 # 16-row weight tiles (an odd last tile pairs with zeros), K of one chunk
-# (waves with no chunks) up to 64.
+# (waves with no chunks) up to 64, and K of 8192 and of 25 64-k chunks.
 @pytest.mark.parametrize("M,K,N", [(17, 64, 50), (31, 320, 100), (32, 4096, 96),
                                    (33, 1024, 4100), (64, 448, 48), (100, 4096, 1000),
-                                   (128, 192, 47)])
+                                   (128, 192, 47), (20, 8192, 64), (45, 1600, 96)])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
 def test_dynamic_qlinear_fragment_kernel(M, K, N, x_dtype):
     x, w, sw, b = make(M, K, N, seed=7 * M + K + N, x_dtype=x_dtype)
