@@ -210,6 +210,22 @@ def test_dynamic_qlinear_fragment_kernel_post_ops(post):
     torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
 
 
+# post-ops in the large-M load-wave kernel's epilogue (the general path of
+# its tile epilogue), with 256 x 128 and 256 x 192 tiles
+@pytest.mark.parametrize("tile", ["2", "9"])
+@pytest.mark.parametrize("post", [("gelu_erf",), ("mul", "add"), ("silu", "mul")])
+def test_dynamic_qlinear_large_m_post_ops(tile, post, knobs):
+    M, K, N = 300, 272, 400
+    knobs.set("ZT_S8_TILE", tile)
+    x, w, sw, b = make(M, K, N, seed=17)
+    g = torch.Generator().manual_seed(19)
+    bufs = [torch.randn(M, N, generator=g).bfloat16() for p in post if p in ("add", "mul")]
+    y_ref = O.dynamic_qlinear(x, w, sw, b, post_ops=post, post_bufs=bufs)
+    y = C.dynamic_qlinear(x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV), post_ops=post,
+                          post_bufs=[t.to(DEV) for t in bufs]).cpu()
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
 # the large-M kernels by name: the load-wave kernel (default, also with its
 # 128 x 128 tiles: ZT_S8_TILE 1 / 0, and 256 x 192: 9) and the kernels it replaced (n: 32x32
 # DMA, r: register-staged, 2 / 3: 16x16 DMA with 2 / 3 stages), on ragged

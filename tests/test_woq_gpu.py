@@ -496,6 +496,24 @@ def test_prefill_gemm_variants(variant, M, K, N, G, s_dtype):
     check_close(y, y_ref)
 
 
+# post-ops in the prefill variants' epilogues: the 32x32 kernel ("1"), its
+# load-wave form with 256 x 128 and 256 x 192 tiles ("w", "x") and the
+# 16x16 DMA kernel ("2"), with bias, elementwise and binary post-ops
+@pytest.mark.parametrize("variant", ["1", "w", "x", "2"])
+@pytest.mark.parametrize("post,nbuf", [(("gelu_erf",), 0), (("mul", "add"), 2),
+                                       (("silu", "mul"), 1)])
+def test_prefill_variants_post_ops(variant, post, nbuf):
+    M, K, N, G = 300, 1024, 264, 8
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=23, bias=True)
+    g = torch.Generator().manual_seed(24)
+    bufs = [torch.randn(M, N, generator=g).to(x.dtype) for _ in range(nbuf)]
+    y_ref = O.woq_linear(x, wp, s, bias=b, post_ops=post, post_bufs=bufs)
+    xd, wd, sd, bd = gpu(x, wp, s, b)
+    with C.tuning(ZT_WOQ_FORCE_KERNEL="gemm", ZT_WOQ_GEMM=variant):
+        y = C.woq_linear(xd, wd, sd, None, bd, post_ops=post, post_bufs=gpu(*bufs))
+    check_close(y, y_ref)
+
+
 # the default prefill dispatch at one round of 256 x 128 tiles (128 tiles
 # here) takes the load-wave kernel
 def test_prefill_one_round_default_kernel():
