@@ -414,3 +414,38 @@ def test_gate_up_left_alone(cpu_passes, case):
     gm = trace(f, x, wp, s, b)
     run_passes(gm)
     assert counters["zentorch"]["zentorch_woq_linear_gate_up_silu_mul"] == 0
+
+
+def test_dynamic_token_count_compiles_once(monkeypatch):
+    # A graph compiled with dynamic shapes must serve every token count from
+    # one compile: reading the weights' compile-time values must not guard
+    # on the activations' symbolic sizes.
+    import torch._dynamo
+    from zentorch import _compile_backend
+
+    torch._dynamo.reset()
+    compiles = []
+    real = _compile_backend._compile_forward
+
+    def counting(gm, ex, inputs=()):
+        compiles.append(len(gm.graph.nodes))
+        return real(gm, ex, inputs)
+
+    monkeypatch.setattr(_compile_backend, "_compile_forward", counting)
+
+    class Lin(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.w = torch.nn.Parameter(torch.randn(32, 64), requires_grad=False)
+
+        def forward(self, x):
+            return torch.nn.functional.linear(x, self.w).relu()
+
+    m = Lin()
+    f = torch.compile(m, backend="zentorch", dynamic=True)
+    with torch.no_grad():
+        for M in (2, 3, 5, 7, 11, 13, 17, 19, 23, 29):
+            x = torch.randn(M, 64)
+            torch.testing.assert_close(f(x), torch.nn.functional.linear(x, m.w).relu())
+    assert len(compiles) == 1
+    torch._dynamo.reset()

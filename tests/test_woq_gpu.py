@@ -534,3 +534,49 @@ def test_prefill_one_round_192_default_kernel():
     xd, wd, sd, bd = gpu(x, wp, s, b)
     y = C.woq_linear(xd, wd, sd, None, bd)
     check_close(y, y_ref)
+
+
+# the lean decode kernel (fast mode, M <= 16, K = 8 waves x 2 / 4 / 8 / 14
+# chunks, x whole in LDS; forced by ZT_WOQ_LEAN=1, as the library takes it
+# only for the shapes where it measured faster): group sizes 128 / 256 /
+# 1024 and per channel, ragged N, every M up to 16, and the same result as
+# the other decode kernels on these shapes
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 13, 16])
+@pytest.mark.parametrize("K,N,G", [(2048, 16, 16), (4096, 4096, 32), (4096, 1000, 16),
+                                   (8192, 256, 8), (8192, 112, 1), (14336, 4096, 112)])
+def test_lean_kernel_vs_oracle(M, K, N, G, knobs):
+    if M * (K + 8) * 2 > 160 * 1024:
+        pytest.skip("x does not fit the lean kernel's LDS (the other kernels take it)")
+    knobs.set("ZT_WOQ_LEAN", "1")
+    y, y_ref = run_case(M, K, N, G, seed=M * 7 + G)
+    knobs.set("ZT_WOQ_LEAN", "0")
+    y_other, _ = run_case(M, K, N, G, seed=M * 7 + G)
+    check_close(y, y_other.cpu())
+
+
+@pytest.mark.parametrize("post,nbuf", [(("relu",), 0), (("gelu_tanh",), 0), (("add",), 1),
+                                       (("mul", "add"), 2)])
+def test_lean_kernel_post_ops(post, nbuf, knobs):
+    knobs.set("ZT_WOQ_LEAN", "1")
+    run_case(3, 4096, 520, 32, post=post, nbuf=nbuf, seed=9, bias=True)
+
+
+def test_lean_kernel_strided_x(knobs):
+    knobs.set("ZT_WOQ_LEAN", "1")
+    M, K, N, G = 2, 14336, 256, 112
+    x, q, wp, s, z, b = make_case(M, K, N, G, seed=79)
+    xs = torch.randn(M, K + 64).bfloat16()
+    xs[:, :K] = x
+    y_ref = O.woq_linear(x, wp, s)
+    y = C.woq_linear(xs.to(DEV)[:, :K], wp.to(DEV), s.to(DEV))
+    check_close(y, y_ref)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("K,I,G", [(4096, 256, 32), (2048, 1040, 1), (8192, 64, 64)])
+def test_lean_kernel_gate_up(M, K, I, G, knobs):
+    knobs.set("ZT_WOQ_LEAN", "1")
+    y, y_ref = run_gate_up(M, K, I, G, seed=M + I + 2)
+    knobs.set("ZT_WOQ_LEAN", "0")
+    y_other, _ = run_gate_up(M, K, I, G, seed=M + I + 2)
+    check_close(y, y_other.cpu())

@@ -113,7 +113,7 @@ constexpr const char *kKnobNames[kKnobCount] = {
     "ZT_WOQ_GEMM",         "ZT_WOQ_DEBUG",       "ZT_WOQ_WAVE",    "ZT_WOQ_PERSIST",
     "ZT_S8_SKINNY32",      "ZT_S8_SKINNY",
     "ZT_S8_FRAG",          "ZT_S8_FORCE",        "ZT_S8_TILE",     "ZT_S8_KIND",
-    "ZT_S8_SPLIT",         "ZT_MOE_BN"};
+    "ZT_S8_SPLIT",         "ZT_MOE_BN",          "ZT_WOQ_LEAN"};
 
 // Values are interned copies that are never freed: a reader may hold an old
 // pointer while another thread replaces the value.

@@ -19,6 +19,11 @@
 //    meet in LDS.  The wave kernel gives every wave its own x slice and no
 //    barrier before the reduction; the stream kernel shares one x copy.
 //    Rows past what one launch holds go in blocks of 16.
+//  * woq_lean_kernel  1..16 rows in the fast mode where it measured faster
+//    (the long-K down projection and the widest matrices at few rows, the
+//    merged gate_up at 2..4 rows): the stream kernel's work split with each
+//    chunk's scales loaded beside its weights, x read only by the lanes of
+//    real tokens and two MFMA accumulators.
 //  * woq_persist_kernel  the merged gate_up at 9..16 rows and plain calls
 //    of 12288 rows or more: one workgroup per CU loops over row units with
 //    x in registers and the next units' weights in flight.
@@ -1904,6 +1909,213 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
   return hipGetLastError();
 }
 
+// ------------------------------------------------------ lean decode
+// The fast mode (signed int4, bf16 scales, bf16 x) at M <= 16 when K is
+// exactly NW * CPW 128-wide chunks and x [M, K] fits the LDS whole.  One
+// workgroup owns TPW 16-row tiles (or, with gu, a gate tile and its up
+// tile) over all of K; wave w owns the chunks [w * CPW, (w + 1) * CPW).
+//
+// Against the stream kernel, three things change and each was measured on
+// the Llama-3-8B decode shapes (graph replays over rotating weights):
+//  * a chunk's scale is loaded by each lane into a register right before
+//    the chunk's weights (one 2-byte load per lane per tile), so a chunk
+//    waits only for its own loads.  With the scales staged through LDS the
+//    workgroup barrier also waits for them; they come from HBM behind the
+//    weight requests of every other resident workgroup, so the dequant of
+//    most workgroups started only after nearly all weights had landed.
+//  * only the lanes of the M real token columns read x from LDS (the B
+//    columns past M keep the zeros they start with; their sums are never
+//    stored), so M = 1 reads 1/16 of the LDS bytes the replicated read did.
+//  * the four MFMAs of a chunk alternate between two accumulators, so
+//    consecutive MFMAs do not wait on each other's results.
+// Partials meet in LDS in wave order (deterministic), then the stream
+// kernel's epilogue (bias, post-ops, or silu(gate) * round(up) with gu).
+template <int NW, int CPW, int TPW>
+__global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_shift, int gmask,
+                                                           int gu) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
+  const int XP = stream_x_pitch(K);
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem);
+  // first weight row of tile t: TPW consecutive tiles, or with gu the gate
+  // rows j0.. (t = 0) and the up rows gu + j0.. (t = 1)
+  auto rowbase = [&](int t) {
+    return gu ? t * gu + blockIdx.x * 16 : (blockIdx.x * TPW + t) * 16;
+  };
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
+  const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
+  // 1. x [M, K] -> LDS by DMA, instruction i moving 1 KB of one row (the
+  //    host checks 16-byte rows and K % 512 == 0)
+  const int per_row = K / 512;
+  for (int i = wv; i < M * per_row; i += NW) {
+    const int m = i / per_row, q = i - m * per_row;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        x_rs, (lds_ptr_t)(xl + m * XP + q * 512), 16,
+        (uint32_t)(m * a.ldx * 2 + q * 1024 + lane * 16), 0, 0, 0);
+  }
+  // 2. per chunk and tile: the row's scale, then its 16 weight bytes (rows
+  //    past N are clamped; their results are never stored)
+  const int c0 = wv * CPW;
+  uint32_t sr[TPW][CPW];
+  u32x4_t wr[TPW][CPW];
+  auto load_chunk = [&](int c) {
+    const uint32_t g = (uint32_t)(((c0 + c) >> cpg_shift) & gmask);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int n = min(rowbase(t) + lr, N - 1);
+      sr[t][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, (g * (uint32_t)N + (uint32_t)n) * 2u,
+                                                      0, 0);
+      wr[t][c] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                       w_rs, (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u +
+                                 (uint32_t)(c0 + c) * 64u, 0, 0));
+    }
+  };
+  constexpr int D = CPW < 2 ? CPW : 2;
+#pragma unroll
+  for (int c = 0; c < D; ++c) load_chunk(c);
+  // this wave's x DMA was issued before its 2 * TPW * D loads: once at most
+  // those are outstanding it has landed; the barrier covers the other waves'
+  constexpr int after = 2 * TPW * D > 63 ? 63 : 2 * TPW * D;
+  __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("s_barrier" ::: "memory");
+
+  // 3. the chunks, each as its loads land; chunk c + D is requested first
+  u32x4_t xb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xb[i] = u32x4_t{0u, 0u, 0u, 0u};
+  f32x4_t acc[TPW][2];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    if (c + D < CPW) load_chunk(c + D);
+    const int kc = c0 + c;
+    if (lr < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xb[i] = *reinterpret_cast<const u32x4_t *>(xl + lr * XP + kc * 128 + 32 * lg + 8 * i);
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const float sc = __uint_as_float(sr[t][c] << 16);
+      const float s16 = sc * 0.0625f, k0 = -1032.f * sc, k1 = -72.f * sc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[t][i & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, dq8_s4_bf16scale(wr[t][c][i], sc, s16, k0, k1)),
+            __builtin_bit_cast(bf16x8_t, xb[i]), acc[t][i & 1], 0, 0, 0);
+    }
+  }
+
+  // 4. partial D[row = 4 lg + r][token = lr] of tile t -> slab[wave][t] (over
+  //    x, once every wave is done with it), then each output adds the NW
+  //    partials in wave order
+  __syncthreads();
+  float *slab = reinterpret_cast<float *>(smem);
+  if (lr < M) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][0][r] + acc[t][1][r];
+  }
+  __syncthreads();
+  if (gu) {
+    const int j0 = blockIdx.x * 16;
+    for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
+      const int m = idx >> 4, r16 = idx & 15;
+      const int j = j0 + r16;
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        g += slab[((w * TPW) * 16 + r16) * 17 + m];
+        u += slab[((w * TPW + 1) * 16 + r16) * 17 + m];
+      }
+      if (a.bias) {
+        g = g + load_elem(a.bias, a.b_dt, j);
+        u = u + load_elem(a.bias, a.b_dt, gu + j);
+      }
+      if (a.y_dt == ZT_DT_BF16) u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+      store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + j, unary_op(ZT_PO_SILU, g) * u);
+    }
+    return;
+  }
+  const int n0 = blockIdx.x * TPW * 16;
+  for (int idx = tid; idx < TPW * 16 * M; idx += 64 * NW) {
+    const int m = idx / (TPW * 16), nr = idx - m * (TPW * 16);
+    const int n = n0 + nr;
+    if (n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += slab[((w * TPW + (nr >> 4)) * 16 + (nr & 15)) * 17 + m];
+    if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
+    v = apply_post_ops(v, a.post, m, n);
+    store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + n, v);
+  }
+}
+
+template <int NW, int CPW, int TPW>
+static hipError_t launch_lean_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int gu) {
+  const size_t x = (size_t)a.M * stream_x_pitch((int)a.K) * 2;
+  const size_t slab = (size_t)NW * TPW * 16 * 17 * 4;
+  const unsigned blocks = gu ? (unsigned)(gu / 16) : (unsigned)((a.N + 16 * TPW - 1) / (16 * TPW));
+  woq_lean_kernel<NW, CPW, TPW><<<dim3(blocks), dim3(64 * NW), x > slab ? x : slab, s>>>(
+      a, shift, gmask, gu);
+  return hipGetLastError();
+}
+
+// Whether the lean kernel serves this call by default: the shapes where it
+// measured faster than the kernel the dispatch would otherwise take (graph
+// replays of the Llama-3-8B decode shapes over rotating weights, same
+// process); ZT_WOQ_LEAN "1" forces it wherever it applies, "0" never.
+// Measured (default dispatch -> lean kernel, one box): 4096 x 14336 at
+// M = 1 / 2 / 4 10.5 -> 9.9, 10.6 -> 10.2, 11.6 -> 10.7 us; 14336 x 4096
+// at M = 1 / 2 11.0 -> 9.9, 11.0 -> 10.1 us and at M = 12 / 16 (against
+// the persistent kernel) 28672 x 4096 25.2 -> 23.6, 25.3 -> 23.8 us;
+// the merged 28672 x 4096 gate_up at M = 2 / 4 18.4 -> 17.8, 19.4 ->
+// 18.6 us.  QKV, the merged gate_up at M = 1 and M >= 8, and most shapes
+// at M = 8 stay where they are (2-43 % slower on the lean kernel).
+static bool lean_preferred(const WoqArgs &a, int gu) {
+  if (gu) return a.M >= 2 && a.M <= 4;
+  if (a.K >= 8192) return a.M <= 4;
+  if (a.N >= 12288) return a.M <= 2 || (a.N >= 28672 && a.M >= 12);
+  return false;
+}
+
+// The lean kernel where it applies: fast mode, bf16 x with 16-byte rows,
+// M <= 16, K = 8 waves x CPW chunks (CPW 2, 4, 8 or 14), x within the LDS,
+// the index ranges within 32-bit buffer offsets; gu > 0 is the merged
+// gate_up (I = gu, a multiple of 16).
+static bool try_launch_lean(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
+                            int gu, hipError_t *err) {
+  const char *e = knob(kKnobWoqLean);  // "0" never, "1" wherever it applies
+  if (e && e[0] == '0') return false;
+  if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || a.K % 1024 ||
+      (gu && gu % 16) || !stream_x_dma(a, 1) || a.N * (a.K / 2) >= (int64_t)kOobOffset ||
+      a.G * a.N * 2 >= (int64_t)kOobOffset)
+    return false;
+  if ((size_t)a.M * stream_x_pitch((int)a.K) * 2 > kStreamLdsMax) return false;
+  if (!(e && e[0] == '1') && !lean_preferred(a, gu)) return false;
+  const int cpw = (int)(a.K / 1024);
+  if (knob(kKnobWoqDebug))
+    std::fprintf(stderr, "[zt] woq lean M=%lld N=%lld K=%lld gu=%d: NW=8 CPW=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, gu, cpw);
+#define ZT_LEAN_CASE(CPW_)                                                         \
+  if (cpw == CPW_) {                                                               \
+    *err = gu ? launch_lean_t<8, CPW_, 2>(a, s, shift, gmask, gu)                  \
+              : launch_lean_t<8, CPW_, 1>(a, s, shift, gmask, 0);                  \
+    return true;                                                                   \
+  }
+  ZT_LEAN_CASE(2) ZT_LEAN_CASE(4) ZT_LEAN_CASE(8) ZT_LEAN_CASE(14)
+#undef ZT_LEAN_CASE
+  return false;
+}
+
 // The weight-streaming kernel, when it applies: M <= 64 and x [M, K] (or,
 // in the fast mode, a 2-, 4- or 8-phase range of it) in at most
 // kStreamLdsMax of LDS.  Returns false when the caller should use another
@@ -1916,6 +2128,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
   // N take the general bf16-scale mode (same weights, same results)
   if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
+  if (!knob(kKnobWoqStream) && try_launch_lean(a, s, shift, gmask, mode, 0, err)) return true;
   if (!knob(kKnobWoqStream) && try_launch_persist(a, s, shift, gmask, mode, 0, err)) return true;
   if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, 0, err)) return true;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
@@ -2385,6 +2598,8 @@ bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   int shift = 0;
   while (cpg > 1 && (1 << shift) < cpg) ++shift;
   const int gmask = a.G == 1 ? 0 : 0x7fffffff;
+  if (!knob(kKnobWoqStream) && try_launch_lean(a, s, shift, gmask, kDecFast, (int)I, err))
+    return true;
   if (!knob(kKnobWoqStream) && try_launch_persist(a, s, shift, gmask, kDecFast, (int)I, err))
     return true;
   if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, kDecFast, (int)I, err))

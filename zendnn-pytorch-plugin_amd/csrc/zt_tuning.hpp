@@ -26,6 +26,7 @@ enum Knob {
   kKnobS8Kind,          // ZT_S8_KIND: w load-wave kernel (default), n 32x32 DMA kernel, r / 2 / 3 older kernels
   kKnobS8Split,         // ZT_S8_SPLIT: "0" disables the split-K skinny kernel, "2"-"4" its load depth
   kKnobMoeBn,           // ZT_MOE_BN: column tile of the MoE GEMMs
+  kKnobWoqLean,         // ZT_WOQ_LEAN: "0" never, "1" forces the lean decode kernel wherever it applies
   kKnobCount
 };
 

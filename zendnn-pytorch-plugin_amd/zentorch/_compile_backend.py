@@ -96,19 +96,29 @@ def _static_values(graph: torch.fx.Graph, weights: set, real_inputs: List[Any]) 
     """Real tensors of the weight placeholders: the forward graph's
     placeholders are the flattened inputs dynamo handed the backend, in
     order (inference, no lifted parameters); matched only when every shape
-    and dtype agrees."""
+    and dtype of the weight placeholders agrees.
+
+    Only weight placeholders are compared, and only those whose sizes are
+    plain ints: comparing a symbolic size (an activation's token count under
+    ``dynamic=True`` or automatic dynamic shapes) with a real one would
+    install a guard that specialises the graph to that count, so every new
+    token count would recompile."""
     ph = [n for n in graph.nodes if n.op == "placeholder"]
     if len(ph) != len(real_inputs):
         return {}
     out = {}
     for node, real in zip(ph, real_inputs):
+        if node not in weights:
+            continue
         val = node.meta.get("val", None)
         if not isinstance(real, torch.Tensor) or not isinstance(val, torch.Tensor):
             continue
-        if tuple(val.shape) != tuple(real.shape) or val.dtype != real.dtype:
+        shape = tuple(val.shape)
+        if not all(type(d) is int for d in shape):
+            continue
+        if shape != tuple(real.shape) or val.dtype != real.dtype:
             return {}
-        if node in weights:
-            out[node] = real
+        out[node] = real
     return out
 
 
