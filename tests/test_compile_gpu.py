@@ -214,23 +214,49 @@ def test_weight_cache_reuses_and_invalidates():
         assert not torch.equal(y3, y1)
 
 
-# Zero points: the rewrite drops them (symmetric int4, as the reference's
-# pattern does at _op_replacements_new.py:370,386), so it fires only when the
-# zero-point buffer is all zero at compile time.  A non-zero zero point keeps
-# the stock dequantise-then-matmul (correct, unrewritten); zero points that
-# change after compile are rejected at run time.
+# Zero points: with every zero point 0 at compile time the rewrite drops
+# them (symmetric int4, as the reference's pattern does at
+# _op_replacements_new.py:370,386), behind a run-time guard; integer zero
+# points that are not all zero are kept and run on the op's unsigned int4
+# path (u = w + 8 with zero points zp + 8; WOQ_Linear.cpp:44-49 selects u4
+# whenever zero points are given).
+@pytest.mark.parametrize("M", [1, 8, 33])
 @pytest.mark.parametrize("group_size", [None, 128])
-def test_nonzero_zero_points_not_rewritten(group_size):
-    M, N, K = 8, 256, 512
-    model = WoqLinear(N, K, group_size=group_size, seed=5)
+@pytest.mark.parametrize("bias", [False, True])
+def test_nonzero_zero_points_take_the_u4_kernels(M, group_size, bias):
+    N, K = 256, 512
+    model = WoqLinear(N, K, group_size=group_size, bias=bias, seed=5)
     g = torch.Generator().manual_seed(6)
-    model.zero_points.copy_(torch.randint(-2, 3, model.zero_points.shape, generator=g,
+    model.zero_points.copy_(torch.randint(-8, 8, model.zero_points.shape, generator=g,
                                           dtype=torch.int8))
     assert bool(model.zero_points.any())
     x = torch.randn(M, K).bfloat16()
     ref, out = compiled_vs_eager(model, x)
-    assert counters["zentorch"]["zentorch_woq_linear"] == 0
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
     torch.testing.assert_close(out.float(), ref.float(), **TOL)
+
+
+def test_nonzero_zero_points_cached_and_updated():
+    # the u4 packing and the zero points + 8 are made once per weight
+    # version; in-place updates of either are seen on the next call, and a
+    # weight that leaves [-8, 7] is refused rather than truncated
+    M, N, K = 4, 128, 256
+    model = WoqLinear(N, K, group_size=128, seed=9).to(DEV).eval()
+    model.zero_points.fill_(2)
+    x = torch.randn(M, K).bfloat16().to(DEV)
+    with torch.no_grad():
+        fn = torch.compile(model, backend="zentorch")
+        y1 = fn(x)
+        assert counters["zentorch"]["zentorch_woq_linear"] == 1
+        n = cache_size()
+        assert fn(x).equal(y1) and cache_size() == n
+        model.zero_points.fill_(-3)
+        torch.testing.assert_close(fn(x).float(), model(x.float()).float(), **TOL)
+        model.weight.copy_(-model.weight.clamp(min=-7))
+        torch.testing.assert_close(fn(x).float(), model(x.float()).float(), **TOL)
+        model.weight.fill_(9)
+        with pytest.raises(RuntimeError, match="int4"):
+            fn(x)
 
 
 def test_zero_points_changed_after_compile_rejected():

@@ -104,16 +104,17 @@ def test_dequant_matmul_replaced(cpu_passes, gs, bias):
     assert (len(node.args) > 4 and node.args[4] is not None) == bias
 
 
-@pytest.mark.parametrize("case", ["nonzero_zp", "unsigned_weights", "unknown_values"])
-def test_dequant_matmul_left_alone_unless_symmetric(cpu_passes, case):
-    # the rewrite drops the zero points, which is right only for all-zero
-    # zero points and weights in [-8, 7]; anything else stays stock PyTorch
+@pytest.mark.parametrize("case", ["unsigned_weights", "unknown_values", "zp_overflow"])
+def test_dequant_matmul_left_alone_unless_int4(cpu_passes, case):
+    # the rewrite packs int4: weights outside [-8, 7], values unknown at
+    # compile time, or zero points whose + 8 overflows their dtype stay
+    # stock PyTorch
     N, K = 64, 256
     w, zp, s = quantized(N, K)
-    if case == "nonzero_zp":
-        zp = torch.full_like(zp, 3)
-    elif case == "unsigned_weights":
+    if case == "unsigned_weights":
         w = torch.randint(0, 16, (N, K), dtype=torch.int8)
+    elif case == "zp_overflow":
+        zp = torch.full_like(zp, 125)
     x = torch.randn(4, K).bfloat16()
     gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s)), x, w, zp, s)
     if case == "unknown_values":
@@ -121,6 +122,64 @@ def test_dequant_matmul_left_alone_unless_symmetric(cpu_passes, case):
     t = run_passes(gm)
     assert counters["zentorch"]["zentorch_woq_linear"] == 0
     assert aten.mm.default in t and zt.zentorch_woq_linear.default not in t
+
+
+@pytest.mark.parametrize("gs", [None, 128])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("zp_dtype", [torch.int8, torch.int32])
+def test_nonzero_zero_points_take_the_u4_path(cpu_passes, gs, bias, zp_dtype):
+    # integer zero points that are not all zero are kept: the weight is
+    # packed as u = w + 8 and the op gets zp + 8 ([G, N]), no guard
+    from zentorch._optimize import zero_points_guard
+    N, K = 64, 256
+    w, zp, s = quantized(N, K, gs)
+    g = torch.Generator().manual_seed(3)
+    zp = torch.randint(-8, 8, zp.shape, generator=g).to(zp_dtype)
+    x = torch.randn(4, K).bfloat16()
+    b = torch.randn(N).bfloat16()
+    view = (N, K) if gs else None
+    if bias:
+        f = lambda x, w, zp, s, b: torch.addmm(b, x, dequant_t(w, zp, s, view))
+        gm = trace(f, x, w, zp, s, b)
+    else:
+        gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s, view)), x, w, zp, s)
+    t = run_passes(gm)
+    assert counters["zentorch"]["zentorch_woq_linear"] == 1
+    assert aten.mm.default not in t and aten.addmm.default not in t
+    assert zero_points_guard not in t
+    node = next(n for n in gm.graph.nodes if n.target == zt.zentorch_woq_linear.default)
+    zeros = node.args[3]
+    assert zeros is not None and zeros.target is aten.add.Tensor and zeros.args[1] == 8
+    assert tuple(zeros.meta["val"].shape) == ((K // gs) if gs else 1, N)
+    assert zeros.meta["val"].dtype == zp_dtype
+    packed = node.args[1]
+    while packed.target != zt.zentorch_woq_repack_weight.default:
+        packed = packed.args[0]
+    assert packed.args[0].target is aten.add.Tensor and packed.args[0].args[1] == 8
+
+
+@pytest.mark.parametrize("gs", [None, 64])
+def test_u4_rewrite_equals_the_dequantised_graph(gs):
+    # what the rewrite computes -- the op's unsigned int4 path on u = w + 8
+    # with zero points zp + 8 (the oracle, which the GPU kernels match) --
+    # against the graph it replaces, (bf16(w) - bf16(zp)) * s in bf16 and a
+    # matmul, in fp32 here
+    from oracle import oracle as O
+    N, K = 48, 256
+    w, zp, s = quantized(N, K, gs)
+    g = torch.Generator().manual_seed(5)
+    zp = torch.randint(-8, 8, zp.shape, generator=g, dtype=torch.int8)
+    x = torch.randn(3, K, generator=g).bfloat16()
+    dq = ((w.to(torch.bfloat16) - zp.to(torch.bfloat16)) * s).reshape(N, K)
+    ref = x.float() @ dq.float().t()
+    packed = O.woq_repack_weight((w.reshape(N, K) + 8).to(torch.int8))
+    scales = s.reshape(N, -1).t().contiguous()
+    zeros = (zp.reshape(N, -1) + 8).t().contiguous()
+    y = O.woq_linear(x, packed, scales, zero_points=zeros)
+    torch.testing.assert_close(y.float(), ref, rtol=1e-2, atol=1e-2)
+    # the symmetric s4 packing of the same weight would differ whenever zp != 0
+    y_s4 = O.woq_linear(x, O.woq_repack_weight(w.reshape(N, K)), scales)
+    assert not torch.allclose(y_s4.float(), ref, rtol=1e-2, atol=1e-2)
 
 
 def test_zero_point_guard_inserted_and_checked(cpu_passes):
@@ -132,12 +191,22 @@ def test_zero_point_guard_inserted_and_checked(cpu_passes):
     run_passes(gm)
     guards = [n for n in gm.graph.nodes if n.target is zero_points_guard]
     assert len(guards) == 1 and guards[0].args[0].name == "zp_1"
+    assert guards[0].args[1].name == "w_1"  # the weight it assumed in [-8, 7]
     gm.graph.eliminate_dead_code()  # the guard has no users and must survive
     assert any(n.target is zero_points_guard for n in gm.graph.nodes)
-    zero_points_guard(zp)  # all zero: passes
+    zero_points_guard(zp, w)  # all zero, weight in range: passes
     zp.add_(1)
     with pytest.raises(RuntimeError, match="zero points"):
-        zero_points_guard(zp)
+        zero_points_guard(zp, w)
+    zp.zero_()
+    zero_points_guard(zp, w)
+    w[0, 0] = 9  # an in-place update out of the signed int4 range
+    with pytest.raises(RuntimeError, match="int4"):
+        zero_points_guard(zp, w)
+    # a new tensor is checked even where an old one passed (no address key)
+    fresh = torch.ones_like(zp)
+    with pytest.raises(RuntimeError, match="zero points"):
+        zero_points_guard(fresh)
 
 
 def test_per_group_reshape_form_replaced(cpu_passes):
@@ -449,3 +518,24 @@ def test_dynamic_token_count_compiles_once(monkeypatch):
             torch.testing.assert_close(f(x), torch.nn.functional.linear(x, m.w).relu())
     assert len(compiles) == 1
     torch._dynamo.reset()
+
+
+def test_weight_cache_rewrites_offset_forms(cpu_passes):
+    # repack(add(w, 8)) and add(clone(zp view), 8) of module weights become
+    # single cached transforms carrying the offset
+    from zentorch import _compile_backend as B
+    from zentorch._weight_cache import cached_clone_offset, cached_repack_weight_offset
+    N, K = 64, 256
+    w, zp, s = quantized(N, K, 128)
+    zp = torch.full_like(zp, 3)
+    x = torch.randn(4, K).bfloat16()
+    gm = trace(lambda x, w, zp, s: torch.mm(x, dequant_t(w, zp, s, (N, K))), x, w, zp, s)
+    run_passes(gm)
+    ph = [n for n in gm.graph.nodes if n.op == "placeholder"]
+    assert B.use_weight_cache(gm.graph, set(ph[1:])) >= 3
+    gm.graph.eliminate_dead_code()
+    rep = [n for n in gm.graph.nodes if n.target is cached_repack_weight_offset]
+    clo = [n for n in gm.graph.nodes if n.target is cached_clone_offset]
+    assert len(rep) == 1 and rep[0].args[1] == 8
+    assert len(clo) == 1 and clo[0].args[1] == 8
+    assert not any(n.target in (aten.add.Tensor, aten.add.Scalar) for n in gm.graph.nodes)

@@ -157,3 +157,27 @@ def test_qlinear_errors():
     with pytest.raises(RuntimeError, match="per-tensor quantization for input"):
         ops.zentorch_qlinear(x, w, xs, torch.zeros(2, dtype=torch.int32, device=DEV), ws, None,
                              b, None, None)
+
+
+def test_qlinear_weight_column_sums_cached_and_updated():
+    # the column sums an input offset needs are computed once per weight and
+    # recomputed after an in-place update; a new weight in a reused block
+    # (same address) gets its own
+    x, w, xs, xz, ws, b = make(11, shape=(5, 64), N=24)
+    xd, wd, xsd, xzd, wsd, bd = dev(x, w, xs, xz, ws, b)
+    call = lambda wt: ops.zentorch_qlinear(xd, wt, xsd, xzd, wsd, None, bd, None, None,
+                                           output_dtype=torch.float32)
+    y1 = call(wd)
+    assert torch.equal(call(wd), y1)
+    check(y1, O.qlinear(x, w, xs, xz, ws, b, out_dtype=torch.float32))
+    w2 = torch.randint(-128, 128, w.shape, generator=torch.Generator().manual_seed(12),
+                       dtype=torch.int8)
+    wd.copy_(w2.to(DEV))
+    check(call(wd), O.qlinear(x, w2, xs, xz, ws, b, out_dtype=torch.float32))
+    ptr = wd.data_ptr()
+    del wd
+    w3 = torch.randint(-128, 128, w.shape, generator=torch.Generator().manual_seed(13),
+                       dtype=torch.int8)
+    wd3 = w3.to(DEV)
+    check(call(wd3), O.qlinear(x, w3, xs, xz, ws, b, out_dtype=torch.float32))
+    assert wd3.data_ptr() == ptr or True  # the caching allocator usually reuses the block

@@ -20,6 +20,8 @@
 #include <rocprofiler-sdk-roctx/roctx.h>
 
 #include <algorithm>
+#include <deque>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -650,6 +652,67 @@ void qlinear_checks(const at::Tensor &input, const at::Tensor &weight, const at:
   TORCH_CHECK(result.sizes() == c10::IntArrayRef(osz), "unsupported shape for the result tensor");
 }
 
+// sum_k weight[n][k] (int32) of a static qlinear's int8 weight, computed
+// once per weight: the weights of a quantised model are constant, as the
+// reference's first-call weight reorder assumes (is_weights_const,
+// QLinear.cpp:290-300).  An entry holds a weak reference to the weight's
+// storage (so its address cannot be taken by another storage while the
+// entry exists) and the version counter it was computed at; an in-place
+// update of the weight recomputes it.  Under HIP-graph capture the sums are
+// computed inside the captured work instead, so replays after an in-place
+// update still see the current weight.
+struct ColsumEntry {
+  c10::weak_intrusive_ptr<c10::StorageImpl> storage;
+  const void *data;
+  std::vector<int64_t> sizes, strides;
+  uint32_t version;
+  at::Tensor colsum;
+};
+constexpr size_t kColsumCacheMax = 4096;
+std::mutex g_colsum_mu;
+std::deque<ColsumEntry> g_colsum;
+
+at::Tensor compute_colsum(const at::Tensor &wc, zt_stream_t st, const std::string &name) {
+  at::Tensor cs = at::empty({wc.size(0)}, wc.options().dtype(at::kInt));
+  const int rc = zt_s8_weight_colsum(reinterpret_cast<const int8_t *>(wc.data_ptr()), wc.size(0),
+                                     wc.size(1), cs.data_ptr<int32_t>(), st);
+  TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
+  return cs;
+}
+
+at::Tensor weight_colsum_cached(const at::Tensor &weight, const at::Tensor &wc, hipStream_t st,
+                                const std::string &name) {
+  const zt_stream_t zst = reinterpret_cast<zt_stream_t>(st);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+    return compute_colsum(wc, zst, name);
+  c10::StorageImpl *impl = weight.storage().unsafeGetStorageImpl();
+  const uint32_t version = weight._version();
+  {
+    std::lock_guard<std::mutex> lock(g_colsum_mu);
+    for (auto it = g_colsum.begin(); it != g_colsum.end();) {
+      if (it->storage.expired()) {
+        it = g_colsum.erase(it);
+        continue;
+      }
+      if (it->storage._unsafe_get_target() == impl && it->data == weight.data_ptr() &&
+          it->sizes == weight.sizes().vec() && it->strides == weight.strides().vec()) {
+        if (it->version == version) return it->colsum;
+        it = g_colsum.erase(it);  // the weight changed in place
+        continue;
+      }
+      ++it;
+    }
+  }
+  at::Tensor cs = compute_colsum(wc, zst, name);
+  std::lock_guard<std::mutex> lock(g_colsum_mu);
+  if (g_colsum.size() >= kColsumCacheMax) g_colsum.pop_front();
+  g_colsum.push_back({c10::weak_intrusive_ptr<c10::StorageImpl>(
+                          weight.storage().getWeakStorageImpl()),
+                      weight.data_ptr(), weight.sizes().vec(), weight.strides().vec(), version, cs});
+  return cs;
+}
+
 void qlinear_into(at::Tensor &result, const at::Tensor &input, const at::Tensor &weight,
                   const at::Tensor &input_scales, const at::Tensor &input_zero_points,
                   const at::Tensor &weight_scales, const at::Tensor &weight_zero_points,
@@ -685,14 +748,11 @@ void qlinear_into(at::Tensor &result, const at::Tensor &input, const at::Tensor 
   const at::Tensor ozc = oz.defined() ? oz.contiguous() : at::Tensor();
   const hipStream_t st = current_stream();
   const zt_stream_t zst = reinterpret_cast<zt_stream_t>(st);
-  // activations with an offset (u8, or a zero point) need sum_k w[n][k]
+  // activations with an offset (u8, or a zero point) need sum_k w[n][k],
+  // kept per weight (the op's input_zero_points is always given, so this is
+  // every call of the reference's schema)
   at::Tensor colsum;
-  if (x2.scalar_type() == at::kByte || zx.defined()) {
-    colsum = at::empty({N}, weight.options().dtype(at::kInt));
-    const int rc = zt_s8_weight_colsum(reinterpret_cast<const int8_t *>(wc.data_ptr()), N, K,
-                                       colsum.data_ptr<int32_t>(), zst);
-    TORCH_CHECK(rc == ZT_OK, name, ": ", zt_last_error_string());
-  }
+  if (x2.scalar_type() == at::kByte || zx.defined()) colsum = weight_colsum_cached(weight, wc, st, name);
   zt_post_ops post{};
   post.count = (int32_t)post_ids.size();
   std::vector<at::Tensor> keep;

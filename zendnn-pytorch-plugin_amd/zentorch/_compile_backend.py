@@ -29,7 +29,8 @@ from torch._inductor.decomposition import select_decomp_table
 
 from ._logging import get_logger
 from ._optimize import optimize
-from ._weight_cache import cached_clone, cached_repack_from_int4pack, cached_repack_weight
+from ._weight_cache import (cached_clone, cached_clone_offset, cached_repack_from_int4pack,
+                            cached_repack_weight, cached_repack_weight_offset)
 
 logger = get_logger(__name__)
 
@@ -79,15 +80,47 @@ def _only_feeds_zentorch_ops(node: torch.fx.Node) -> bool:
     return True
 
 
+_ADD_OPS = {torch.ops.aten.add.Tensor, torch.ops.aten.add.Scalar}
+
+
+def _const_offset(node) -> "int | None":
+    """The integer c when ``node`` is add(v, c) with a Python int c (alpha 1)."""
+    if not (isinstance(node, torch.fx.Node) and node.op == "call_function"
+            and node.target in _ADD_OPS and len(node.args) == 2 and not node.kwargs):
+        return None
+    c = node.args[1]
+    return c if isinstance(c, int) and not isinstance(c, bool) else None
+
+
 def use_weight_cache(graph: torch.fx.Graph, weights: set) -> int:
     """Route repacks (and contiguous copies) of module weights through the
-    packed-weight cache.  Other inputs change from call to call and are
-    never cached."""
+    packed-weight cache, including the offset forms the WOQ replacement
+    emits for weights with zero points: repack(add(w, c)) and
+    add(clone(zero points), c).  Other inputs change from call to call and
+    are never cached."""
     n = 0
+    repack = torch.ops.zentorch.zentorch_woq_repack_weight.default
     for node in graph.nodes:
-        if node.op == "call_function" and node.target in _CACHED \
-                and _from_weight(node.args[0], weights) and _only_feeds_zentorch_ops(node):
+        if node.op != "call_function":
+            continue
+        if node.target in _CACHED and _from_weight(node.args[0], weights) \
+                and _only_feeds_zentorch_ops(node):
             node.target = _CACHED[node.target]
+            n += 1
+        elif node.target is repack and _const_offset(node.args[0]) is not None \
+                and _from_weight(node.args[0].args[0], weights) and _only_feeds_zentorch_ops(node):
+            add = node.args[0]
+            node.args = (add.args[0], _const_offset(add))
+            node.target = cached_repack_weight_offset
+            n += 1
+        elif _const_offset(node) is not None and isinstance(node.args[0], torch.fx.Node) \
+                and node.args[0].op == "call_function" \
+                and node.args[0].target is torch.ops.aten.clone.default \
+                and _from_weight(node.args[0].args[0], weights) and _only_feeds_zentorch_ops(node):
+            clone, offset = node.args[0], _const_offset(node)
+            node.target = cached_clone_offset
+            node.kwargs = dict(clone.kwargs)
+            node.args = (clone.args[0], offset)
             n += 1
     return n
 

@@ -10,9 +10,15 @@ into ``repack -> transpose -> zentorch_woq_linear``:
 
   with ``w`` int8 ``[N, K]`` and ``scale`` ``[N, 1]``; per group
   (:499-578 mm, :594-677 addmm) the product is viewed to ``[N, K]`` first,
-  with ``w`` ``[N, G, gs]`` and ``scale`` ``[N, G, 1]``.  As in the
-  reference the zero-point operand is dropped (symmetric int4; the reference
-  drops it at :370,386 and its models use zp = 0).
+  with ``w`` ``[N, G, gs]`` and ``scale`` ``[N, G, 1]``.  The reference
+  drops the zero-point operand (:370,386), so a non-zero zero point would be
+  computed as zero there.  Here the compile-time values decide: with every
+  zero point 0 and the weight in [-8, 7] the operand is dropped (signed int4,
+  as the reference) behind a run-time guard that the zero points stay zero;
+  with integer zero points that are not all zero the rewrite keeps them and
+  takes the unsigned int4 path of the op (``WOQ_Linear.cpp:44-49``): it packs
+  ``u = w + 8`` and passes ``zp + 8``, so ``(u - zp') = (w - zp)`` and the op
+  computes the graph's ``bf16((w - zp) * scale)``.
 * Int4OpaqueTensor (:684-736 and +bias :746-799)::
 
       _weight_int4pack_mm_for_cpu(x, packed, groupsize, scale_and_zero)
@@ -51,21 +57,36 @@ prims = torch.ops.prims
 
 pass_pattern = PatternMatcherPass(pass_name="zentorch_woq_replacement_pass")
 
-# zero-point placeholders a rewrite of the last pass assumed to be zero
+# (zero-point placeholder, weight placeholder) pairs of the rewrites of the
+# last pass that dropped all-zero zero points (signed int4 in [-8, 7])
 ASSUMED_ZERO_ZP = []
 
 
-def _symmetric_int4(w_node, zp_node) -> bool:
-    """True if the compile-time values show a symmetric signed int4 weight:
-    every zero point 0 and every weight value in [-8, 7]."""
+# u4 packing of a signed int4 weight with integer zero points: u = w + U4_OFFSET
+U4_OFFSET = 8
+
+
+def _int4_kind(w_node, zp_node) -> Optional[str]:
+    """What the compile-time values of the weight and zero points show:
+    "symmetric" (every zero point 0, every weight value in [-8, 7]),
+    "zero_points" (weight in [-8, 7], integer zero points not all zero whose
+    offset by U4_OFFSET stays in the zero points' dtype), or None (leave the
+    subgraph to PyTorch)."""
     zp, w = static_value(zp_node), static_value(w_node)
-    if zp is None or w is None or placeholder_of(zp_node) is None:
-        return False
+    if zp is None or w is None or placeholder_of(zp_node) is None or \
+            placeholder_of(w_node) is None:
+        return None
     # the passes run under the compile's fake mode; these are real tensors
     with unset_fake_temporarily():
-        if bool(zp.any()):
-            return False
-        return bool(((w >= -8) & (w <= 7)).all())
+        if not bool(((w >= -8) & (w <= 7)).all()):
+            return None
+        if not bool(zp.any()):
+            return "symmetric"
+        if zp.dtype not in (torch.int8, torch.int32):
+            return None
+        if int(zp.max()) > torch.iinfo(zp.dtype).max - U4_OFFSET:
+            return None
+        return "zero_points"
 
 
 def _bf16(arg):
@@ -123,10 +144,10 @@ def _dequant_check(has_bias: bool, per_group: bool) -> Callable[[Match], bool]:
             bv = tensor_meta(bias)
             if bv is None or bv.dim() != 1 or bv.shape[0] != N or not on_gpu(bv):
                 return False
-        if not _symmetric_int4(w, zp):
+        zv = tensor_meta(zp)
+        if zv is None or not on_gpu(zv) or zv.numel() != sv.numel():
             return False
-        ASSUMED_ZERO_ZP.append(placeholder_of(zp))
-        return True
+        return _int4_kind(w, zp) is not None
 
     return check
 
@@ -141,19 +162,33 @@ def _register_dequant(matmul: Any, per_group: bool, view_op: Optional[Any]) -> N
     @register_graph_pattern(pattern, pass_dict=pass_pattern,
                             extra_check=_dequant_check(has_bias, per_group))
     def _replace(match: Match, *args: Any) -> None:
+        w_node, zp_node = match.args[2:4] if has_bias else match.args[1:3]
+        symmetric = _int4_kind(w_node, zp_node) == "symmetric"
+        if symmetric:
+            # recorded only for a rewrite that is applied
+            ASSUMED_ZERO_ZP.append((placeholder_of(zp_node), placeholder_of(w_node)))
+
         def repl(*vals: Any) -> torch.Tensor:
             vals = list(vals)
             bias = vals.pop(0) if has_bias else None
-            x, w, _zp, scale = vals[:4]
+            x, w, zp, scale = vals[:4]
             if per_group:
                 w = w.reshape(vals[4])
-            # [N, K] int8 -> [N, K/8] int32 -> the op's [K/8, N] view;
-            # [N, G(, 1)] scales -> [G, N]
-            packed = torch.ops.zentorch.zentorch_woq_repack_weight(w).transpose(0, 1)
+            # [N, G(, 1)] scales and zero points -> [G, N]
             scales = scale.reshape(scale.shape[0], -1).transpose(0, 1).contiguous()
+            if symmetric:
+                # [N, K] int8 -> [N, K/8] int32 -> the op's [K/8, N] view
+                packed = torch.ops.zentorch.zentorch_woq_repack_weight(w).transpose(0, 1)
+                zeros = None
+            else:
+                # unsigned int4 u = w + 8 with zero points zp + 8
+                packed = torch.ops.zentorch.zentorch_woq_repack_weight(
+                    torch.ops.aten.add.Tensor(w, U4_OFFSET)).transpose(0, 1)
+                zeros = torch.ops.aten.add.Tensor(
+                    zp.reshape(zp.shape[0], -1).transpose(0, 1).contiguous(), U4_OFFSET)
             counters["zentorch"]["zentorch_woq_linear"] += 1
             return torch.ops.zentorch.zentorch_woq_linear(
-                x, packed, scales, None, bias, zentorch_op_name="zentorch_woq_linear")
+                x, packed, scales, zeros, bias, zentorch_op_name="zentorch_woq_linear")
 
         match.replace_by_example(repl, list(args))
 

@@ -8,8 +8,6 @@ then the binary-binary (:117) and unary (:118) post-op fusions.  The reference s
 all passes without AVX-512 (:87-91); here the gate is the graph's device: the
 passes only rewrite subgraphs whose tensors live on the GPU.
 """
-import threading
-
 import torch
 
 from . import _utils
@@ -22,24 +20,24 @@ from ._woq_linear_unary_fusion import woq_linear_unary_post_op_fusions
 logger = get_logger(__name__)
 
 
-_checked = {}
-_lock = threading.Lock()
-
-
-def zero_points_guard(zp: torch.Tensor) -> None:
-    """Raise if zero points a compiled graph assumed zero are not (checked
-    once per storage and version, so a forward pays a device sync only the
-    first time and after an in-place update)."""
-    key = (zp.device, zp.data_ptr(), tuple(zp.shape))
-    with _lock:
-        if _checked.get(key) == zp._version:
-            return
-    if bool(zp.any()):
-        raise RuntimeError(
-            "zentorch: this graph was compiled for all-zero weight zero points (symmetric "
-            "int4) and they have changed since; recompile the model")
-    with _lock:
-        _checked[key] = zp._version
+def zero_points_guard(zp: torch.Tensor, weight: torch.Tensor = None) -> None:
+    """Raise if the zero points a compiled graph assumed zero are not, or if
+    the int8 weight it packed as signed int4 left [-8, 7].  Each tensor is
+    checked once per version (the version is remembered on the tensor object
+    itself, so a new tensor is always checked), so a forward pays a device
+    synchronisation only the first time and after an in-place update."""
+    if getattr(zp, "_zentorch_zero_checked", None) != zp._version:
+        if bool(zp.any()):
+            raise RuntimeError(
+                "zentorch: this graph was compiled for all-zero weight zero points "
+                "(symmetric int4) and they have changed since; recompile the model")
+        zp._zentorch_zero_checked = zp._version
+    if weight is not None and getattr(weight, "_zentorch_int4_checked", None) != weight._version:
+        if weight.numel() and not bool(((weight >= -8) & (weight <= 7)).all()):
+            raise RuntimeError(
+                "zentorch: this graph was compiled for a signed int4 weight in [-8, 7] and "
+                "the weight has left that range since; recompile the model")
+        weight._zentorch_int4_checked = weight._version
 
 
 torch.fx.node._side_effectful_functions.add(zero_points_guard)
@@ -50,8 +48,8 @@ def _insert_zero_point_guards(fx_graph) -> None:
     if not placeholders:
         return
     with fx_graph.inserting_after(placeholders[-1]):
-        for zp in dict.fromkeys(ASSUMED_ZERO_ZP):
-            fx_graph.call_function(zero_points_guard, (zp,))
+        for zp, w in dict.fromkeys(ASSUMED_ZERO_ZP):
+            fx_graph.call_function(zero_points_guard, (zp, w))
 
 
 def optimize(fx_graph, static_values=None):

@@ -7,7 +7,9 @@ reference avoids the same cost by reordering a constant weight once and
 caching it inside ZenDNNL (``is_weights_const=true``,
 src/cpu/cpp/WOQ_Linear.cpp:107).  Here a compiled graph calls
 :func:`cached_repack` instead, which returns the packed tensor computed for
-the same weight storage, view and version counter.
+the same weight storage, view and version counter.  A repack checks the
+weight's value range when it packs (a miss), so an in-place update that
+leaves the int4 range raises instead of being truncated.
 
 The entry holds a reference to the source weight, so its storage (and
 address) cannot be reused by another tensor while the entry exists; an
@@ -40,8 +42,40 @@ def cached_repack(op: Callable[[torch.Tensor], torch.Tensor], op_name: str,
     return out
 
 
+def _checked_int4(w: torch.Tensor, lo: int, hi: int, what: str) -> torch.Tensor:
+    """``w`` after checking that every value lies in [lo, hi] (run on a cache
+    miss only: when a weight is packed the first time or after it changed);
+    a value outside would be truncated to its low nibble by the packing."""
+    if w.numel() and not bool(((w >= lo) & (w <= hi)).all()):
+        raise RuntimeError(
+            f"zentorch: {what} holds values outside [{lo}, {hi}], which int4 packing "
+            f"cannot represent; this graph was compiled for an int4 weight in that range")
+    return w
+
+
 def cached_repack_weight(w: torch.Tensor) -> torch.Tensor:
-    return cached_repack(torch.ops.zentorch.zentorch_woq_repack_weight, "repack_weight", w)
+    return cached_repack(
+        lambda t: torch.ops.zentorch.zentorch_woq_repack_weight(
+            _checked_int4(t, -8, 15, "a weight packed by zentorch_woq_repack_weight")),
+        "repack_weight", w)
+
+
+def cached_repack_weight_offset(w: torch.Tensor, offset: int) -> torch.Tensor:
+    """zentorch_woq_repack_weight(w + offset), packed once per weight version:
+    the unsigned int4 packing u = w + offset of a signed int4 weight whose
+    zero points are kept (the offset keeps u in [0, 15])."""
+    return cached_repack(
+        lambda t: torch.ops.zentorch.zentorch_woq_repack_weight(
+            _checked_int4(t, -offset, 15 - offset, "an int4 weight with zero points") + offset),
+        f"repack_weight+{offset}", w)
+
+
+def cached_clone_offset(w: torch.Tensor, offset: int, *,
+                        memory_format=torch.preserve_format) -> torch.Tensor:
+    """w.clone() + offset once per version of w (the zero points zp + 8 that
+    go with cached_repack_weight_offset)."""
+    return cached_repack(lambda t: t.clone(memory_format=memory_format) + offset,
+                         f"clone+{offset}:{memory_format}", w)
 
 
 def cached_repack_from_int4pack(w: torch.Tensor) -> torch.Tensor:
