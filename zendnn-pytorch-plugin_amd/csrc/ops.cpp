@@ -869,13 +869,127 @@ ZT_QLIN_INST(ZT_PO_RELU)
 ZT_QLIN_INST(ZT_PO_SIGMOID)
 #undef ZT_QLIN_INST
 
-// zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema :728-736)
-// for int4-packed expert weights: w13 int32 [E, 2I, H/8], w2 int32
-// [E, H, I/8] (each expert packed by zentorch_woq_repack_weight) with bf16
-// group scales w13_scales [E, G13, 2I], w2_scales [E, G2, H].  The
-// reference's bf16 / int8 expert weights are refused with a message.
-// `output` ([T, H], the input's dtype) is overwritten with the result, which
-// equals the reference's accumulation into its zero-initialised output.
+// The reference's own expert formats (FusedMoE.cpp:470-718,
+// docs/zentorch_fused_moe.md:80-101): bf16 / fp32 experts in the input's
+// dtype, or int8 experts with per-output-channel scales whose activations
+// are quantised per token inside each GEMM.  As the reference, the (token, k)
+// pairs are grouped by expert with the per-expert counts on the host
+// (FusedMoE.cpp:289-433; here one device-to-host copy of E + 2 counts, so
+// these formats are not capturable in a HIP graph, as the reference's host
+// grouping is not).  Each active expert then runs
+//   h = act(x . W13[e, :I]^T + b13[e, :I]) * (x . W13[e, I:]^T + b13[e, I:])
+//   y = h . W2[e]^T + b2[e]
+// as the reference's per-expert fallback does (vllm/_int8_moe_patch.py:
+// 149-206): int8 experts on zentorch_dynamic_qlinear's kernels (the gate's
+// activation and the product with the up half in its fused epilogue, on the
+// fp32 accumulator with one rounding, as the int4 path computes h), float
+// experts on the plain library
+// GEMM (hipBLASLt through at::matmul).  out[t] = sum_k w[t, k] * y[t, k] in
+// fp32 (k in order), rounded once; pairs whose id is outside [0, E) are
+// dropped.
+void fused_moe_dense(at::Tensor &output, const at::Tensor &input, const at::Tensor &w13,
+                     const at::Tensor &w2, const at::Tensor &b13, const at::Tensor &b2,
+                     const at::Tensor &topk_weights, const at::Tensor &topk_id,
+                     bool skip_weighted, int32_t act_id,
+                     const c10::optional<at::Tensor> &w13_scales,
+                     const c10::optional<at::Tensor> &w2_scales, const std::string &name) {
+  const char *op = "zentorch_fused_moe";
+  const int64_t T = input.size(0), H = input.size(1), E = w13.size(0);
+  const int64_t I = w13.size(1) / 2, topk = topk_id.size(1), P = T * topk;
+  const bool int8 = w13.scalar_type() == at::kChar;
+  at::Tensor s13, s2;
+  if (int8) {
+    TORCH_CHECK(w2.scalar_type() == at::kChar, op, ": w13 is int8, so w2 must be int8 too, got ",
+                w2.scalar_type());
+    TORCH_CHECK(w13_scales.has_value() && w13_scales->defined() && w2_scales.has_value() &&
+                    w2_scales->defined(),
+                op, ": int8 experts need w13_scales and w2_scales");
+    s13 = *w13_scales;
+    s2 = *w2_scales;
+    TORCH_CHECK(s13.numel() == E * 2 * I && s2.numel() == E * H, op,
+                ": int8 experts take per-output-channel scales [E, 2I] and [E, H] (per-group "
+                "int8 scales are not supported by this build); got ", s13.sizes(), " and ",
+                s2.sizes());
+    TORCH_CHECK((s13.scalar_type() == at::kFloat || s13.scalar_type() == at::kBFloat16) &&
+                    (s2.scalar_type() == at::kFloat || s2.scalar_type() == at::kBFloat16),
+                op, ": int8 expert scales must be float32 or bfloat16");
+    s13 = s13.reshape({E, 2 * I});
+    s2 = s2.reshape({E, H});
+    check_device(s13, input, op, "w13_scales");
+    check_device(s2, input, op, "w2_scales");
+  } else {
+    TORCH_CHECK(w13.scalar_type() == input.scalar_type() && w2.scalar_type() == input.scalar_type(),
+                op, ": float experts must have the input's dtype (", input.scalar_type(),
+                "), got w13 ", w13.scalar_type(), " and w2 ", w2.scalar_type());
+    TORCH_CHECK(!(w13_scales.has_value() && w13_scales->defined()) &&
+                    !(w2_scales.has_value() && w2_scales->defined()),
+                op, ": scales are only taken with int8 or int4 experts");
+  }
+  TORCH_CHECK(w13.dim() == 3 && w13.size(1) == 2 * I && w13.size(2) == H, op,
+              ": w13 must be [E, 2I, H] for H=", H, ", got ", w13.sizes());
+  TORCH_CHECK(w2.dim() == 3 && w2.size(0) == E && w2.size(1) == H && w2.size(2) == I, op,
+              ": w2 must be [E, H, I] = [", E, ", ", H, ", ", I, "], got ", w2.sizes());
+  if (T == 0) return;
+  // group the pairs by expert: a stable sort of the ids, and the counts of
+  // ids below 0, of each expert and of ids >= E in one host copy
+  const at::Tensor flat = topk_id.reshape({-1}).to(at::kLong);
+  const at::Tensor order = std::get<1>(at::sort(flat, /*stable=*/true, 0, false));
+  const at::Tensor bins = (flat.clamp(-1, E) + 1);
+  const at::Tensor counts = at::bincount(bins, {}, E + 2).cpu();
+  const int64_t *cnt = counts.data_ptr<int64_t>();
+  const at::Tensor tokens = input.index_select(0, at::div(order, topk, "floor"));
+  at::Tensor y = at::zeros({P, H}, input.options());
+  int64_t cursor = cnt[0];  // the ids below 0 sort first and stay zero
+  for (int64_t e = 0; e < E; ++e) {
+    const int64_t n = cnt[e + 1];
+    if (n == 0) continue;
+    const at::Tensor xe = tokens.narrow(0, cursor, n);
+    const at::Tensor we = w13[e];
+    const c10::optional<at::Tensor> bg =
+        b13.defined() ? c10::optional<at::Tensor>(b13[e].narrow(0, 0, I)) : c10::nullopt;
+    const c10::optional<at::Tensor> bu =
+        b13.defined() ? c10::optional<at::Tensor>(b13[e].narrow(0, I, I)) : c10::nullopt;
+    const c10::optional<at::Tensor> bd =
+        b2.defined() ? c10::optional<at::Tensor>(b2[e]) : c10::nullopt;
+    at::Tensor h, ye;
+    if (int8) {
+      // the gate's activation runs on its fp32 accumulator in the GEMM
+      // epilogue, times the rounded up half, with one rounding (the int4
+      // path's convention); h is then quantised per token for W2
+      const at::Tensor up = dynamic_qlinear_impl(xe, we.narrow(0, I, I), s13[e].narrow(0, I, I),
+                                                 bu, {}, {}, name);
+      h = dynamic_qlinear_impl(xe, we.narrow(0, 0, I), s13[e].narrow(0, 0, I), bg,
+                               {act_id, ZT_PO_MUL}, {up}, name);
+      ye = dynamic_qlinear_impl(h, w2[e], s2[e], bd, {}, {}, name);
+    } else {
+      at::Tensor gu = at::matmul(xe, we.t());
+      if (b13.defined()) gu = gu + b13[e];
+      const at::Tensor g = gu.narrow(1, 0, I), u = gu.narrow(1, I, I);
+      h = (act_id == ZT_PO_SILU ? at::silu(g)
+                                : at::gelu(g, act_id == ZT_PO_GELU_TANH ? "tanh" : "none")) * u;
+      ye = at::matmul(h, w2[e].t());
+      if (b2.defined()) ye = ye + b2[e];
+    }
+    y.narrow(0, cursor, n).copy_(ye);
+    cursor += n;
+  }
+  // back to (token, k) order, then the weighted sum over k in fp32
+  at::Tensor yu = at::empty_like(y);
+  yu.index_copy_(0, order, y);
+  at::Tensor acc = yu.view({T, topk, H}).to(at::kFloat);
+  if (!skip_weighted) acc = acc * topk_weights.to(at::kFloat).unsqueeze(-1);
+  output.copy_(acc.sum(1));
+}
+
+// zentorch_fused_moe (src/cpu/cpp/FusedMoE.cpp:443-700, schema :728-736).
+// int4-packed expert weights (an extension: w13 int32 [E, 2I, H/8], w2
+// int32 [E, H, I/8], each expert packed by zentorch_woq_repack_weight, with
+// bf16 group scales w13_scales [E, G13, 2I], w2_scales [E, G2, H]) run the
+// grouped HIP kernels of zt_woq_moe, routing included, with no host
+// synchronisation; the reference's bf16 / fp32 / int8 experts take
+// fused_moe_dense above.  `output` ([T, H], the input's dtype) is
+// overwritten with the result, which equals the reference's accumulation
+// into its zero-initialised output.
 void fused_moe(at::Tensor &output, const at::Tensor &input, const at::Tensor &w13,
                const at::Tensor &w2, const c10::optional<at::Tensor> &w13_bias,
                const c10::optional<at::Tensor> &w2_bias, const at::Tensor &topk_weights,
@@ -884,13 +998,43 @@ void fused_moe(at::Tensor &output, const at::Tensor &input, const at::Tensor &w1
                const c10::optional<at::Tensor> &w2_scales, c10::string_view zentorch_op_name) {
   const char *op = "zentorch_fused_moe";
   const OpRange range{std::string(zentorch_op_name)};
-  TORCH_CHECK(input.dim() == 2 && input.scalar_type() == at::kBFloat16,
-              op, ": input must be a 2D bfloat16 tensor [T, H]");
-  TORCH_CHECK(w13.scalar_type() == at::kInt && w2.scalar_type() == at::kInt,
-              op, ": this build runs int4-packed expert weights (int32 [E, 2I, H/8] and "
-              "[E, H, I/8] from zentorch_woq_repack_weight per expert); got w13 ",
-              w13.scalar_type(), " and w2 ", w2.scalar_type());
+  TORCH_CHECK(input.dim() == 2 && (input.scalar_type() == at::kBFloat16 ||
+                                   input.scalar_type() == at::kFloat),
+              op, ": input must be a 2D bfloat16 or float32 tensor [T, H]");
   TORCH_CHECK(w13.dim() == 3 && w2.dim() == 3, op, ": w13 and w2 must be 3D");
+  if (w13.scalar_type() != at::kInt) {
+    TORCH_CHECK(topk_id.dim() == 2 && topk_id.size(0) == input.size(0), op,
+                ": topk_id must be [T, K]");
+    TORCH_CHECK(topk_weights.sizes() == topk_id.sizes(), op,
+                ": topk_weights must have topk_id's shape ", topk_id.sizes());
+    TORCH_CHECK(!skip_weighted || topk_id.size(1) == 1, op,
+                ": skip_weighted requires K == 1 (got K=", topk_id.size(1), ")");
+    TORCH_CHECK(w13.size(1) % 2 == 0, op, ": w13 must be [E, 2I, H]");
+    TORCH_CHECK(output.sizes() == input.sizes() && output.scalar_type() == input.scalar_type(),
+                op, ": output must be a tensor like input");
+    int32_t act_id = 0;
+    if (act == "silu") act_id = ZT_PO_SILU;
+    else if (act == "gelu") act_id = ZT_PO_GELU_ERF;
+    else if (act == "gelu_tanh") act_id = ZT_PO_GELU_TANH;
+    else TORCH_CHECK(false, op, ": activation '", std::string(act), "' is not supported here "
+                     "(silu, gelu, gelu_tanh)");
+    at::Tensor b13, b2;
+    if (w13_bias.has_value() && w13_bias->defined()) b13 = w13_bias->reshape({w13.size(0), -1});
+    if (w2_bias.has_value() && w2_bias->defined()) b2 = w2_bias->reshape({w13.size(0), -1});
+    for (const at::Tensor *t : std::initializer_list<const at::Tensor *>{
+             &input, &w13, &w2, &topk_id, &topk_weights, &output})
+      check_device(*t, input, op, "argument");
+    if (b13.defined()) check_device(b13, input, op, "w13_bias");
+    if (b2.defined()) check_device(b2, input, op, "w2_bias");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(input.device());
+    fused_moe_dense(output, input.contiguous(), w13, w2, b13, b2, topk_weights, topk_id,
+                    skip_weighted, act_id, w13_scales, w2_scales, std::string(zentorch_op_name));
+    return;
+  }
+  TORCH_CHECK(input.scalar_type() == at::kBFloat16, op,
+              ": int4-packed experts take a bfloat16 input");
+  TORCH_CHECK(w2.scalar_type() == at::kInt, op, ": w13 is int4-packed (int32), so w2 must be "
+              "too, got ", w2.scalar_type());
   const int64_t T = input.size(0), H = input.size(1);
   const int64_t E = w13.size(0), I = w13.size(1) / 2;
   TORCH_CHECK(w13.size(1) == 2 * I && w13.size(2) * 8 == H, op,
