@@ -97,12 +97,13 @@ def test_gemm_kernel_vs_oracle(M, K, N, G):
 
 
 # the wide decode kernel (17..64 rows, bf16 scales, no zero points,
-# K % 512 == 0, N % 4 == 0): one or two 32-token tiles, K split over several
+# K % 256 == 0, N % 4 == 0): one or two 32-token tiles, K split over several
 # workgroups (partials + reduce) or not (epilogue in the kernel), ragged N,
-# group 128 / 256 / per-channel
+# group 128 / 256 / per-channel; K = 768 and 1280 give splits of 3 and 5
+# phases (the padded kernel form)
 @pytest.mark.parametrize("M", [17, 24, 32, 33, 48, 64])
 @pytest.mark.parametrize("K,N,G", [(4096, 1000, 32), (2048, 200, 8), (1024, 2052, 1),
-                                   (14336, 384, 112)])
+                                   (14336, 384, 112), (768, 260, 6), (1280, 132, 5)])
 def test_wide_kernel_vs_oracle(M, K, N, G):
     run_case(M, K, N, G, kernel="wide", seed=M + K + N, bias=(M % 2 == 1))
 

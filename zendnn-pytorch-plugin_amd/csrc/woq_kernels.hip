@@ -2207,58 +2207,80 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
 // ------------------------------------------------ wide decode (17..64 rows)
 // Weight streaming for 17..64 tokens, where re-reading x per 16-row weight
 // tile (the stream kernel) moves up to 16 bytes of x per byte of int4.  A
-// workgroup owns 128 weight rows over one K split and keeps x [32*MT][512]
-// of the current K phase in LDS, shared by its waves, so x costs at most
-// 4*M/128 bytes per weight byte.  Its 8 waves form 4 row groups of 32; the
-// two waves of a group take alternate chunk pairs of each phase (two waves
-// per SIMD, so one wave's dequantisation overlaps the other's MFMAs) and
-// add their halves in LDS at the end.
+// workgroup owns 128 weight rows over one K split and keeps x [32*MT][256]
+// of each 256-k phase in LDS, shared by its 8 waves, so x costs 4*M/128
+// bytes per weight byte.  The waves form 4 row groups of 32; the two waves
+// of a group take the two 128-k chunks of each phase (two waves per SIMD,
+// so one wave's dequantisation overlaps the other's MFMAs) and add their
+// halves in LDS at the end.
 //
-// A wave loads its 32 rows as two 16-row x 64-byte tiles per 128-k chunk
-// (16 rows x 64 B per instruction, straight from HBM to registers, two
-// phases ahead) and turns each pair into the 32-row A operands of
-// v_mfma_f32_32x32x16_bf16 with one v_permlane16_swap per dword: lanes 0-31
+// Loads, all issued three phases before their use: x and the phase's scales
+// move by DMA into four LDS stages; each wave's weights go straight from HBM
+// to registers (two 16-row x 64-byte loads per chunk) into four register
+// sets.  A wave's loads retire in issue order and every phase issues the
+// same loads (past the split out of range, so zeros), so one wait per phase
+// -- everything issued for this phase has landed -- and the barrier after it
+// cover x, scales and weights; the barrier also retires the stage the new
+// DMA overwrites.  The weights are issued at the start of a phase, the DMA
+// spread over its first steps.  The phase loop runs whole rounds of four
+// phases with the register sets fixed per position and nothing skipped, so
+// the compiler's own wait counting stays exact (a remainder or a skipped
+// compute makes it wait for every load at each phase).  The PAD form pads a
+// split that is not a whole number of rounds and skips the compute of the
+// padding; it is the slower fallback.
+//
+// Compute: a chunk's two 16-row tiles become the 32-row A operands of
+// v_mfma_f32_32x32x16_bf16 with one v_permlane16_swap per dword (lanes 0-31
 // then hold bytes [0, 16) and [16, 32) of rows 0-31, lanes 32-63 bytes
-// [32, 48) and [48, 64), so MFMA q of the chunk takes k block 8*(l/32) + q
-// (8 k each) in both operands.  B is x from LDS: 1 KB rows, 16-byte chunk c
-// of token row t at position c ^ (t & 15) (16 distinct bank groups for the
-// 16 rows one read pass touches).  Dequantisation is the decode kernels'
-// (bf16_rne of the exact fp32 product).  The scales of a phase's four
-// chunks for the workgroup's 128 rows come with its x, one 256-byte DMA per
-// chunk into a double-buffered LDS block [4][128].
+// [32, 48) and [48, 64)), so MFMA q of the chunk takes k block 8*(l/32) + q
+// in both operands.  B is x from LDS: 512-byte token rows, 16-byte column c
+// of row t at position c ^ (t & 15) (16 distinct bank groups per read pass).
+// A wave reads the phase's eight B fragments first, then dequantises
+// (bf16_rne of the exact fp32 product, dq_word) and multiplies.
 //
 // D is [n][token]: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4
 // of the wave's 32 and token 32*j + l%32.  With one K split the workgroup
 // applies the epilogue; with several it writes fp32 partials
 // [split][M][N], which woq_splitk_reduce_kernel adds in split order.
 
-constexpr int kWideKP = 512;    // k per phase
+// sched_barrier mask: everything but vector-memory instructions may cross
+constexpr int kSchedAllButVmem = 0x78f;
+constexpr int kWideKP = 256;    // k per phase (two 128-k chunks)
 constexpr int kWideRows = 128;  // weight rows per workgroup
+constexpr int kWideAhead = 3;   // phases between a load's issue and its use
+constexpr int kWideRound = kWideAhead + 1;  // LDS stages, register sets, phases per loop round
+
+template <int MT>
+constexpr size_t woq_wide_xstage() {
+  return (size_t)(32 * MT) * (kWideKP * 2);
+}
 
 template <int MT>
 constexpr size_t woq_wide_lds() {
-  // two x phase buffers, then two phase buffers of scales [4 chunks][128 rows]
-  const size_t x = 2 * (size_t)(32 * MT) * 1024 + 2 * 4 * kWideRows * 2;
+  // x stages, scale stages [round][2 chunks][128 rows], and a spare 256-byte
+  // block the out-of-range scale DMA of waves 2..7 writes
+  const size_t x = kWideRound * woq_wide_xstage<MT>() + kWideRound * 2 * (kWideRows * 2) + 256;
   const size_t tile = (size_t)(32 * MT) * (kWideRows + 4) * 4;
   return x > tile ? x : tile;
 }
 
-template <int MT>
+template <int MT, bool PAD>
 __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int cpg_shift, int gmask,
                                                        float *partial, int gu) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  constexpr int XB = 32 * MT * 1024;  // one x phase buffer
-  constexpr int XL = 4 * MT;          // x rows (one load each) per wave per phase
-  constexpr int WL = 4;  // weight loads per wave per phase
-  constexpr int WAIT = vmcnt_imm_woq(WL);
+  constexpr int XS = (int)woq_wide_xstage<MT>();
+  constexpr int XL = 2 * MT;        // x DMA (two token rows each) per wave per phase
+  constexpr int OPS = 3 + XL;       // loads per wave per phase: 2 weight tiles, scales, x
+  constexpr int WAIT = vmcnt_imm_woq((kWideAhead - 1) * OPS);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rw = wv & 3, kh = wv >> 2;  // row group; chunk pair {2kh, 2kh+1} of each phase
+  const int rw = wv & 3, kh = wv >> 2;  // row group; chunk of each phase
   const int lr = lane & 15, lg = lane >> 4, l32 = lane & 31, hl = lane >> 5;
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
   const int ldx2 = (int)a.ldx * 2;
   const int n0 = blockIdx.x * kWideRows;
   const int ph0 = blockIdx.y * pps;  // first phase of this K split
+  const int pend = ph0 + pps;
   // merged gate_up (gu = N/2, a multiple of 64): local rows [0, 64) are gate
   // rows j0.., local rows [64, 128) the up rows gu + j0..
   const int j0 = blockIdx.x * (kWideRows / 2);
@@ -2273,43 +2295,42 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
   const int r_lo = row_of(rw * 32 + lr), r_hi = row_of(rw * 32 + lr + 16);
   const uint32_t off_lo = (uint32_t)r_lo * (uint32_t)KW * 4u + 16u * lg;
   const uint32_t off_hi = (uint32_t)r_hi * (uint32_t)KW * 4u + 16u * lg;
+  const uint32_t oob_lo = r_lo < N ? 0u : kOobOffset, oob_hi = r_hi < N ? 0u : kOobOffset;
 
-  u32x4_t wq[3][2][2];
-  // Phases past the split (or past K) load zeros so every phase issues the
-  // same number of loads.  The out-of-range bit is ORed into the offsets
+  u32x4_t wq[kWideRound][2];
+  unsigned char *sbuf0 = smem + kWideRound * XS;
+  // Load i of phase ph.  The out-of-range bit is ORed into the offsets
   // (valid offsets stay below it): a select on the wave-uniform condition
   // would be compiled into branches around each load.
-  const uint32_t oob_lo = r_lo < N ? 0u : kOobOffset, oob_hi = r_hi < N ? 0u : kOobOffset;
-  auto load_w = [&](int set, int ph) {
-    const uint32_t oob = ph < ph0 + pps ? 0u : kOobOffset;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const uint32_t kc = (uint32_t)(ph * 4 + 2 * kh + c);
-      wq[set][c][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-          w_rs, (off_lo + kc * 64u) | oob_lo | oob, 0, 0));
-      wq[set][c][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-          w_rs, (off_hi + kc * 64u) | oob_hi | oob, 0, 0));
-    }
-  };
-  // x of a phase, and its scales: wave w < 4 moves the 128 row scales of
-  // chunk w's group (one 256-byte DMA; N % 4 == 0 keeps the dwords aligned)
-  unsigned char *sbuf0 = smem + 2 * XB;
-  auto dma_x = [&](int ph) {
-    const uint32_t oob = ph < ph0 + pps ? 0u : kOobOffset;
-    unsigned char *buf = smem + (ph & 1) * XB;
-    if (wv < 4) {
-      const uint32_t g = ((uint32_t)(ph * 4 + wv) >> cpg_shift) & (uint32_t)gmask;
+  //  0, 1: the weight tiles of the lane's low / high row (register set `set`)
+  //  2:    the scales: waves 0 and 1 move chunk wv's 128 row scales (one
+  //        256-byte DMA; N % 4 == 0 keeps the dwords aligned), the others an
+  //        out-of-range DMA into the spare block, so no branch surrounds it
+  //  3..:  x token rows 2 (wv + 8 i) and 2 (wv + 8 i) + 1, 512 bytes each
+  auto load = [&](int i, int ph, int set) {
+    const uint32_t oob = ph < pend ? 0u : kOobOffset;
+    if (i < 2) {
+      const uint32_t kc = (uint32_t)(ph * 2 + kh);
+      const uint32_t off = i == 0 ? (off_lo + kc * 64u) | oob_lo : (off_hi + kc * 64u) | oob_hi;
+      wq[set][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+          w_rs, off | oob, 0, 0));
+    } else if (i == 2) {
+      const int ch = wv & 1;
+      const uint32_t g = ((uint32_t)(ph * 2 + ch) >> cpg_shift) & (uint32_t)gmask;
+      const uint32_t soob = wv < 2 ? 0u : kOobOffset;
+      const int slot = wv < 2 ? (ph & (kWideRound - 1)) * 2 + ch : 2 * kWideRound;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          s_rs, (lds_ptr_t)(sbuf0 + ((ph & 1) * 4 + wv) * (kWideRows * 2)), 4,
-          ((g * (uint32_t)N + (uint32_t)row_of(2 * lane)) * 2u) | oob, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < XL; ++i) {
-      const int t = wv + 8 * i;
-      const int c = lane ^ (t & 15);
+          s_rs, (lds_ptr_t)(sbuf0 + slot * (kWideRows * 2)), 4,
+          ((g * (uint32_t)N + (uint32_t)row_of(2 * lane)) * 2u) | oob | soob, 0, 0, 0);
+    } else {
+      const int r = 2 * (wv + 8 * (i - 3));
+      const int t = r + hl;
+      const int c = l32 ^ (t & 15);
       const uint32_t off = (uint32_t)(t * ldx2 + ph * (kWideKP * 2) + c * 16) |
                            (t < M ? 0u : kOobOffset) | oob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rs, (lds_ptr_t)(buf + t * 1024), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          x_rs, (lds_ptr_t)(smem + (ph & (kWideRound - 1)) * XS + r * (kWideKP * 2)), 16, off, 0,
+          0, 0);
     }
   };
 
@@ -2319,55 +2340,77 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 
+  // the compute of phase ph, issuing the DMA loads 2.. of phase ph + 3 one
+  // per step (VMEM pinned in place, everything else free to move around it)
   auto compute = [&](int set, int ph) {
-    const unsigned char *buf = smem + (ph & 1) * XB;
+    const unsigned char *buf = smem + (ph & (kWideRound - 1)) * XS;
+    bf16x8_t xf[8][MT];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      u32x4_t w0 = wq[set][c][0], w1 = wq[set][c][1];
+    for (int q = 0; q < 8; ++q)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const auto sw = __builtin_amdgcn_permlane16_swap(w0[e], w1[e], false, false);
-        w0[e] = sw[0];
-        w1[e] = sw[1];
+      for (int j = 0; j < MT; ++j) {
+        const int t = 32 * j + l32;
+        const int cc = kh * 16 + 8 * hl + q;
+        xf[q][j] = *reinterpret_cast<const bf16x8_t *>(buf + t * (kWideKP * 2) + ((cc ^ (t & 15)) * 16));
       }
-      const float sc = __uint_as_float(
-          (uint32_t)reinterpret_cast<const uint16_t *>(
-              sbuf0 + ((ph & 1) * 4 + 2 * kh + c) * (kWideRows * 2))[rw * 32 + l32]
-          << 16);
+    const float sc = __uint_as_float(
+        (uint32_t)reinterpret_cast<const uint16_t *>(
+            sbuf0 + ((ph & (kWideRound - 1)) * 2 + kh) * (kWideRows * 2))[rw * 32 + l32]
+        << 16);
+    u32x4_t w0 = wq[set][0], w1 = wq[set][1];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const bf16x8_t wb = dq_word<kDecFast>(q < 4 ? w0[q] : w1[q - 4], sc, 0.f, 0);
-        const int cc = (2 * kh + c) * 16 + 8 * hl + q;
+    for (int e = 0; e < 4; ++e) {
+      const auto sw = __builtin_amdgcn_permlane16_swap(w0[e], w1[e], false, false);
+      w0[e] = sw[0];
+      w1[e] = sw[1];
+    }
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          const int t = 32 * j + l32;
-          const bf16x8_t xb =
-              *reinterpret_cast<const bf16x8_t *>(buf + t * 1024 + ((cc ^ (t & 15)) * 16));
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb, xb, acc[j], 0, 0, 0);
-        }
+    for (int q = 0; q < 8; ++q) {
+      if (q < OPS - 2) {
+        __builtin_amdgcn_sched_barrier(kSchedAllButVmem);
+        load(2 + q, ph + kWideAhead, 0);
+        __builtin_amdgcn_sched_barrier(kSchedAllButVmem);
       }
+      const bf16x8_t wb = dq_word<kDecFast>(q < 4 ? w0[q] : w1[q - 4], sc, 0.f, 0);
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb, xf[q][j], acc[j], 0, 0, 0);
     }
   };
-  // phase j: x(j) and W(j) landed once only the loads of W(j + 1) are
-  // outstanding (issued after x(j)); the barrier also means every wave is
-  // done with phase j - 1, whose x buffer the next DMA overwrites
+  static_assert(OPS - 2 <= 8, "the DMA loads fit the steps of a phase");
   auto phase = [&](int j, int set) {
+    const int ph = ph0 + j;
     __builtin_amdgcn_s_waitcnt(WAIT);
     asm volatile("s_barrier" ::: "memory");
-    dma_x(ph0 + j + 1);
-    load_w((set + 2) % 3, ph0 + j + 2);
-    compute(set, ph0 + j);
+    load(0, ph + kWideAhead, (set + kWideAhead) % kWideRound);
+    load(1, ph + kWideAhead, (set + kWideAhead) % kWideRound);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!PAD || ph < pend) {
+      compute(set, ph);
+    } else {
+#pragma unroll
+      for (int i = 2; i < OPS; ++i) load(i, ph + kWideAhead, 0);
+    }
   };
-  dma_x(ph0);
-  load_w(0, ph0);
-  load_w(1, ph0 + 1);
-  for (int j = 0; j < pps; j += 3) {
+  // prologue: the loads of phases 0 .. 2, in the order the phases issue them
+#pragma unroll
+  for (int v = 0; v < kWideAhead; ++v)
+#pragma unroll
+    for (int i = 0; i < OPS; ++i) load(i, ph0 + v, v);
+  // whole rounds (the host gives PAD = false only when pps is a multiple of 4)
+  const int jend = PAD ? (pps + kWideRound - 1) / kWideRound * kWideRound : pps;
+  int j = 0;
+  do {
+    static_assert(kWideRound == 4, "one loop round is four phases");
     phase(j, 0);
-    if (j + 1 < pps) phase(j + 1, 1);
-    if (j + 2 < pps) phase(j + 2, 2);
-  }
+    phase(j + 1, 1);
+    phase(j + 2, 2);
+    phase(j + 3, 3);
+    j += kWideRound;
+  } while (j < jend);
 
-  // the two chunk halves meet in LDS: waves kh = 1 store, kh = 0 add
+  // the two chunk halves meet in LDS: waves kh = 1 store, kh = 0 add (the
+  // out-of-range DMA of the padding phases lands before the stages are reused)
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("s_barrier" ::: "memory");
   f32x16_t *red = reinterpret_cast<f32x16_t *>(smem) + (rw * MT) * 64 + lane;
@@ -2472,6 +2515,18 @@ __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const
   }
 }
 
+static void launch_wide_t(const WoqArgs &a, const WidePlan &p, dim3 grid, int shift, int gmask,
+                          float *partial, int gu, hipStream_t s) {
+  if (p.mt == 1 && !p.pad)
+    woq_wide_kernel<1, false><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial, gu);
+  else if (p.mt == 1)
+    woq_wide_kernel<1, true><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial, gu);
+  else if (!p.pad)
+    woq_wide_kernel<2, false><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial, gu);
+  else
+    woq_wide_kernel<2, true><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial, gu);
+}
+
 bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   const char *e = knob(kKnobWoqWide);  // "0" disables; "KS" forces the split count
   if (e && e[0] == '0') return false;
@@ -2493,11 +2548,17 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   if (G != 1 && (gs % 128 || (cpg & (cpg - 1)))) return false;
   const int phases = (int)(K / kWideKP);
   const int64_t blocks = (N + kWideRows - 1) / kWideRows;
-  int ks = 1;
-  // the most K splits (a divisor of the phase count) that keep the grid
-  // within about 1.25 rounds of 256 CUs
+  // the most K splits (a divisor of the phase count) of whole rounds of
+  // phases that keep the grid within about 1.25 rounds of 256 CUs; without
+  // such a split the padded form with the most splits
+  int ks = 0;
   for (int d = 1; d <= phases; ++d)
-    if (phases % d == 0 && blocks * d <= 320) ks = d;
+    if (phases % d == 0 && (phases / d) % kWideRound == 0 && blocks * d <= 320) ks = d;
+  if (ks == 0) {
+    ks = 1;
+    for (int d = 1; d <= phases; ++d)
+      if (phases % d == 0 && blocks * d <= 320) ks = d;
+  }
   if (e) {
     const int f = std::atoi(e);
     if (f >= 1 && phases % f == 0) ks = f;
@@ -2509,6 +2570,7 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   p->mt = M <= 32 ? 1 : 2;
   p->splits = ks;
   p->pps = phases / ks;
+  p->pad = p->pps % kWideRound != 0;
   return true;
 }
 
@@ -2535,12 +2597,11 @@ hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace,
   if (p.splits > 1 && !partial) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((a.N + kWideRows - 1) / kWideRows), (unsigned)p.splits);
   if (knob(kKnobWoqDebug))
-    std::fprintf(stderr, "[zt] woq wide M=%lld N=%lld K=%lld: MT=%d splits=%d phases/split=%d\n",
-                 (long long)a.M, (long long)a.N, (long long)a.K, p.mt, p.splits, p.pps);
-  if (p.mt == 1)
-    woq_wide_kernel<1><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, partial, 0);
-  else
-    woq_wide_kernel<2><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial, 0);
+    std::fprintf(stderr,
+                 "[zt] woq wide M=%lld N=%lld K=%lld: MT=%d splits=%d phases/split=%d%s\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, p.mt, p.splits, p.pps,
+                 p.pad ? " (padded)" : "");
+  launch_wide_t(a, p, grid, shift, gmask, partial, 0, s);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const int64_t n4 = a.M * (a.N / 4);
@@ -2565,10 +2626,7 @@ bool woq_try_wide_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
   if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq wide gate_up M=%lld N=%lld K=%lld: MT=%d\n", (long long)a.M,
                  (long long)a.N, (long long)a.K, p.mt);
-  if (p.mt == 1)
-    woq_wide_kernel<1><<<grid, dim3(512), woq_wide_lds<1>(), s>>>(a, p.pps, shift, gmask, nullptr, gu);
-  else
-    woq_wide_kernel<2><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, nullptr, gu);
+  launch_wide_t(a, p, grid, shift, gmask, nullptr, gu, s);
   *err = hipGetLastError();
   return true;
 }

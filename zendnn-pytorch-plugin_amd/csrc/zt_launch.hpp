@@ -64,7 +64,8 @@ hipError_t launch_silu_mul_halves(const float *h, int64_t ld_h, int64_t M, int64
 struct WidePlan {
   int mt;      // 32-token tiles (1 or 2)
   int splits;  // K splits
-  int pps;     // 512-k phases per split
+  int pps;     // 256-k phases per split
+  bool pad;    // pps not a multiple of 4: the padded kernel form
 };
 bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p);
 size_t woq_wide_workspace(const WidePlan &p, int64_t M, int64_t N);
