@@ -337,6 +337,50 @@ def bench_decode_layer(M, args, gen):
             "layer_copies": len(layers), "calls_timed": SECONDARY_REPS * len(calls)}
 
 
+FLOOR_BIN = os.path.join(ROOT, "tests", "native", "read_floor")
+
+
+def bench_floors(args, gen):
+    """Each Llama-3-8B decode projection (the layer bench's four calls) at
+    M = 1 / 8 / 16 / 64, timed alone over rotating weight copies, beside the
+    read floor of its algorithmic bytes: tests/native/read_floor, a plain
+    grid-stride read of the same number of bytes, timed the same way (HIP
+    graph replays of 20 back-to-back launches over buffers rotated through
+    more than 512 MB), and the in-graph cost of an empty launch."""
+    import subprocess
+    rows = []
+    for name, N, K, post in LLAMA:
+        per_copy = N * K // 2 + (K // 128) * N * 2
+        lin = WoqLinear(64, N, K, post=post, copies=copies_for(per_copy), gen=gen)
+        x64, extra64 = lin.x, lin.extra
+        for M in (1, 8, 16, 64):
+            lin.M, lin.x = M, x64[:M]
+            lin.extra = None if extra64 is None else extra64[:M]
+            calls = [lambda i=i: lin(i) for i in range(len(lin.w))]
+            t = graph_time(calls, SECONDARY_REPS, args.warmup) / len(calls)
+            rows.append({"shape": name, "N": N, "K": K, "M": M, "bytes": lin.bytes(),
+                         "us": round(t * 1e6, 3)})
+        del lin, x64, extra64
+        torch.cuda.empty_cache()
+    sizes = sorted({r["bytes"] for r in rows})
+    out = subprocess.run([FLOOR_BIN] + [str(b) for b in sizes], check=True,
+                         capture_output=True, text=True).stdout
+    floors, empty = {}, None
+    for line in out.splitlines():
+        d = json.loads(line)
+        if "empty_launch_us" in d:
+            empty = d["empty_launch_us"]
+        else:
+            floors[d["bytes"]] = d
+    for r in rows:
+        f = floors[(r["bytes"] + 15) // 16 * 16]
+        r["floor_us"] = f["us"]
+        r["floor_GBps"] = f["GBps"]
+        r["ratio"] = round(r["us"] / f["us"], 3)
+        r["GBps"] = round(r["bytes"] / r["us"] / 1e3, 1)
+    return {"rows": rows, "empty_launch_us": empty}
+
+
 def bench_dyn(M, shapes, args, gen, asym=False):
     """dynamic_qlinear over `shapes`, the weights rotated through enough
     copies that one pass reads more than ROTATE_BYTES (the 256 MB Infinity
@@ -586,7 +630,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default=None,
                     help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | moe | traffic"
-                         " | pmc | decode_pmc")
+                         " | pmc | decode_pmc | floors (not part of the default run)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline-child", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -612,6 +656,8 @@ def main():
             decode_pmc_pass(gen)
             return
         res = {}
+        if only == "floors":
+            res["decode_floors"] = bench_floors(args, gen)
         if only in (None, "config0"):
             res["config0"] = bench_config0(args, gen)
         if only in (None, "decode"):

@@ -5,6 +5,8 @@
 * zentorch/_C.so -- TORCH_LIBRARY(zentorch) registration and the AOTInductor
   shims of include/shim_cuda_zentorch.h, linked against the library above and
   PyTorch-ROCm.
+* tests/native/read_floor -- a plain streaming read of given sizes, the read
+  floor bench.py --only floors reports beside the decode kernels.
 * tests/native/bf16_rne_check -- a GPU program that checks the kernels' bf16
   rounding on every fp32 bit pattern (run by tests/test_bf16_rne_gpu.py).
 
@@ -108,6 +110,10 @@ def build(verbose=False, jobs=8):
     check = os.path.join(ROOT, "tests", "native", "bf16_rne_check")
     _run([HIPCC] + HIP_FLAGS + ["-o", check + ".tmp", check + ".hip"], verbose)
     os.replace(check + ".tmp", check)
+    # the plain streaming read bench.py --only floors times beside the library
+    floor = os.path.join(ROOT, "tests", "native", "read_floor")
+    _run([HIPCC] + HIP_FLAGS + ["-o", floor + ".tmp", floor + ".hip"], verbose)
+    os.replace(floor + ".tmp", floor)
     return hiplib, clib
 
 
