@@ -416,6 +416,9 @@ def bench_woq_prefill(args, gen):
             "weight_copies": copies, "calls_timed": SECONDARY_REPS * len(calls)}
 
 
+MOE_CALLS_PER_GRAPH = 4
+
+
 def bench_moe(args, gen):
     """Mixtral-shaped int4 MoE FFN, 8 experts, hidden 4096,
     intermediate 14336, top-2 of router logits over 256 tokens, through
@@ -441,14 +444,19 @@ def bench_moe(args, gen):
     out = torch.empty_like(x)
     call = lambda: ops.zentorch_fused_moe(out, x, w13, w2, None, None, wts, ids, False,
                                           "silu", s13, s2)
-    t = graph_time([call], SECONDARY_REPS, args.warmup)
+    # MOE_CALLS_PER_GRAPH back-to-back calls per graph replay, so the replay's
+    # own launch cost is spread as in the other workloads; the 705 MB of
+    # expert weights are more than the 256 MB Infinity Cache holds, so every
+    # call reads them from HBM
+    t = graph_time([call] * MOE_CALLS_PER_GRAPH, SECONDARY_REPS, args.warmup) / MOE_CALLS_PER_GRAPH
     wbytes = E * (2 * I * H // 2 + H * I // 2) + E * (H // 128 * 2 * I + I // 128 * H) * 2
     byts = wbytes + T * H * 2 * 2
     flops = 2 * T * k * (2 * I * H + H * I)
     return {"T": T, "H": H, "I": I, "E": E, "topk": k, "s_per_layer": t,
             "GBps": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / HBM_PEAK_GBS,
             "TFLOPS": flops / t / 1e12, "frac_bf16_peak": flops / t / 1e12 / BF16_PEAK_TFLOPS,
-            "weight_bytes": wbytes, "bytes_per_layer": byts, "calls_timed": SECONDARY_REPS}
+            "weight_bytes": wbytes, "bytes_per_layer": byts,
+            "calls_timed": SECONDARY_REPS * MOE_CALLS_PER_GRAPH}
 
 
 # ------------------------------------------------------------ CPU baseline
