@@ -542,12 +542,16 @@ def test_prefill_one_round_192_default_kernel():
 # only for the shapes where it measured faster): group sizes 128 / 256 /
 # 1024 and per channel, ragged N, every M up to 16, and the same result as
 # the other decode kernels on these shapes
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 13, 16])
-@pytest.mark.parametrize("K,N,G", [(2048, 16, 16), (4096, 4096, 32), (4096, 1000, 16),
-                                   (8192, 256, 8), (8192, 112, 1), (14336, 4096, 112)])
+# (only the cases whose x [M, K] fits the lean kernel's LDS; the other
+# kernels take the rest)
+_LEAN_CASES = [(M, K, N, G) for M in (1, 2, 3, 4, 7, 8, 13, 16)
+               for K, N, G in ((2048, 16, 16), (4096, 4096, 32), (4096, 1000, 16),
+                               (8192, 256, 8), (8192, 112, 1), (14336, 4096, 112))
+               if M * (K + 8) * 2 <= 160 * 1024]
+
+
+@pytest.mark.parametrize("M,K,N,G", _LEAN_CASES)
 def test_lean_kernel_vs_oracle(M, K, N, G, knobs):
-    if M * (K + 8) * 2 > 160 * 1024:
-        pytest.skip("x does not fit the lean kernel's LDS (the other kernels take it)")
     knobs.set("ZT_WOQ_LEAN", "1")
     y, y_ref = run_case(M, K, N, G, seed=M * 7 + G)
     knobs.set("ZT_WOQ_LEAN", "0")
