@@ -176,7 +176,9 @@ size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K, int64_t N);
  * GPU (different streams, or threads without ordering) race and must not be
  * issued.  Nothing in the scratch needs to start at zero; it keeps the last
  * call's contents.  Results equal zt_dynamic_qlinear's bit for bit (the same
- * kernels).  Call with the stream's device current.
+ * kernels).  The call uses the array of the stream's device (the null stream:
+ * the current device), making that device current for the call and
+ * restoring the caller's current device afterwards.
  */
 #define ZT_DYN_SCRATCH_BYTES (32u << 20)
 

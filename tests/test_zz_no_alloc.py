@@ -98,3 +98,19 @@ def test_scratch_refuses_oversized_call():
                                       C.DT[torch.bfloat16], C._stream())
     assert rc == 1
     assert b"scratch" in L.zt_last_error_string()
+
+
+def test_scratch_on_a_side_stream():
+    # a stream other than the null stream: the call takes the array of the
+    # stream's device and leaves the caller's current device as it was
+    M, N, K = 64, 1000, 2048
+    x, w, sw, b = case(M, N, K, seed=5)
+    xd, wd, sd, bd = x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV)
+    y_ws = C.dynamic_qlinear(xd, wd, sd, bd)
+    dev_before = torch.cuda.current_device()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        y_sc = scratch_call(xd, wd, sd, bd)
+    assert torch.cuda.current_device() == dev_before
+    assert torch.equal(y_sc, y_ws)

@@ -653,10 +653,10 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices];
 
-int scratch_address(const char *op, void **out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(ZT_EHIP, "%s: no current HIP device (or device id %d >= %d)", op, dev,
+// The array's address on device `dev`, which must be the current device.
+int scratch_address(const char *op, int dev, void **out) {
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ZT_EHIP, "%s: device id %d out of range (at most %d devices)", op, dev,
                 kMaxDevices);
   std::lock_guard<std::mutex> g(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
@@ -690,11 +690,27 @@ int zt_dynamic_qlinear_scratch(const void *x, int32_t x_dtype, int64_t M, int64_
     return fail(ZT_EINVAL, "%s: M=%lld x K=%lld needs %zu bytes of scratch, more than the "
                 "%zu this entry point holds (use zt_dynamic_qlinear with a workspace)",
                 op, (long long)M, (long long)K, need, (size_t)ZT_DYN_SCRATCH_BYTES);
+  // the stream's device holds the array this call uses; it is made current
+  // for the call (and the caller's current device restored) when it is not
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int cur = -1, dev = -1;
+  if (hipGetDevice(&cur) != hipSuccess)
+    return fail(ZT_EHIP, "%s: no current HIP device", op);
+  if (s == nullptr) {
+    dev = cur;
+  } else if (hipStreamGetDevice(s, &dev) != hipSuccess) {
+    return fail(ZT_EHIP, "%s: cannot query the stream's device", op);
+  }
+  if (dev != cur && hipSetDevice(dev) != hipSuccess)
+    return fail(ZT_EHIP, "%s: cannot make the stream's device %d current", op, dev);
   void *ws = nullptr;
-  const int rc = scratch_address(op, &ws);
-  if (rc) return rc;
-  return zt_dynamic_qlinear(x, x_dtype, M, K, w, N, w_scales, w_scales_dtype, bias, bias_dtype,
+  int rc = scratch_address(op, dev, &ws);
+  if (rc == ZT_OK)
+    rc = zt_dynamic_qlinear(x, x_dtype, M, K, w, N, w_scales, w_scales_dtype, bias, bias_dtype,
                             post, y, y_dtype, ws, (size_t)ZT_DYN_SCRATCH_BYTES, stream);
+  if (dev != cur && hipSetDevice(cur) != hipSuccess && rc == ZT_OK)
+    return fail(ZT_EHIP, "%s: cannot restore the current device %d", op, cur);
+  return rc;
 }
 
 int zt_woq_repack_weight(const int8_t *w, int64_t N, int64_t K, int32_t *out,
