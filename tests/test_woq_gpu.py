@@ -108,12 +108,21 @@ def test_wide_kernel_vs_oracle(M, K, N, G):
     run_case(M, K, N, G, kernel="wide", seed=M + K + N, bias=(M % 2 == 1))
 
 
-@pytest.mark.parametrize("splits", ["1", "2", "4"])
+@pytest.mark.parametrize("splits", ["1", "2", "4", "8"])
 @pytest.mark.parametrize("post,nbuf", [(("gelu_tanh",), 0), (("mul", "add"), 2),
                                        (("silu", "mul"), 1)])
 def test_wide_kernel_post_ops_and_splits(splits, post, nbuf, knobs):
     knobs.set("ZT_WOQ_WIDE", splits)
     run_case(40, 2048, 264, 16, kernel="wide", post=post, nbuf=nbuf, seed=21, bias=True)
+
+
+# split counts of the reduce kernel's remaining unrolled form (6) and of its
+# general form past eight splits (12 = eight, then four one by one); K =
+# 3072 is 12 phases of 256
+@pytest.mark.parametrize("splits", ["6", "12"])
+def test_wide_kernel_reduce_split_counts(splits, knobs):
+    knobs.set("ZT_WOQ_WIDE", splits)
+    run_case(33, 3072, 136, 24, kernel="wide", post=("add",), nbuf=1, seed=int(splits), bias=True)
 
 
 def test_wide_kernel_strided_x():

@@ -2477,26 +2477,40 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
   }
 }
 
-// y = epilogue(sum over the splits of partial[split][m][n], in split order)
+// y = epilogue(sum over the splits of partial[split][m][n], in split order).
+// The partials were written by another kernel, most of them on other XCDs,
+// so each load is a round trip to memory: every split's load is issued
+// before the first add.  S = 2..8 splits unroll fully; S = 0 (any count)
+// issues eight at a time.  The adds run in split order either way.
+template <int S>
 __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const float *partial,
                                                                 int splits) {
   const int M = (int)a.M, N = (int)a.N;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)M * (N / 4)) return;
   const int m = (int)(idx / (N / 4)), n = (int)(idx % (N / 4)) * 4;
-  // four splits' loads in flight at a time, added in split order
   const size_t stride = (size_t)M * N;
   const float *p0 = partial + (size_t)m * N + n;
-  f32x4_t v = *reinterpret_cast<const f32x4_t *>(p0);
-  int s = 1;
-  for (; s + 4 <= splits; s += 4) {
-    f32x4_t q[4];
+  f32x4_t v;
+  if constexpr (S > 0) {
+    f32x4_t q[S];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q[i] = *reinterpret_cast<const f32x4_t *>(p0 + (s + i) * stride);
+    for (int i = 0; i < S; ++i) q[i] = *reinterpret_cast<const f32x4_t *>(p0 + i * stride);
+    v = q[0];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v += q[i];
+    for (int i = 1; i < S; ++i) v += q[i];
+  } else {
+    v = *reinterpret_cast<const f32x4_t *>(p0);
+    int s = 1;
+    for (; s + 8 <= splits; s += 8) {
+      f32x4_t q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const f32x4_t *>(p0 + (s + i) * stride);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v += q[i];
+    }
+    for (; s < splits; ++s) v += *reinterpret_cast<const f32x4_t *>(p0 + s * stride);
   }
-  for (; s < splits; ++s) v += *reinterpret_cast<const f32x4_t *>(p0 + s * stride);
   float f[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -2605,8 +2619,15 @@ hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace,
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const int64_t n4 = a.M * (a.N / 4);
-  woq_splitk_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(a, partial,
-                                                                                   p.splits);
+  const dim3 rgrid((unsigned)((n4 + 255) / 256)), rblock(256);
+  switch (p.splits) {
+#define ZT_REDUCE_CASE(S_) \
+  case S_: woq_splitk_reduce_kernel<S_><<<rgrid, rblock, 0, s>>>(a, partial, p.splits); break;
+    ZT_REDUCE_CASE(2) ZT_REDUCE_CASE(3) ZT_REDUCE_CASE(4) ZT_REDUCE_CASE(5)
+    ZT_REDUCE_CASE(6) ZT_REDUCE_CASE(7) ZT_REDUCE_CASE(8)
+#undef ZT_REDUCE_CASE
+    default: woq_splitk_reduce_kernel<0><<<rgrid, rblock, 0, s>>>(a, partial, p.splits); break;
+  }
   return hipGetLastError();
 }
 
