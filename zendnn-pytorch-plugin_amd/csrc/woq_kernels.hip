@@ -1,6 +1,6 @@
 // int4 weight-only linear kernels for gfx950 (zentorch_woq_linear family).
 //
-// Numerics (all three kernels): each weight is dequantised to the bf16 value
+// Numerics (every kernel in this file): each weight is dequantised to the bf16 value
 // bf16_rne(q*s) (or the zero-point forms, woq_dequant.hpp) and multiplied
 // with the bf16 activations on the bf16 MFMA with fp32 accumulation; bias
 // and post-ops run in fp32 and the output is rounded once.  That is the
