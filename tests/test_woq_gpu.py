@@ -434,10 +434,11 @@ def test_wave_kernel_ragged_n(M, K, N, G, knobs):
     check_close(y, y_stream.cpu())
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8])
 @pytest.mark.parametrize("K,I,G", [(4096, 256, 32), (2048, 1040, 1), (8192, 64, 64)])
 def test_wave_kernel_gate_up(M, K, I, G, knobs):
-    knobs.set("ZT_WOQ_WAVE", "1")  # also below 5 rows
+    knobs.set("ZT_WOQ_PERSIST", "0")
+    knobs.set("ZT_WOQ_WAVE", "1")  # also below 3 rows
     y, y_ref = run_gate_up(M, K, I, G, seed=M + I)
     knobs.set("ZT_WOQ_WAVE", "0")
     y_stream, _ = run_gate_up(M, K, I, G, seed=M + I)
@@ -466,8 +467,10 @@ def test_persist_kernel_post_ops(post, nbuf, knobs):
     run_case(8, 4096, 8200, 32, post=post, nbuf=nbuf, seed=6, bias=True)
 
 
-# None: the library's choice, the persistent kernel from 9 rows
-@pytest.mark.parametrize("variant", ["1", "2", None])
+# None: the library's choice, the persistent kernel from 3 rows; "1" / "2"
+# 8 / 16 waves over units of 8 gate rows and their 8 up rows, "1p" / "2p"
+# over gate/up tile pairs
+@pytest.mark.parametrize("variant", ["1", "2", "1p", "2p", None])
 @pytest.mark.parametrize("M", [1, 5, 12, 16])
 @pytest.mark.parametrize("K,I,G", [(4096, 256, 32), (2048, 4112, 1), (4096, 14336, 32)])
 def test_persist_kernel_gate_up(variant, M, K, I, G, knobs):
@@ -586,10 +589,13 @@ def test_lean_kernel_strided_x(knobs):
     check_close(y, y_ref)
 
 
+# form "1": one 16-row tile per workgroup, its rows 0-7 gate and 8-15 up;
+# "p": a gate tile and its up tile per workgroup
+@pytest.mark.parametrize("form", ["1", "p"])
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("K,I,G", [(4096, 256, 32), (2048, 1040, 1), (8192, 64, 64)])
-def test_lean_kernel_gate_up(M, K, I, G, knobs):
-    knobs.set("ZT_WOQ_LEAN", "1")
+def test_lean_kernel_gate_up(M, K, I, G, form, knobs):
+    knobs.set("ZT_WOQ_LEAN", form)
     y, y_ref = run_gate_up(M, K, I, G, seed=M + I + 2)
     knobs.set("ZT_WOQ_LEAN", "0")
     y_other, _ = run_gate_up(M, K, I, G, seed=M + I + 2)

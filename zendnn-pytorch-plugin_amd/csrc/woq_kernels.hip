@@ -21,10 +21,10 @@
 //    Rows past what one launch holds go in blocks of 16.
 //  * woq_lean_kernel  1..16 rows in the fast mode where it measured faster
 //    (the long-K down projection and the widest matrices at few rows, the
-//    merged gate_up at 2..4 rows): the stream kernel's work split with each
+//    merged gate_up at 1..2 rows): the stream kernel's work split with each
 //    chunk's scales loaded beside its weights, x read only by the lanes of
 //    real tokens and two MFMA accumulators.
-//  * woq_persist_kernel  the merged gate_up at 9..16 rows and plain calls
+//  * woq_persist_kernel  the merged gate_up at 3..16 rows and plain calls
 //    of 12288 rows or more: one workgroup per CU loops over row units with
 //    x in registers and the next units' weights in flight.
 //  * woq_decode_kernel   the older decode kernel for shapes the two above do
@@ -1644,8 +1644,9 @@ static hipError_t launch_wave_t(const WoqArgs &a, hipStream_t s, int shift, int 
 // The wave-independent kernel where it applies: fast mode, bf16 x with
 // 16-byte rows, M <= 16, K = 16 waves x CPW chunks (CPW 1, 2 or 4) and the
 // x slices within 64 KB, more than 4096 rows unless forced; gu > 0 is the
-// merged gate_up (I = gu, a multiple of 16; "1" in ZT_WOQ_WAVE takes it
-// below 5 rows and on 4096 rows or fewer too).
+// merged gate_up (I = gu, a multiple of 16, a gate tile and its up tile per
+// workgroup; "1" in ZT_WOQ_WAVE takes it below 3 rows and on 4096 rows or
+// fewer too).
 static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                             int gu, hipError_t *err) {
   const char *e = knob(kKnobWoqWave);  // "0" disables
@@ -1660,10 +1661,11 @@ static bool try_launch_wave(const WoqArgs &a, hipStream_t s, int shift, int gmas
   const int cpw = (int)(a.K / (16 * 128));
   // measured against the stream kernel in the same process (graph replays
   // over rotating weights, Llama-3 8B shapes): QKV 6.3-6.4 us against
-  // 6.7-6.9 at M = 2..8, O even; the merged gate_up only from M = 5 (18.2 us
-  // against 20.0 at M = 8, but 18.2 against 17.3 at M = 1); the down
-  // projection (16 x 7 chunks, M <= 2) no faster, so CPW 7 is not used
-  if (gu && a.M < 5 && !e) return false;
+  // 6.7-6.9 at M = 2..8, O even; the merged gate_up from M = 3 when the
+  // persistent kernel does not take it (16.4-17.1 us at M = 3..8 against
+  // 17.1-19.1 on the lean and stream kernels); the down projection (16 x 7
+  // chunks, M <= 2) no faster, so CPW 7 is not used
+  if (gu && a.M < 3 && !e) return false;
   // at most one tile per CU (N <= 4096), the stream kernel's 8 waves did as
   // well or better on every box measured but one (4096 x 4096 at M = 1..8:
   // 4.96-5.38 us against 5.21-5.42), and its rocprof kernel durations agree
@@ -1731,7 +1733,15 @@ __global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg
   const int G0 = (int)gridDim.x;
   // units of this workgroup: blockIdx.x + i G0, i < nu
   const int nu = (units - (int)blockIdx.x + G0 - 1) / G0;  // >= 1: the grid is <= units
-  auto rowbase = [&](int u, int t) { return gu ? t * gu + u * 16 : (u * TPW + t) * 16; };
+  // weight row of row r of unit u's tile t: TPW consecutive 16-row tiles;
+  // with gu > 0 and TPW == 2 gate rows 16 u.. (t = 0) and their up rows
+  // (t = 1); with gu > 0 and TPW == 1 gate rows 8 u .. 8 u + 7, then their
+  // up rows (gu / 8 units instead of gu / 16)
+  constexpr bool kHalf = TPW == 1;
+  auto row_of = [&](int u, int t, int r) {
+    if (gu && kHalf) return u * 8 + r + (r < 8 ? 0 : gu - 8);
+    return (gu ? t * gu + u * 16 : (u * TPW + t) * 16) + r;
+  };
   // unconditional loads (a load under a lane condition becomes a branch,
   // and the compiler then drains every load in flight at it): a unit index
   // past nu re-reads the workgroup's last unit into a set nothing uses, and
@@ -1740,7 +1750,7 @@ __global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg
     const int u = (int)blockIdx.x + min(i, nu - 1) * G0;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int n = min(rowbase(u, t) + lr, N - 1);
+      const int n = min(row_of(u, t, lr), N - 1);
       const uint32_t row_off = (uint32_t)n * (uint32_t)KW * 4u + (uint32_t)lg * 16u;
 #pragma unroll
       for (int c = 0; c < CPW; ++c) {
@@ -1775,6 +1785,25 @@ __global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg
       for (int r = 0; r < 4; ++r) slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][r];
     __syncthreads();
     const int u = (int)blockIdx.x + i * G0;
+    if (gu && kHalf) {
+      for (int idx = tid; idx < 8 * M; idx += 64 * NW) {
+        const int m = idx >> 3, r8 = idx & 7;
+        const int jj = u * 8 + r8;
+        float g = 0.f, up = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          g += slab[(w * 16 + r8) * 17 + m];
+          up += slab[(w * 16 + 8 + r8) * 17 + m];
+        }
+        if (a.bias) {
+          g = g + load_elem(a.bias, a.b_dt, jj);
+          up = up + load_elem(a.bias, a.b_dt, gu + jj);
+        }
+        if (a.y_dt == ZT_DT_BF16) up = bf16_bits_to_f32(f32_to_bf16_bits(up));
+        store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + jj, unary_op(ZT_PO_SILU, g) * up);
+      }
+      return;
+    }
     if (gu) {
       for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
         const int m = idx / 16, nr = idx - m * 16;
@@ -1839,21 +1868,24 @@ static hipError_t launch_persist_t(const WoqArgs &a, hipStream_t s, int shift, i
 
 // The persistent kernel where it applies: fast mode, bf16 x with 16-byte
 // rows, M <= 16, K = NW waves x CPW chunks, gu > 0 the merged gate_up (I =
-// gu, a multiple of 16; units of a gate/up tile pair), else units of one
-// 16-row tile.  Taken by default with 16 waves where it measured faster (HIP-graph
-// replays over rotating weights): the merged gate_up from M = 9 (28672 x
-// 4096: 19.3 / 20.2 us at M = 12 / 16 against 25.1 / 25.8 for the wave
-// kernel, whose per-workgroup x copy then fills the LDS; within 0.6 us of
-// it at M <= 8), and plain calls from 12288 rows, three or more units per
-// CU (14336 x 4096: 10.2 / 10.7 / 12.6 us at M = 1 / 8 / 16 against 10.9 /
-// 11.9 / 13.5 for the stream kernel); QKV- and O-sized calls (1.5 and 1
-// unit per CU) are slower on it.  ZT_WOQ_PERSIST: "0" never, "1" / "2"
-// force 8 / 16 waves wherever the shape allows.
+// gu, a multiple of 16; units of 8 gate rows and their 8 up rows), else
+// units of one 16-row tile.  Taken by default with 16 waves where it
+// measured faster (HIP-graph replays over rotating weights): the merged
+// gate_up from M = 3 (28672 x 4096, one box: 16.8 / 17.0 / 17.1 / 17.4 /
+// 18.3 / 19.3 us at M = 3 / 6 / 8 / 9 / 12 / 16 against 18.9 / 18.7 / 18.2
+// / 17.8 / 18.3 / 19.3 on the wave kernel and 17.7 / 17.8 / 18.2 / 18.2 /
+// 18.8 / 20.0 here in gate/up tile pairs, 896 units for 256 workgroups
+// where half tiles make 1792, 7 each), and plain calls from 12288 rows,
+// three or more units per CU (14336 x 4096: 10.2 / 10.7 / 12.6 us at M = 1
+// / 8 / 16 against 10.9 / 11.9 / 13.5 for the stream kernel); QKV- and
+// O-sized calls (1.5 and 1 unit per CU) are slower on it.  ZT_WOQ_PERSIST: "0" never, "1" / "2"
+// force 8 / 16 waves wherever the shape allows ("1p" / "2p": the merged
+// gate_up in gate/up tile pairs instead of half tiles).
 static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                                int gu, hipError_t *err) {
   const char *e = knob(kKnobWoqPersist);
   if (e && e[0] == '0') return false;
-  if (!e && !(gu ? a.M >= 9 : a.N >= 12288)) return false;
+  if (!e && !(gu ? a.M >= 3 : a.N >= 12288)) return false;
   if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || (gu && gu % 16))
     return false;
   if (((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) ||
@@ -1863,8 +1895,11 @@ static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int g
   const int nw = e && e[0] == '1' ? 8 : 16;
   if (a.K % (nw * 128)) return false;
   const int cpw = (int)(a.K / (nw * 128));
-  // units: gate/up tile pairs, or single 16-row tiles of a plain call
-  const int units = gu ? (int)(gu / 16) : (int)((a.N + 15) / 16);  // rows past N read row N - 1
+  // units: one 16-row tile of 8 gate rows and their 8 up rows (a "p" in the
+  // knob: a gate tile and its up tile), or single 16-row tiles of a plain
+  // call (rows past N read row N - 1)
+  const bool pairs = gu && e && std::strchr(e, 'p');
+  const int units = gu ? (int)(gu / (pairs ? 16 : 8)) : (int)((a.N + 15) / 16);
   if (knob(kKnobWoqDebug))
     std::fprintf(stderr, "[zt] woq persist M=%lld N=%lld K=%lld gu=%d: NW=%d CPW=%d units=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, gu, nw, cpw, units);
@@ -1872,8 +1907,8 @@ static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int g
   // 16 CPW, D + 1 sets of 20 TPW CPW)
 #define ZT_PERSIST_CASE(NW_, CPW_, D_)                                              \
   if (nw == NW_ && cpw == CPW_) {                                                   \
-    *err = gu ? launch_persist_t<NW_, CPW_, 2, D_>(a, s, shift, gmask, gu, units)   \
-              : launch_persist_t<NW_, CPW_, 1, D_>(a, s, shift, gmask, 0, units);   \
+    *err = pairs ? launch_persist_t<NW_, CPW_, 2, D_>(a, s, shift, gmask, gu, units) \
+                 : launch_persist_t<NW_, CPW_, 1, D_>(a, s, shift, gmask, gu, units); \
     return true;                                                                    \
   }
   ZT_PERSIST_CASE(8, 2, 2) ZT_PERSIST_CASE(8, 4, 1) ZT_PERSIST_CASE(16, 1, 2)
@@ -1930,6 +1965,11 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
 //    consecutive MFMAs do not wait on each other's results.
 // Partials meet in LDS in wave order (deterministic), then the stream
 // kernel's epilogue (bias, post-ops, or silu(gate) * round(up) with gu).
+// With gu and TPW == 1 a workgroup's one 16-row tile is half gate, half up:
+// rows 0-7 are gate rows j0 .. j0 + 7 and rows 8-15 their up rows gu + j0
+// .., j0 = 8 * blockIdx.x, so the merged gate_up makes gu / 8 workgroups
+// (1792 for the Llama-3-8B gate_up, 7 per CU) where pairs of whole tiles
+// make gu / 16 (896, 3.5 per CU: half the CUs then carry a third more).
 template <int NW, int CPW, int TPW>
 __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_shift, int gmask,
                                                            int gu) {
@@ -1940,10 +1980,13 @@ __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_sh
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K, KW = K / 8;
   const int XP = stream_x_pitch(K);
   uint16_t *xl = reinterpret_cast<uint16_t *>(smem);
-  // first weight row of tile t: TPW consecutive tiles, or with gu the gate
-  // rows j0.. (t = 0) and the up rows gu + j0.. (t = 1)
-  auto rowbase = [&](int t) {
-    return gu ? t * gu + blockIdx.x * 16 : (blockIdx.x * TPW + t) * 16;
+  // weight row of row r of tile t: TPW consecutive tiles; with gu and
+  // TPW == 2 the gate rows j0.. (t = 0) and the up rows gu + j0.. (t = 1);
+  // with gu and TPW == 1 gate rows j0 .. j0 + 7, then their up rows
+  constexpr bool kHalf = TPW == 1;
+  auto row_of = [&](int t, int r) {
+    if (gu && kHalf) return (int)blockIdx.x * 8 + r + (r < 8 ? 0 : gu - 8);
+    return (gu ? t * gu + (int)blockIdx.x * 16 : ((int)blockIdx.x * TPW + t) * 16) + r;
   };
   const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
   const auto s_rs = make_rsrc(a.scales, (uint32_t)(a.G * N * 2));
@@ -1966,7 +2009,7 @@ __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_sh
     const uint32_t g = (uint32_t)(((c0 + c) >> cpg_shift) & gmask);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int n = min(rowbase(t) + lr, N - 1);
+      const int n = min(row_of(t, lr), N - 1);
       sr[t][c] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, (g * (uint32_t)N + (uint32_t)n) * 2u,
                                                       0, 0);
       wr[t][c] = __builtin_bit_cast(
@@ -2025,6 +2068,26 @@ __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_sh
         slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][0][r] + acc[t][1][r];
   }
   __syncthreads();
+  if (gu && kHalf) {
+    const int j0 = blockIdx.x * 8;
+    for (int idx = tid; idx < 8 * M; idx += 64 * NW) {
+      const int m = idx >> 3, r8 = idx & 7;
+      const int j = j0 + r8;
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        g += slab[(w * 16 + r8) * 17 + m];
+        u += slab[(w * 16 + 8 + r8) * 17 + m];
+      }
+      if (a.bias) {
+        g = g + load_elem(a.bias, a.b_dt, j);
+        u = u + load_elem(a.bias, a.b_dt, gu + j);
+      }
+      if (a.y_dt == ZT_DT_BF16) u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+      store_elem(a.y, a.y_dt, (int64_t)m * a.ldy + j, unary_op(ZT_PO_SILU, g) * u);
+    }
+    return;
+  }
   if (gu) {
     const int j0 = blockIdx.x * 16;
     for (int idx = tid; idx < 16 * M; idx += 64 * NW) {
@@ -2063,7 +2126,8 @@ template <int NW, int CPW, int TPW>
 static hipError_t launch_lean_t(const WoqArgs &a, hipStream_t s, int shift, int gmask, int gu) {
   const size_t x = (size_t)a.M * stream_x_pitch((int)a.K) * 2;
   const size_t slab = (size_t)NW * TPW * 16 * 17 * 4;
-  const unsigned blocks = gu ? (unsigned)(gu / 16) : (unsigned)((a.N + 16 * TPW - 1) / (16 * TPW));
+  const unsigned blocks = gu ? (unsigned)(gu / (TPW == 1 ? 8 : 16))
+                             : (unsigned)((a.N + 16 * TPW - 1) / (16 * TPW));
   woq_lean_kernel<NW, CPW, TPW><<<dim3(blocks), dim3(64 * NW), x > slab ? x : slab, s>>>(
       a, shift, gmask, gu);
   return hipGetLastError();
@@ -2076,12 +2140,14 @@ static hipError_t launch_lean_t(const WoqArgs &a, hipStream_t s, int shift, int 
 // Measured (default dispatch -> lean kernel, one box): 4096 x 14336 at
 // M = 1 / 2 / 4 10.5 -> 9.9, 10.6 -> 10.2, 11.6 -> 10.7 us; 14336 x 4096
 // at M = 1 / 2 11.0 -> 9.9, 11.0 -> 10.1 us and at M = 12 / 16 (against
-// the persistent kernel) 28672 x 4096 25.2 -> 23.6, 25.3 -> 23.8 us;
-// the merged 28672 x 4096 gate_up at M = 2 / 4 18.4 -> 17.8, 19.4 ->
-// 18.6 us.  QKV, the merged gate_up at M = 1 and M >= 8, and most shapes
-// at M = 8 stay where they are (2-43 % slower on the lean kernel).
+// the persistent kernel) 28672 x 4096 25.2 -> 23.6, 25.3 -> 23.8 us.
+// The merged 28672 x 4096 gate_up in half-gate / half-up tiles at M = 1 /
+// 2: 15.5 / 16.2 us, against 16.4-16.5 / 16.3 on the stream and wave
+// kernels and 17.1 / 17.2 in tile pairs; from M = 3 the wave kernel is
+// faster (M = 3 / 4: 16.6 / 16.4 against 17.3 / 18.2 here).  QKV and most
+// shapes at M = 8 stay where they are (2-43 % slower on the lean kernel).
 static bool lean_preferred(const WoqArgs &a, int gu) {
-  if (gu) return a.M >= 2 && a.M <= 4;
+  if (gu) return a.M <= 2;
   if (a.K >= 8192) return a.M <= 4;
   if (a.N >= 12288) return a.M <= 2 || (a.N >= 28672 && a.M >= 12);
   return false;
@@ -2093,22 +2159,27 @@ static bool lean_preferred(const WoqArgs &a, int gu) {
 // gate_up (I = gu, a multiple of 16).
 static bool try_launch_lean(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                             int gu, hipError_t *err) {
-  const char *e = knob(kKnobWoqLean);  // "0" never, "1" wherever it applies
+  // "0" never, "1" wherever it applies, "p" also, with the merged gate_up in
+  // pairs of whole tiles instead of half-gate / half-up tiles
+  const char *e = knob(kKnobWoqLean);
   if (e && e[0] == '0') return false;
+  const bool pairs = e && e[0] == 'p';
   if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || a.K % 1024 ||
       (gu && gu % 16) || !stream_x_dma(a, 1) || a.N * (a.K / 2) >= (int64_t)kOobOffset ||
       a.G * a.N * 2 >= (int64_t)kOobOffset)
     return false;
   if ((size_t)a.M * stream_x_pitch((int)a.K) * 2 > kStreamLdsMax) return false;
-  if (!(e && e[0] == '1') && !lean_preferred(a, gu)) return false;
+  if (!(e && (e[0] == '1' || pairs)) && !lean_preferred(a, gu)) return false;
   const int cpw = (int)(a.K / 1024);
   if (knob(kKnobWoqDebug))
-    std::fprintf(stderr, "[zt] woq lean M=%lld N=%lld K=%lld gu=%d: NW=8 CPW=%d\n",
-                 (long long)a.M, (long long)a.N, (long long)a.K, gu, cpw);
+    std::fprintf(stderr, "[zt] woq lean M=%lld N=%lld K=%lld gu=%d%s: NW=8 CPW=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, gu,
+                 gu ? (pairs ? " (tile pairs)" : " (half tiles)") : "", cpw);
 #define ZT_LEAN_CASE(CPW_)                                                         \
   if (cpw == CPW_) {                                                               \
-    *err = gu ? launch_lean_t<8, CPW_, 2>(a, s, shift, gmask, gu)                  \
-              : launch_lean_t<8, CPW_, 1>(a, s, shift, gmask, 0);                  \
+    *err = !gu     ? launch_lean_t<8, CPW_, 1>(a, s, shift, gmask, 0)              \
+           : pairs ? launch_lean_t<8, CPW_, 2>(a, s, shift, gmask, gu)             \
+                   : launch_lean_t<8, CPW_, 1>(a, s, shift, gmask, gu);            \
     return true;                                                                   \
   }
   ZT_LEAN_CASE(2) ZT_LEAN_CASE(4) ZT_LEAN_CASE(8) ZT_LEAN_CASE(14)

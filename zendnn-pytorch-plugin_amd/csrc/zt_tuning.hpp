@@ -17,7 +17,7 @@ enum Knob {
   kKnobWoqGemm,         // ZT_WOQ_GEMM: "o" 16x16 kernel, "d" 16x16 DMA, "1" 128x128, "w" / "v" / "x" load-wave kernel (4 / 3 stages, 256x192)
   kKnobWoqDebug,        // ZT_WOQ_DEBUG: print each launch shape to stderr
   kKnobWoqWave,         // ZT_WOQ_WAVE: "0" disables the wave-independent decode kernel
-  kKnobWoqPersist,      // ZT_WOQ_PERSIST: "0" never, "1" / "2" force the persistent decode kernel (8 / 16 waves)
+  kKnobWoqPersist,      // ZT_WOQ_PERSIST: "0" never, "1" / "2" force the persistent decode kernel (8 / 16 waves), "1p" / "2p" with gate_up tile pairs
   kKnobS8Skinny32,      // ZT_S8_SKINNY32: "TPW,PF,NW" of the 32-token skinny kernel
   kKnobS8Skinny,        // ZT_S8_SKINNY: "TPW,PF,NW" of the 16-token skinny kernel
   kKnobS8Frag,          // ZT_S8_FRAG: "0" never, "1" from M = 1 (fragment-order qx)
@@ -26,7 +26,7 @@ enum Knob {
   kKnobS8Kind,          // ZT_S8_KIND: w load-wave kernel (default), n 32x32 DMA kernel, r / 2 / 3 older kernels
   kKnobS8Split,         // ZT_S8_SPLIT: "0" disables the split-K skinny kernel, "2"-"4" its load depth
   kKnobMoeBn,           // ZT_MOE_BN: column tile of the MoE GEMMs
-  kKnobWoqLean,         // ZT_WOQ_LEAN: "0" never, "1" forces the lean decode kernel wherever it applies
+  kKnobWoqLean,         // ZT_WOQ_LEAN: "0" never, "1" forces the lean decode kernel wherever it applies, "p" too with gate_up tile pairs
   kKnobCount
 };
 
