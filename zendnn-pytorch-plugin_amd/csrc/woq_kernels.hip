@@ -1731,8 +1731,21 @@ __global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg
                        x_rs, (uint32_t)(xrow * a.ldx * 2 + ((c0 + c) * 128 + 32 * lg + 8 * i) * 2),
                        0, 0));
   const int G0 = (int)gridDim.x;
-  // units of this workgroup: blockIdx.x + i G0, i < nu
-  const int nu = (units - (int)blockIdx.x + G0 - 1) / G0;  // >= 1: the grid is <= units
+  // units of this workgroup: ub + i us, i < nu (>= 1: the grid is <= units).
+  // Round robin (ub = blockIdx.x, us = G0), or for the merged gate_up's half
+  // tiles on a grid of whole XCD groups, a contiguous range of units per XCD
+  // (XCD x = blockIdx.x % 8), dealt round robin over its G0 / 8 workgroups,
+  // so the scale lines that neighbouring units share are fetched once into
+  // that XCD's L2
+  int ub = (int)blockIdx.x, us = G0, nu = (units - (int)blockIdx.x + G0 - 1) / G0;
+  if (gu && TPW == 1 && (G0 & 7) == 0) {
+    const int x = (int)blockIdx.x & 7, jw = (int)blockIdx.x >> 3, per = G0 >> 3;
+    const int q = units >> 3, r = units & 7;
+    const int cnt = q + (x < r ? 1 : 0);  // >= per: G0 <= units
+    ub = x * q + (x < r ? x : r) + jw;
+    us = per;
+    nu = (cnt - jw + per - 1) / per;
+  }
   // weight row of row r of unit u's tile t: TPW consecutive 16-row tiles;
   // with gu > 0 and TPW == 2 gate rows 16 u.. (t = 0) and their up rows
   // (t = 1); with gu > 0 and TPW == 1 gate rows 8 u .. 8 u + 7, then their
@@ -1747,7 +1760,7 @@ __global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg
   // past nu re-reads the workgroup's last unit into a set nothing uses, and
   // rows past N (plain calls' last unit) re-read row N - 1, never stored
   auto issue = [&](int i, PersistSet<NW, CPW, TPW> &S) {
-    const int u = (int)blockIdx.x + min(i, nu - 1) * G0;
+    const int u = ub + min(i, nu - 1) * us;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int n = min(row_of(u, t, lr), N - 1);
@@ -1784,7 +1797,7 @@ __global__ __launch_bounds__(64 * NW) void woq_persist_kernel(WoqArgs a, int cpg
 #pragma unroll
       for (int r = 0; r < 4; ++r) slab[((wv * TPW + t) * 16 + 4 * lg + r) * 17 + lr] = acc[t][r];
     __syncthreads();
-    const int u = (int)blockIdx.x + i * G0;
+    const int u = ub + i * us;
     if (gu && kHalf) {
       for (int idx = tid; idx < 8 * M; idx += 64 * NW) {
         const int m = idx >> 3, r8 = idx & 7;
@@ -1984,8 +1997,12 @@ __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_sh
   // TPW == 2 the gate rows j0.. (t = 0) and the up rows gu + j0.. (t = 1);
   // with gu and TPW == 1 gate rows j0 .. j0 + 7, then their up rows
   constexpr bool kHalf = TPW == 1;
+  // half tiles: the workgroups of one XCD take consecutive units, so the
+  // scale lines that neighbouring units share are fetched once into that
+  // XCD's L2 (round robin, every XCD would fetch each line)
+  const int hu = gu && kHalf ? xcd_contiguous_tile((int)blockIdx.x, (int)gridDim.x) : 0;
   auto row_of = [&](int t, int r) {
-    if (gu && kHalf) return (int)blockIdx.x * 8 + r + (r < 8 ? 0 : gu - 8);
+    if (gu && kHalf) return hu * 8 + r + (r < 8 ? 0 : gu - 8);
     return (gu ? t * gu + (int)blockIdx.x * 16 : ((int)blockIdx.x * TPW + t) * 16) + r;
   };
   const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * KW * 4));
@@ -2069,7 +2086,7 @@ __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_sh
   }
   __syncthreads();
   if (gu && kHalf) {
-    const int j0 = blockIdx.x * 8;
+    const int j0 = hu * 8;
     for (int idx = tid; idx < 8 * M; idx += 64 * NW) {
       const int m = idx >> 3, r8 = idx & 7;
       const int j = j0 + r8;
