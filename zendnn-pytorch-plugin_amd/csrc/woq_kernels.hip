@@ -2035,7 +2035,11 @@ __global__ __launch_bounds__(64 * NW) void woq_lean_kernel(WoqArgs a, int cpg_sh
                                  (uint32_t)(c0 + c) * 64u, 0, 0));
     }
   };
-  constexpr int D = CPW < 2 ? CPW : 2;
+  // chunks in flight per wave: all of them up to 4 (the merged gate_up at M
+  // = 2, K = 4096: 16.3-16.8 -> 15.5-15.6 us), else 2 (the down
+  // projection's 14 chunks: 9.6 / 10.6 us at M = 1 / 4 against 10.0-10.4 /
+  // 11.1-11.6 with 4 or 6)
+  constexpr int D = CPW <= 4 ? CPW : 2;
 #pragma unroll
   for (int c = 0; c < D; ++c) load_chunk(c);
   // this wave's x DMA was issued before its 2 * TPW * D loads: once at most
