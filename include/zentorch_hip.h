@@ -343,7 +343,7 @@ const char *zt_last_error_string(void);
  * variable that sets it when the library is loaded (ZT_WOQ_FORCE_KERNEL,
  * ZT_WOQ_DECODE_PLAN, ZT_WOQ_STREAM, ZT_WOQ_WIDE, ZT_WOQ_GEMM, ZT_WOQ_DEBUG,
  * ZT_WOQ_WAVE, ZT_WOQ_PERSIST, ZT_S8_SKINNY32, ZT_S8_SKINNY, ZT_S8_FRAG, ZT_S8_FORCE,
- * ZT_S8_TILE, ZT_S8_KIND, ZT_S8_SPLIT, ZT_MOE_BN, ZT_WOQ_LEAN); the environment is not
+ * ZT_S8_TILE, ZT_S8_KIND, ZT_S8_SPLIT, ZT_MOE_BN, ZT_WOQ_LEAN, ZT_S8_FUSED); the environment is not
  * read again.  value NULL or
  * "" unsets the knob.  Returns ZT_EINVAL for an unknown name.  Launches
  * already enqueued are not affected.

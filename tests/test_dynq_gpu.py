@@ -162,6 +162,72 @@ def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, knobs):
 # holds its exchange (two K halves per 96-column tile, the second to finish
 # adds the other's int32 partial): bit-identical to the unsplit kernel (the
 # least workspace), on ragged M, N past a tile, N % 4 != 0, one or an odd
+# The skinny GEMM with the per-token quantisation in its prologue (one
+# launch for at most 16 tokens of bf16 x): bit-identical to the quantise
+# launch + skinny GEMM (the same qx, sx and int32 sums) for every register
+# layout it has (1, 2 and 4 vectors per thread and row), ragged N and K,
+# with and without bias.  ZT_WOQ_DEBUG names the kernel that ran.
+@pytest.mark.parametrize("M,K,N", [(1, 64, 8), (2, 4096, 11008), (3, 192, 70), (5, 4096, 6144),
+                                   (8, 4096, 4096), (9, 4096, 200), (16, 4096, 136),
+                                   (4, 8192, 300), (3, 5120, 77), (2, 14336, 4096),
+                                   (1, 16384, 64)])
+@pytest.mark.parametrize("bias", [True, False])
+def test_dynamic_qlinear_fused_quantise(M, K, N, bias, knobs, capfd):
+    x, w, sw, b = make(M, K, N, seed=M * 31 + K + N, bias=bias)
+    args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV) if bias else None)
+    knobs.set("ZT_S8_FUSED", "0")
+    y0 = C.dynamic_qlinear(*args).cpu()
+    knobs.set("ZT_S8_FUSED", "1")
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    y1 = C.dynamic_qlinear(*args).cpu()
+    assert "s8 fused quantise" in capfd.readouterr().err
+    assert torch.equal(y1, y0)
+    y_ref = O.dynamic_qlinear(x, w, sw, b if bias else None)
+    torch.testing.assert_close(y1.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
+# every tile shape of both one-token-tile paths (ZT_S8_SKINNY "TPW,PF,NW":
+# 64-, 32- and 16-row weight tiles, 4 or 8 chunks in flight), with the
+# quantisation in the GEMM's prologue and as its own launch: all
+# bit-identical to one another and within tolerance of the oracle
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (7, 1024, 300), (16, 2048, 11008),
+                                   (2, 14336, 520), (8, 192, 36)])
+def test_dynamic_qlinear_skinny_tile_shapes(M, K, N, knobs):
+    x, w, sw, b = make(M, K, N, seed=M * 13 + K + N)
+    args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV))
+    ys = []
+    for fused in ("0", "1"):
+        for shape in ("4,4,8", "2,4,8", "1,4,8", "1,8,8"):
+            knobs.set("ZT_S8_FUSED", fused)
+            knobs.set("ZT_S8_SKINNY", shape)
+            ys.append(C.dynamic_qlinear(*args).cpu())
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    torch.testing.assert_close(ys[0].float(), O.dynamic_qlinear(x, w, sw, b).float(),
+                               rtol=1e-2, atol=1e-2)
+
+
+# post-ops in the fused kernel's epilogue (row scales read from LDS), with
+# N a multiple of 4 and not
+@pytest.mark.parametrize("N", [136, 130])
+@pytest.mark.parametrize("post", [("relu",), ("add",), ("mul", "add"), ("silu",)])
+def test_dynamic_qlinear_fused_quantise_post_ops(post, N, knobs):
+    M, K = 6, 1024
+    x, w, sw, b = make(M, K, N, seed=N + len(post))
+    g = torch.Generator().manual_seed(17)
+    bufs = [torch.randn(M, N, generator=g).bfloat16() for p in post if p in ("add", "mul")]
+    args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV))
+    kw = dict(post_ops=post, post_bufs=[t.to(DEV) for t in bufs])
+    knobs.set("ZT_S8_FUSED", "0")
+    y0 = C.dynamic_qlinear(*args, **kw).cpu()
+    knobs.set("ZT_S8_FUSED", "1")
+    y1 = C.dynamic_qlinear(*args, **kw).cpu()
+    assert torch.equal(y1, y0)
+    y_ref = O.dynamic_qlinear(x, w, sw, b, post_ops=post, post_bufs=bufs)
+    torch.testing.assert_close(y1.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
+
+
 # number of 128-k chunks per half, every load depth.  Calls alternate two
 # inputs, so a partial left from the previous call cannot pass for the
 # current one; each call reuses the freed workspace, whose tile counters the

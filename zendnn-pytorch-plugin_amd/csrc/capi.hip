@@ -113,7 +113,7 @@ constexpr const char *kKnobNames[kKnobCount] = {
     "ZT_WOQ_GEMM",         "ZT_WOQ_DEBUG",       "ZT_WOQ_WAVE",    "ZT_WOQ_PERSIST",
     "ZT_S8_SKINNY32",      "ZT_S8_SKINNY",
     "ZT_S8_FRAG",          "ZT_S8_FORCE",        "ZT_S8_TILE",     "ZT_S8_KIND",
-    "ZT_S8_SPLIT",         "ZT_MOE_BN",          "ZT_WOQ_LEAN"};
+    "ZT_S8_SPLIT",         "ZT_MOE_BN",          "ZT_WOQ_LEAN",    "ZT_S8_FUSED"};
 
 // Values are interned copies that are never freed: a reader may hold an old
 // pointer while another thread replaces the value.
@@ -513,8 +513,10 @@ static int dynamic_qlinear_common(const char *op, const void *x, int32_t x_dtype
   int32_t *azp = asym ? reinterpret_cast<int32_t *>(ws + dyn_qx_bytes(M, K) + M * 4) : nullptr;
   a.qx = qx, a.sx = sx, a.azp = azp, a.colsum = colsum;
   a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
-  const int nc = a.qx_frag ? attach_split(a, ws, workspace_bytes, need) : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // few tokens: one launch that quantises x in the GEMM's prologue
+  if (zt::s8_fused_ok(a)) return hip_status(zt::launch_s8_skinny_fused(a, s), op);
+  const int nc = a.qx_frag ? attach_split(a, ws, workspace_bytes, need) : 0;
   rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s, azp,
                                           a.split_cnt, nc),
                   op);

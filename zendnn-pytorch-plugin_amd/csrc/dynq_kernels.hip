@@ -246,14 +246,16 @@ __device__ __forceinline__ float wscale(const DynArgs &a, int64_t n) {
   return load_elem(a.sw, a.sw_dt, a.sw_bcast ? 0 : n);
 }
 
+// sxp, when set, replaces a.sx (the fused kernel keeps the row scales in LDS).
 __device__ __forceinline__ void dyn_epilogue(const DynArgs &a, int64_t m,
-                                             int64_t n, int32_t acc) {
+                                             int64_t n, int32_t acc,
+                                             const float *sxp = nullptr) {
   if (a.azp) acc -= a.azp[m] * a.colsum[n];
   if (a.y_dt == ZT_DT_S32) {
     reinterpret_cast<int32_t *>(a.y)[m * a.N + n] = acc;
     return;
   }
-  float v = (float)acc * a.sx[m];
+  float v = (float)acc * (sxp ? sxp[m] : a.sx[m]);
   v = v * wscale(a, n);
   if (a.bias) v = v + load_elem(a.bias, a.b_dt, n);
   v = apply_post_ops(v, a.post, m, n);
@@ -382,7 +384,8 @@ __device__ __forceinline__ i32x4_t asym_fix4(const DynArgs &a, int m, int n, i32
   return v - c * z;
 }
 
-__device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i32x4_t v) {
+__device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i32x4_t v,
+                                              const float *sxp = nullptr) {
   const int N = (int)a.N;
   const bool vec_out = a.y_dt == ZT_DT_S32 || a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32;
   if (n + 3 < N && (N & 3) == 0 && vec_out) {
@@ -392,7 +395,7 @@ __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i3
       return;
     }
     float f[4];
-    const float sxm = a.sx[m];
+    const float sxm = sxp ? sxp[m] : a.sx[m];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float t = (float)v[r] * sxm;
@@ -415,7 +418,7 @@ __device__ __forceinline__ void dyn_epilogue4(const DynArgs &a, int m, int n, i3
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    if (n + r < N) dyn_epilogue(a, m, n + r, v[r]);
+    if (n + r < N) dyn_epilogue(a, m, n + r, v[r], sxp);
 }
 
 // Epilogue of a BM x BN int32 tile staged in LDS (row pitch acc_pitch),
@@ -1139,7 +1142,12 @@ struct QuadEpi {
   float sw[4], b[4], sx[KR];
   int32_t cs[4], az[KR];
 
-  __device__ __forceinline__ void prefetch(const DynArgs &a, int n0, int tid) {
+  // sxp, when set, replaces a.sx
+  const float *sxp;
+
+  __device__ __forceinline__ void prefetch(const DynArgs &a, int n0, int tid,
+                                           const float *sx_override = nullptr) {
+    sxp = sx_override;
     const int M = (int)a.M, N = (int)a.N;
     fast = (a.y_dt == ZT_DT_BF16 || a.y_dt == ZT_DT_F32) && a.post.count == 0 && (N & 3) == 0;
     c4 = (tid % Q) * 4;
@@ -1154,7 +1162,7 @@ struct QuadEpi {
 #pragma unroll
     for (int k = 0; k < KR; ++k) {
       const int m = r0 + k * RP;
-      sx[k] = m < M && m < ROWS ? a.sx[m] : 0.f;
+      sx[k] = m < M && m < ROWS ? (sxp ? sxp[m] : a.sx[m]) : 0.f;
       az[k] = a.azp && m < M && m < ROWS ? a.azp[m] : 0;
     }
   }
@@ -1166,7 +1174,7 @@ struct QuadEpi {
     if (!fast) {
       for (int idx = tid; idx < ROWS * Q; idx += NT) {
         const int m = idx / Q, c = (idx % Q) * 4;
-        if (m < M && n0 + c < N) dyn_epilogue4(a, m, n0 + c, v(m, c));
+        if (m < M && n0 + c < N) dyn_epilogue4(a, m, n0 + c, v(m, c), sxp);
       }
       return;
     }
@@ -1307,6 +1315,175 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunk
   }
   __syncthreads();
   skinny_epilogue<16 * MT, TPW, NW>(a, slab, n0, tid, ep);
+}
+
+// The 16-token skinny GEMM with the per-token quantisation in its
+// prologue (symmetric s8; bf16 x [M, K] in 16-byte rows, M <= RM, and each
+// row at most VR vectors of 8 elements per thread).  Every workgroup
+// quantises all of x itself into an LDS copy of qx [M][K + 16] and of sx,
+// with the quantise kernel's arithmetic (the row's amax over the whole
+// workgroup, sx = max(amax, 1e-12) / 127, q = clamp(rint(x / sx), -128,
+// 127)), so qx and sx are bit-identical to that pass.  Its first PF chunks
+// of weights are requested before x, so the quantisation runs while they
+// are in flight; the chunk loop then reads its B operands from LDS (token
+// columns past M read row M - 1; their sums are never stored).  The call
+// loses the quantise launch and the trip of qx through memory; in exchange
+// every workgroup reads x (2 M K bytes, from its XCD's L2) and repeats the
+// quantisation, so it serves few tokens only.
+template <int TPW, int PF, int NW, int RM, int VR>
+__global__ __launch_bounds__(64 * NW) void s8_skinny_fused_kernel(DynArgs a, int chunks_per_wave) {
+  extern __shared__ __attribute__((aligned(16))) int8_t s8_smem[];
+  constexpr int NT = 64 * NW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
+  const int n0 = blockIdx.x * (16 * TPW);
+  const int QP = K + 16;  // qx row pitch (K % 64 == 0: rows stay 16-byte aligned)
+  // LDS: the K-partial slabs, qx [M][QP], sx [16], the amax partials [NW][RM]
+  int32_t *slab = reinterpret_cast<int32_t *>(s8_smem);
+  int8_t *ql = s8_smem + s8_skinny_lds<1, TPW>();
+  float *sxl = reinterpret_cast<float *>(ql + (size_t)M * QP);
+  float *red = sxl + 16;
+  const auto w_rs = make_rsrc(a.w, (uint32_t)((int64_t)N * K));
+  const auto x_rs = make_rsrc(a.x, (uint32_t)((int64_t)M * K * 2));
+
+  uint32_t w_row[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int n = n0 + t * 16 + lr;
+    w_row[t] = n < N ? (uint32_t)(n * K) : kOobOffset;
+  }
+  const int c_begin = wv * chunks_per_wave;
+  const int total = K / 64;
+  const int nch = max(0, min(chunks_per_wave, total - c_begin));
+  // weight chunks past the wave's slice read zeros (as in s8_skinny_kernel);
+  // the qx reads of those chunks are clamped into the row and never used
+  i32x4_t wf[PF][TPW], qf[PF];
+  auto load_w = [&](int slot, int c) {
+    const uint32_t kc = c < nch ? (uint32_t)((c_begin + c) * 64) : kOobOffset;
+    const uint32_t k = kc + 16u * lg;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+      wf[slot][t] = __builtin_bit_cast(
+          i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, w_row[t] + k, 0, 0));
+  };
+  const int qrow = min(lr, M - 1) * QP + 16 * lg;
+  auto load_q = [&](int slot, int c) {
+    const int kc = min(c_begin + c, total - 1) * 64;
+    qf[slot] = *reinterpret_cast<const i32x4_t *>(ql + qrow + kc);
+  };
+
+  // 1. the first PF chunks of weights, then x: thread tid holds the vectors
+  //    j = tid + NT * i (i < VR) of each row m < RM (rows past M and vectors
+  //    past the row read zeros)
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load_w(p, p);
+  const int nv = K >> 3;
+  u32x4_t xv[RM][VR];
+#pragma unroll
+  for (int m = 0; m < RM; ++m)
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      const int j = tid + NT * i;
+      const uint32_t off = m < M && j < nv ? (uint32_t)(m * K + j * 8) * 2u : kOobOffset;
+      xv[m][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off, 0, 0));
+    }
+  // 2. each row's amax: per thread, per wave, then over the NW waves
+  float hi[RM];
+#pragma unroll
+  for (int m = 0; m < RM; ++m) {
+    hi[m] = 0.f;
+#pragma unroll
+    for (int i = 0; i < VR; ++i)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float e0 = __uint_as_float(xv[m][i][w] << 16);
+        const float e1 = __uint_as_float(xv[m][i][w] & 0xffff0000u);
+        hi[m] = fmaxf(hi[m], fmaxf(fabsf(e0), fabsf(e1)));
+      }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) hi[m] = fmaxf(hi[m], __shfl_xor(hi[m], off, kWave));
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int m = 0; m < RM; ++m) red[wv * RM + m] = hi[m];
+  __syncthreads();
+  // 3. lane m < RM of every wave forms row m's scale and its reciprocal;
+  //    the wave shares them by shuffles
+  float s_l, inv_l;
+  {
+    const int m = lane < RM ? lane : 0;
+    float amax = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) amax = fmaxf(amax, red[w * RM + m]);
+    float zp;
+    row_qparams<false>(-amax, amax, s_l, zp);
+    inv_l = __fdiv_rn(1.0f, s_l);
+  }
+  if (wv == 0 && lane < RM && lane < M) sxl[lane] = s_l;
+  // 4. qx into LDS, eight bytes per vector
+#pragma unroll
+  for (int m = 0; m < RM; ++m) {
+    const float sm = __shfl(s_l, m, kWave), im = __shfl(inv_l, m, kWave);
+    if (m >= M) break;
+    auto q1 = [&](float f) { return (uint32_t)(uint8_t)(int8_t)quant_one<false>(f, sm, im, 0.f); };
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      const int j = tid + NT * i;
+      if (j >= nv) break;
+      u32x2_t o;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t a0 = xv[m][i][2 * h], a1 = xv[m][i][2 * h + 1];
+        o[h] = q1(__uint_as_float(a0 << 16)) | (q1(__uint_as_float(a0 & 0xffff0000u)) << 8) |
+               (q1(__uint_as_float(a1 << 16)) << 16) | (q1(__uint_as_float(a1 & 0xffff0000u)) << 24);
+      }
+      *reinterpret_cast<u32x2_t *>(ql + m * QP + j * 8) = o;
+    }
+  }
+  __syncthreads();
+
+  // 5. the chunks, as in s8_skinny_kernel; the epilogue reads sx from LDS
+  QuadEpi<16, 16 * TPW, NT> ep;
+  ep.prefetch(a, n0, tid, sxl);
+  i32x4_t acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load_q(p, p);
+  for (int c = 0; c < nch; c += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[p][t], qf[p], acc[t], 0, 0, 0);
+      load_w(p, c + p + PF);
+      load_q(p, c + p + PF);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // 6. K partials: slab[w][m][n_local], n_local = t*16 + 4*lg + r
+  constexpr int P = 16 * TPW + kSkPitchPad;
+  auto slab_at = [&](int w, int t) {
+    return reinterpret_cast<i32x4_t *>(slab + (w * 16 + lr) * P + t * 16 + 4 * lg);
+  };
+  if (NW == 8 && wv >= 4) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) *slab_at(wv - 4, t) = acc[t];
+  }
+  if (NW == 8) __syncthreads();
+  if (wv < 4) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      i32x4_t v = acc[t];
+      if (NW == 8) v += *slab_at(wv, t);
+      *slab_at(wv, t) = v;
+    }
+  }
+  __syncthreads();
+  skinny_epilogue<16, TPW, NW>(a, slab, n0, tid, ep);
 }
 
 // The skinny GEMM on v_mfma_i32_32x32x32_i8 (twice the int8 rate of the
@@ -1713,15 +1890,40 @@ hipError_t launch_s8_skinny(const DynArgs &a, hipStream_t s) {
   const int mt = (int)((a.M + 15) / 16);
   const char *e = knob(kKnobS8Skinny);  // "TPW,PF,NW"
   int tpw = 0, pf = 0, nw = 0;
-  if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+  if (e) {
+    std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+  } else if (mt == 1) {
+    // one token tile: 16-row weight tiles, as many workgroups as CUs or
+    // more, except 32-row tiles from 4097 to 8192 rows and 64-row tiles
+    // past 16384 (graph replays over rotating weights, M = 1..16, one box:
+    // at M = 1 O 4096 x 4096 18.1 -> 11.0 us, down 4096 x 14336 44.9 ->
+    // 20.3, QKV 6144 x 4096 18.7 -> 13.8, 11008 x 4096 20.4 -> 17.8, all
+    // against 64-row tiles; gate_up 28672 x 4096 keeps them, 37.4 against
+    // 40.2 with 16-row tiles at M = 8)
+    tpw = a.N > 16384 ? 4 : (a.N > 4096 && a.N <= 8192) ? 2 : 1;
+    pf = 4, nw = 8;
+  }
 #define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
   if (mt <= MT_ && (!tpw || (tpw == TPW_ && pf == PF_ && nw == NW_)))          \
     return launch_s8_skinny_t<MT_, TPW_, PF_, NW_>(a, s);
-  ZT_SK(1, 4, 4, 8) ZT_SK(2, 4, 4, 8) ZT_SK(4, 2, 4, 8)
+  ZT_SK(1, 4, 4, 8) ZT_SK(1, 1, 4, 8) ZT_SK(1, 1, 8, 8) ZT_SK(1, 2, 4, 8)
+  ZT_SK(2, 4, 4, 8) ZT_SK(4, 2, 4, 8)
   ZT_SK(8, 3, 2, 8) ZT_SK(8, 2, 3, 8) ZT_SK(8, 2, 4, 4) ZT_SK(8, 1, 4, 8) ZT_SK(8, 4, 2, 8)
   ZT_SK(8, 3, 4, 4)
 #undef ZT_SK
   return hipErrorInvalidValue;
+}
+
+template <int TPW, int PF, int RM, int VR>
+hipError_t launch_s8_skinny_fused_t(const DynArgs &a, hipStream_t s) {
+  constexpr int NW = 8;
+  const int total = (int)(a.K / 64);
+  int cpw = (total + NW - 1) / NW;
+  cpw = (cpw + PF - 1) / PF * PF;
+  const int blocks = (int)((a.N + 16 * TPW - 1) / (16 * TPW));
+  s8_skinny_fused_kernel<TPW, PF, NW, RM, VR><<<dim3((unsigned)blocks), dim3(64 * NW),
+                                                 s8_fused_lds(a.M, a.K, TPW), s>>>(a, cpw);
+  return hipGetLastError();
 }
 
 template <int BM, int BN>
@@ -1734,6 +1936,64 @@ hipError_t launch_s8_tiled(const DynArgs &a, hipStream_t s) {
 }
 
 }  // namespace
+
+// Tokens up to which the fused kernel takes a call by default.
+constexpr int64_t kS8FusedRows = 8;
+
+// Vectors of 8 elements per thread and row of the fused kernel (512
+// threads), and the fused kernel's LDS.
+static int s8_fused_vr(int64_t K) { return (int)((K / 8 + 511) / 512); }
+size_t s8_fused_lds(int64_t M, int64_t K, int tpw) {
+  // the K-partial slabs (s8_skinny_lds<1, tpw>), qx, sx, the amax partials
+  return (size_t)4 * 16 * (16 * tpw + kSkPitchPad) * 4 + (size_t)M * (size_t)(K + 16) + 16 * 4 +
+         8 * 16 * 4;
+}
+
+bool s8_fused_ok(const DynArgs &a) {
+  // "0": never; "1": wherever it applies; unset: up to kS8FusedRows tokens
+  const char *e = knob(kKnobS8Fused);
+  if (e && e[0] == '0') return false;
+  if (a.x_dt != ZT_DT_BF16 || a.azp || a.qx_frag || a.out_scale || a.y_dt == ZT_DT_S32 ||
+      a.M < 1 || a.M > 16 || a.K % 64 != 0 || a.N < 1)
+    return false;
+  if (((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) & 15u) != 0)
+    return false;
+  if (a.N * a.K >= (int64_t)kOobOffset || a.M * a.K * 2 >= (int64_t)kOobOffset) return false;
+  const int vr = s8_fused_vr(a.K);
+  const int64_t rm = vr == 1 ? 16 : vr == 2 ? 4 : vr <= 4 ? 2 : 0;
+  if (a.M > rm || s8_fused_lds(a.M, a.K, 4) > 160 * 1024) return false;
+  return (e && e[0] == '1') || a.M <= kS8FusedRows;
+}
+
+template <int TPW, int PF>
+hipError_t launch_s8_skinny_fused_tp(const DynArgs &a, hipStream_t s) {
+  const int vr = s8_fused_vr(a.K);
+  if (vr == 1) return a.M <= 8 ? launch_s8_skinny_fused_t<TPW, PF, 8, 1>(a, s)
+                               : launch_s8_skinny_fused_t<TPW, PF, 16, 1>(a, s);
+  if (vr == 2) return launch_s8_skinny_fused_t<TPW, PF, 4, 2>(a, s);
+  return launch_s8_skinny_fused_t<TPW, PF, 2, 4>(a, s);
+}
+
+hipError_t launch_s8_skinny_fused(const DynArgs &a, hipStream_t s) {
+  if (!s8_fused_ok(a)) return hipErrorInvalidValue;
+  // ZT_S8_SKINNY "TPW,PF,8" picks the tile shape as for the 16-token
+  // kernel.  By default 16-row tiles with 8 chunks in flight up to 4096
+  // rows (one workgroup per CU), else 32-row tiles (graph replays over
+  // rotating weights, M = 1..8, one box: at M = 1 O 4096 x 4096 8.6 us
+  // against 9.3 / 10.5 / 15.4 with 16-row tiles and 4 chunks / 32 / 64-row
+  // tiles; QKV 6144 x 4096 11.2 against 11.6 / 16.1 with 16 / 64-row tiles;
+  // gate_up 28672 x 4096 33.0 against 36.1 with 64-row tiles)
+  const char *e = knob(kKnobS8Skinny);
+  int tpw = a.N <= 4096 ? 1 : 2, pf = a.N <= 4096 ? 8 : 4, nw = 8;
+  if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+  if (knob(kKnobWoqDebug))
+    std::fprintf(stderr, "[zt] s8 fused quantise + skinny GEMM M=%lld N=%lld K=%lld TPW=%d PF=%d\n",
+                 (long long)a.M, (long long)a.N, (long long)a.K, tpw, pf);
+  if (tpw == 1 && pf == 8) return launch_s8_skinny_fused_tp<1, 8>(a, s);
+  if (tpw == 1) return launch_s8_skinny_fused_tp<1, 4>(a, s);
+  if (tpw == 2) return launch_s8_skinny_fused_tp<2, 4>(a, s);
+  return launch_s8_skinny_fused_tp<4, 4>(a, s);
+}
 
 hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                                int8_t *qx, float *sx, bool frag, hipStream_t s,

@@ -137,6 +137,13 @@ bool s8_frag_ok(const DynArgs &a);
 size_t s8_split_bytes(int64_t M, int64_t K, int64_t N);
 int s8_split_counters(int64_t N);
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);
+// The 16-token skinny GEMM with the per-token quantisation in its prologue
+// (symmetric s8, bf16 x): whether it takes this call (a.qx and a.sx unused),
+// its LDS bytes, and its launch, which replaces launch_dyn_quantize +
+// launch_s8_gemm.
+bool s8_fused_ok(const DynArgs &a);
+size_t s8_fused_lds(int64_t M, int64_t K, int tpw);
+hipError_t launch_s8_skinny_fused(const DynArgs &a, hipStream_t s);
 
 // Grouped int4 MoE (moe_kernels.hip).  Device scratch of one call.
 struct MoeWork {

@@ -27,6 +27,7 @@ enum Knob {
   kKnobS8Split,         // ZT_S8_SPLIT: "0" disables the split-K skinny kernel, "2"-"4" its load depth
   kKnobMoeBn,           // ZT_MOE_BN: column tile of the MoE GEMMs
   kKnobWoqLean,         // ZT_WOQ_LEAN: "0" never, "1" forces the lean decode kernel wherever it applies, "p" too with gate_up tile pairs
+  kKnobS8Fused,         // ZT_S8_FUSED: "0" never, "1" the quantise-in-prologue skinny kernel wherever it applies
   kKnobCount
 };
 
