@@ -11,8 +11,10 @@ resident in HBM before timing starts.
 
 Secondary workloads in the same line (``workloads``): the Llama-3-8B decode
 layer at M in {1, 8, 16, 64} (config 2), dynamic int8 qlinear at M=128
-(config 1), the M=2048 prefill layer through both paths (config 3) and the
-Mixtral-shaped int4 MoE FFN over 256 tokens (config 4).
+(config 1), the dynamic int8 qlinear over the same layer's four linears at
+M in {1, 8} (the dynamic path at decode sizes), the M=2048 prefill layer
+through both paths (config 3) and the Mixtral-shaped int4 MoE FFN over 256
+tokens (config 4).
 
 ``roofline`` is for the dominant kernel of the headline workload (the
 decode GEMV, one launch per call): ``achieved`` = algorithmic bytes per
@@ -338,6 +340,8 @@ def read_traffic():
 
 LLAMA = [("qkv", 6144, 4096, None), ("o", 4096, 4096, None),
          ("gate_up", 28672, 4096, "gate_up"), ("down", 4096, 14336, "add")]
+# (N, K) of the same four linears, for the dynamic int8 workloads
+LLAMA_SHAPES = [(N, K) for _, N, K, _ in LLAMA]
 
 
 # Secondary workloads: each is timed over SECONDARY_REPS replays of one graph
@@ -663,7 +667,8 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default=None,
-                    help="config0 | decode | dyn128 | prefill_int8 | prefill_int4 | moe | traffic"
+                    help="config0 | decode | dyn128 | dyn_decode | prefill_int8 | prefill_int4 | moe"
+                         " | traffic"
                          " | pmc | decode_pmc | floors (not part of the default run)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline-child", type=int, default=0, help=argparse.SUPPRESS)
@@ -699,6 +704,8 @@ def main():
         if only in (None, "dyn128"):
             res["dyn_qlinear_m128"] = bench_dyn(128, [(11008, 4096)], args, gen)
             res["dyn_qlinear_asym_m128"] = bench_dyn(128, [(11008, 4096)], args, gen, asym=True)
+        if only in (None, "dyn_decode"):
+            res["dyn_decode_layer"] = [bench_dyn(M, LLAMA_SHAPES, args, gen) for M in (1, 8)]
         if only in (None, "prefill_int8"):
             res["prefill_int8_m2048"] = bench_dyn(
                 2048, [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)], args, gen)
@@ -764,6 +771,15 @@ def secondary_rooflines(res):
                     "kernels": "dyn_quantize_asym (u8) + s8_splitk_kernel with the zero-point "
                                "column-sum correction",
                     "op_avg_us": round(d["s_per_call"] * 1e6, 3)})
+    for d in res.get("dyn_decode_layer", []):
+        out.append({"workload": f"dynamic int8 qlinear over the Llama-3-8B layer at decode size, "
+                                f"M={d['M']} (the dynamic path of config 1 at config 2's shapes)",
+                    "bound": "hbm", "achieved": round(d["GBps"], 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(d["frac_hbm"], 4),
+                    "kernels": "s8_skinny_fused_kernel (quantisation in the GEMM prologue, "
+                               "one launch per op)",
+                    "layer_avg_us": round(d["s_per_layer"] * 1e6, 3),
+                    "weight_copies": d["weight_copies"]})
     d = res.get("prefill_int8_m2048")
     if d:
         out.append({"workload": "config 3 int8: dynamic qlinear over the Llama-3-8B layer, M=2048",

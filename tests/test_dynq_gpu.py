@@ -170,7 +170,7 @@ def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, knobs):
 @pytest.mark.parametrize("M,K,N", [(1, 64, 8), (2, 4096, 11008), (3, 192, 70), (5, 4096, 6144),
                                    (8, 4096, 4096), (9, 4096, 200), (16, 4096, 136),
                                    (4, 8192, 300), (3, 5120, 77), (2, 14336, 4096),
-                                   (1, 16384, 64)])
+                                   (1, 16384, 64), (4, 4096, 28672)])
 @pytest.mark.parametrize("bias", [True, False])
 def test_dynamic_qlinear_fused_quantise(M, K, N, bias, knobs, capfd):
     x, w, sw, b = make(M, K, N, seed=M * 31 + K + N, bias=bias)

@@ -1324,8 +1324,10 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_kernel(DynArgs a, int chunk
 // with the quantise kernel's arithmetic (the row's amax over the whole
 // workgroup, sx = max(amax, 1e-12) / 127, q = clamp(rint(x / sx), -128,
 // 127)), so qx and sx are bit-identical to that pass.  Its first PF chunks
-// of weights are requested before x, so the quantisation runs while they
-// are in flight; the chunk loop then reads its B operands from LDS (token
+// of weights are requested in the prologue, so the quantisation runs while
+// they are in flight (the compiler issues them once x has landed; pinning
+// them before x, right after it or before the amax shuffles measured 1-4 %
+// slower); the chunk loop then reads its B operands from LDS (token
 // columns past M read row M - 1; their sums are never stored).  The call
 // loses the quantise launch and the trip of qx through memory; in exchange
 // every workgroup reads x (2 M K bytes, from its XCD's L2) and repeats the
@@ -1374,7 +1376,7 @@ __global__ __launch_bounds__(64 * NW) void s8_skinny_fused_kernel(DynArgs a, int
     qf[slot] = *reinterpret_cast<const i32x4_t *>(ql + qrow + kc);
   };
 
-  // 1. the first PF chunks of weights, then x: thread tid holds the vectors
+  // 1. the first PF chunks of weights and x: thread tid holds the vectors
   //    j = tid + NT * i (i < VR) of each row m < RM (rows past M and vectors
   //    past the row read zeros)
 #pragma unroll
