@@ -146,7 +146,8 @@ def test_dynamic_qlinear_fragment_kernel(M, K, N, x_dtype):
 # forced onto it too
 @pytest.mark.parametrize("M,shape", [(20, "4,4,8"), (40, "4,2,8"), (64, "3,2,8"), (90, "2,2,8"),
                                      (128, "4,2,8"), (128, "3,4,4"), (97, "4,4,4"),
-                                     (1, None), (9, None), (16, None)])
+                                     (20, "2,4,8"), (31, "1,4,8"), (40, "2,2,8"), (64, "2,4,8"),
+                                     (50, "1,4,8"), (1, None), (9, None), (16, None)])
 def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, knobs):
     K, N = 1344, 232
     if shape:
@@ -158,10 +159,20 @@ def test_dynamic_qlinear_fragment_kernel_shapes(M, shape, knobs):
     torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
 
 
-# 64 < M <= 128 with K % 256 == 0 runs the split-K kernel when the workspace
-# holds its exchange (two K halves per 96-column tile, the second to finish
-# adds the other's int32 partial): bit-identical to the unsplit kernel (the
-# least workspace), on ragged M, N past a tile, N % 4 != 0, one or an odd
+# 17..64 tokens on the 32-token kernel: the default tile shape (16- or
+# 32-row tiles up to 8192 rows) bit-identical to 64-row tiles
+@pytest.mark.parametrize("M,N,K", [(17, 4096, 4096), (64, 4096, 14336), (33, 6144, 4096),
+                                   (24, 11008, 1024)])
+def test_dynamic_qlinear_fragment_kernel_default_tiles(M, N, K, knobs):
+    x, w, sw, b = make(M, K, N, seed=M + N)
+    args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV))
+    y = C.dynamic_qlinear(*args).cpu()
+    knobs.set("ZT_S8_SKINNY32", "4,4,8" if M <= 32 else "4,2,8")
+    assert torch.equal(C.dynamic_qlinear(*args).cpu(), y)
+    torch.testing.assert_close(y.float(), O.dynamic_qlinear(x, w, sw, b).float(),
+                               rtol=1e-2, atol=1e-2)
+
+
 # The skinny GEMM with the per-token quantisation in its prologue (one
 # launch for at most 16 tokens of bf16 x): bit-identical to the quantise
 # launch + skinny GEMM (the same qx, sx and int32 sums) for every register
@@ -228,6 +239,10 @@ def test_dynamic_qlinear_fused_quantise_post_ops(post, N, knobs):
     torch.testing.assert_close(y1.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
 
 
+# 64 < M <= 128 with K % 256 == 0 runs the split-K kernel when the workspace
+# holds its exchange (two K halves per 96-column tile, the second to finish
+# adds the other's int32 partial): bit-identical to the unsplit kernel (the
+# least workspace), on ragged M, N past a tile, N % 4 != 0, one or an odd
 # number of 128-k chunks per half, every load depth.  Calls alternate two
 # inputs, so a partial left from the previous call cannot pass for the
 # current one; each call reuses the freed workspace, whose tile counters the

@@ -1625,12 +1625,23 @@ hipError_t launch_s8_skinny32(const DynArgs &a, hipStream_t s) {
   const int mt = (int)((a.M + 31) / 32);
   const char *e = knob(kKnobS8Skinny32);  // "TPW,PF,NW"
   int tpw = 0, pf = 0, nw = 0;
-  if (e) std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+  if (e) {
+    std::sscanf(e, "%d,%d,%d", &tpw, &pf, &nw);
+  } else if (mt <= 2 && a.N <= 8192) {
+    // up to 64 tokens: 16-row weight tiles up to 4096 rows, 32-row tiles up
+    // to 8192, so that those matrices give at least 128 workgroups (graph
+    // replays over rotating weights, one box, against 64-row tiles: at M =
+    // 17 / 64 O 4096 x 4096 20.3 -> 12.5 / 22.1 -> 15.3 us, down 4096 x
+    // 14336 51.9 -> 27.0 / 58.8 -> 34.4, QKV 6144 x 4096 20.7 -> 16.1 /
+    // 22.8 -> 18.7; 11008 and 28672 rows keep 64-row tiles, 4-30 % faster)
+    tpw = a.N <= 4096 ? 1 : 2, pf = 4, nw = 8;
+  }
 #define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
   if (mt <= MT_ && (!tpw || (tpw == TPW_ && pf == PF_ && nw == NW_)))          \
     return launch_s8_skinny32_t<MT_, TPW_, PF_, NW_>(a, s);
   ZT_SK(1, 4, 4, 8) ZT_SK(2, 4, 2, 8) ZT_SK(4, 3, 2, 8) ZT_SK(4, 2, 2, 8) ZT_SK(4, 4, 2, 8)
-  ZT_SK(4, 3, 4, 4) ZT_SK(4, 4, 4, 4)
+  ZT_SK(4, 3, 4, 4) ZT_SK(4, 4, 4, 4) ZT_SK(1, 2, 4, 8) ZT_SK(1, 1, 4, 8) ZT_SK(2, 2, 2, 8)
+  ZT_SK(2, 2, 4, 8) ZT_SK(2, 1, 4, 8)
 #undef ZT_SK
   return hipErrorInvalidValue;
 }
