@@ -304,6 +304,21 @@ def test_stream_kernel_phases_down_shape(M, post, nbuf):
     run_case(M, 14336, 256, 112, post=post, nbuf=nbuf, seed=M + 3 * nbuf, bias=True)
 
 
+# K phases whose rows are not whole 1 KB pieces (K / P % 512 != 0): the
+# last DMA piece of each row is partial and lands in the row's padding.
+# 4096 x 11008 at M = 8 (Llama-2's down projection) runs in 2 phases of
+# 5504; before, it fell to the wide kernel on 32 workgroups.  ZT_WOQ_DEBUG
+# names the stream kernel and its phase count.
+@pytest.mark.parametrize("M,K,N,post,nbuf", [(8, 11008, 136, (), 0), (7, 10496, 64, ("add",), 1),
+                                             (8, 18944, 72, (), 0), (6, 18944, 40, ("add",), 1)])
+def test_stream_kernel_phases_partial_pieces(M, K, N, post, nbuf, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    run_case(M, K, N, K // 128, post=post, nbuf=nbuf, seed=M + K, bias=True)
+    err = capfd.readouterr().err
+    assert "woq stream" in err and " P=1 " not in err, err
+
+
 # 17..64 rows on the stream kernel: 2 or 4 token tiles per weight fragment,
 # x staged in 1, 2, 4 or 8 K-phases (M = 17: whole; 20..32: 2; 33..48: 4;
 # 49..64: 8 at K = 4096)

@@ -408,6 +408,9 @@ __host__ __device__ constexpr size_t stream_scale_offset(size_t slab, size_t x) 
   return slab > x ? slab : x;
 }
 __host__ __device__ inline int stream_x_pitch(int K) { return K + 8; }  // bf16
+// row pitch of one K phase of x (kp elements): whole 1 KB DMA pieces, so
+// the lanes of a partial last piece land in the row's own padding
+__host__ __device__ inline int stream_phase_pitch(int kp) { return (kp + 511) / 512 * 512 + 8; }
 // fast mode: the bf16 scales of the workgroup's TPW*16 rows for all G groups,
 // [G][TPW*16], moved by 256-byte DMA instructions
 __host__ __device__ constexpr size_t stream_scale_bytes(int G, int tpw) {
@@ -455,16 +458,21 @@ __global__ __launch_bounds__(64 * NW) void woq_stream_kernel(WoqArgs a, int cpg_
   //    when x_dma (stream_x_dma: every row 16-byte aligned and whole 1 KB
   //    pieces; always for P > 1): instruction i moves 64 16-byte chunks of
   //    one row.
-  const int XP = P == 1 ? stream_x_pitch(K) : stream_x_pitch(K / P);
+  const int XP = P == 1 ? stream_x_pitch(K) : stream_phase_pitch(K / P);
   uint16_t *xl = reinterpret_cast<uint16_t *>(smem);
   const auto x_rsrc = make_rsrc(a.x, (uint32_t)((int64_t)(M - 1) * a.ldx * 2 + (int64_t)K * 2));
   auto dma_x = [&](int p) {
-    const int per_row = (P == 1 ? K : K / P) / 512;  // 1 KB pieces per row
+    // 1 KB pieces per row and phase; with phases the last may be partial:
+    // its lanes past the row read nothing and write zeros into the row's
+    // padding (stream_phase_pitch)
+    const int kp = P == 1 ? K : K / P;
+    const int per_row = (kp + 511) / 512;
     for (int i = wv; i < M * per_row; i += NW) {
       const int m = i / per_row, q = i - m * per_row;
+      const int e = q * 512 + lane * 8;  // the lane's first element of the row's phase
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           x_rsrc, (lds_ptr_t)(xl + m * XP + q * 512), 16,
-          (uint32_t)(m * a.ldx * 2 + p * (K / P) * 2 + q * 1024 + lane * 16), 0, 0, 0);
+          e < kp ? (uint32_t)(m * a.ldx * 2 + p * kp * 2 + e * 2) : kOobOffset, 0, 0, 0);
     }
   };
   if (x_dma) dma_x(0);
@@ -1930,8 +1938,10 @@ static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int g
   return false;
 }
 
+// one phase (p == 1): rows of whole 1 KB pieces; several: rows of 16-byte
+// pieces (the phase pitch rounds each row up to whole 1 KB pieces)
 static bool stream_x_dma(const WoqArgs &a, int p) {
-  return (a.K / p) % 512 == 0 &&
+  return (p == 1 ? a.K % 512 == 0 : (a.K / p) % 8 == 0) &&
          ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) == 0 &&
          (a.M - 1) * a.ldx * 2 + a.K * 2 < (int64_t)kOobOffset;
 }
@@ -1943,7 +1953,8 @@ static hipError_t launch_stream_t(const WoqArgs &a, hipStream_t s, int shift, in
   if (P > 1 && !x_dma) return hipErrorInvalidValue;  // phases need the DMA (host-checked)
   const size_t lds =
       stream_scale_offset(stream_slab_bytes(NW, TPW, MT),
-                          (size_t)a.M * stream_x_pitch((int)(a.K / P)) * 2) +
+                          (size_t)a.M *
+                              (P == 1 ? stream_x_pitch((int)a.K) : stream_phase_pitch((int)(a.K / P))) * 2) +
       (mode == kDecFast ? stream_scale_bytes((int)a.G, TPW) : 0);
   dim3 grid((unsigned)((tiles + TPW - 1) / TPW)), block(64 * NW);
   if (mode == kDecFast)
@@ -2234,7 +2245,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   const int mt = (int)((a.M + 15) / 16) == 3 ? 4 : (int)((a.M + 15) / 16);
   auto fits = [&](int p) {
     return stream_scale_offset(stream_slab_bytes(nw, tpw, mt),
-                               (size_t)a.M * stream_x_pitch((int)(a.K / p)) * 2) +
+                               (size_t)a.M *
+                                   (p == 1 ? stream_x_pitch((int)a.K) : stream_phase_pitch((int)(a.K / p))) * 2) +
                (mode == kDecFast ? stream_scale_bytes((int)a.G, tpw) : 0) <=
            kStreamLdsMax;
   };
@@ -2257,7 +2269,7 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
   }
       // smallest CPW first, so that every wave has chunks in each phase
       ZT_STREAM_PCASE(8, 2, 1) ZT_STREAM_PCASE(14, 2, 1) ZT_STREAM_PCASE(16, 2, 1)
-      ZT_STREAM_PCASE(16, 4, 1)
+      ZT_STREAM_PCASE(16, 4, 1) ZT_STREAM_PCASE(20, 2, 1) ZT_STREAM_PCASE(20, 4, 1)
       ZT_STREAM_PCASE(4, 1, 2) ZT_STREAM_PCASE(4, 2, 2) ZT_STREAM_PCASE(16, 4, 2)
       ZT_STREAM_PCASE(4, 1, 4) ZT_STREAM_PCASE(4, 4, 4) ZT_STREAM_PCASE(8, 8, 4)
 #undef ZT_STREAM_PCASE
@@ -2671,8 +2683,10 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   }
   // up to 16 rows: only without a K split (measured: gate_up 28672 x 4096
   // at M = 12 / 16 takes 22.6 / 22.9 us here against 25.9 / 27.2 on the
-  // stream kernel, while the split shapes lose the reduce launch)
-  if (M < 17 && ks > 1 && !forced) return false;
+  // stream kernel, while the split shapes lose the reduce launch), and only
+  // with at least half a round of workgroups (a prime phase count leaves no
+  // split: 4096 x 11008 at M = 8 took 40.9 us on 32 workgroups)
+  if (M < 17 && (ks > 1 || blocks < 128) && !forced) return false;
   p->mt = M <= 32 ? 1 : 2;
   p->splits = ks;
   p->pps = phases / ks;
