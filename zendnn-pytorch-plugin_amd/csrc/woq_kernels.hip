@@ -1896,17 +1896,18 @@ static hipError_t launch_persist_t(const WoqArgs &a, hipStream_t s, int shift, i
 // 18.3 / 19.3 us at M = 3 / 6 / 8 / 9 / 12 / 16 against 18.9 / 18.7 / 18.2
 // / 17.8 / 18.3 / 19.3 on the wave kernel and 17.7 / 17.8 / 18.2 / 18.2 /
 // 18.8 / 20.0 here in gate/up tile pairs, 896 units for 256 workgroups
-// where half tiles make 1792, 7 each), and plain calls from 12288 rows,
-// three or more units per CU (14336 x 4096: 10.2 / 10.7 / 12.6 us at M = 1
-// / 8 / 16 against 10.9 / 11.9 / 13.5 for the stream kernel); QKV- and
-// O-sized calls (1.5 and 1 unit per CU) are slower on it.  ZT_WOQ_PERSIST: "0" never, "1" / "2"
+// where half tiles make 1792, 7 each), and plain calls from 8193 rows,
+// more than two units per CU (14336 x 4096: 10.2 / 10.7 / 12.6 us at M = 1
+// / 8 / 16 against 10.9 / 11.9 / 13.5 for the stream kernel; 11008 x 4096
+// at M = 4 / 8: 9.6 / 10.1 us against 11.0 / 10.7-11.0 on the wave
+// kernel); QKV- and O-sized calls (1.5 and 1 unit per CU) are slower on it.  ZT_WOQ_PERSIST: "0" never, "1" / "2"
 // force 8 / 16 waves wherever the shape allows ("1p" / "2p": the merged
 // gate_up in gate/up tile pairs instead of half tiles).
 static bool try_launch_persist(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
                                int gu, hipError_t *err) {
   const char *e = knob(kKnobWoqPersist);
   if (e && e[0] == '0') return false;
-  if (!e && !(gu ? a.M >= 3 : a.N >= 12288)) return false;
+  if (!e && !(gu ? a.M >= 3 : a.N > 8192)) return false;
   if (mode != kDecFast || a.x_dt != ZT_DT_BF16 || a.M < 1 || a.M > 16 || (gu && gu % 16))
     return false;
   if (((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.ldx * 2)) & 15u) ||
@@ -2172,7 +2173,10 @@ static hipError_t launch_lean_t(const WoqArgs &a, hipStream_t s, int shift, int 
 // Measured (default dispatch -> lean kernel, one box): 4096 x 14336 at
 // M = 1 / 2 / 4 10.5 -> 9.9, 10.6 -> 10.2, 11.6 -> 10.7 us; 14336 x 4096
 // at M = 1 / 2 11.0 -> 9.9, 11.0 -> 10.1 us and at M = 12 / 16 (against
-// the persistent kernel) 28672 x 4096 25.2 -> 23.6, 25.3 -> 23.8 us.
+// the persistent kernel) 28672 x 4096 25.2 -> 23.6, 25.3 -> 23.8 us; from
+// 8193 rows (11008 x 4096 at M = 1 / 2: 9.1 / 9.5 us against 10.1-10.8 /
+// 10.8-10.9 on the wave kernel, which the persistent kernel also replaces
+// there from M = 3: 9.6 / 10.1 us against 11.0 / 10.7-11.0 at M = 4 / 8).
 // The merged 28672 x 4096 gate_up in half-gate / half-up tiles at M = 1 /
 // 2: 15.5 / 16.2 us, against 16.4-16.5 / 16.3 on the stream and wave
 // kernels and 17.1 / 17.2 in tile pairs; from M = 3 the wave kernel is
@@ -2181,7 +2185,7 @@ static hipError_t launch_lean_t(const WoqArgs &a, hipStream_t s, int shift, int 
 static bool lean_preferred(const WoqArgs &a, int gu) {
   if (gu) return a.M <= 2;
   if (a.K >= 8192) return a.M <= 4;
-  if (a.N >= 12288) return a.M <= 2 || (a.N >= 28672 && a.M >= 12);
+  if (a.N > 8192) return a.M <= 2 || (a.N >= 28672 && a.M >= 12);
   return false;
 }
 
