@@ -125,6 +125,32 @@ def test_wide_kernel_reduce_split_counts(splits, knobs):
     run_case(33, 3072, 136, 24, kernel="wide", post=("add",), nbuf=1, seed=int(splits), bias=True)
 
 
+# uneven K splits, where no divisor of the phase count (K / 256) gives whole
+# rounds of four phases: splits of whole rounds with a shorter last split
+# (43 phases at K = 11008, 74 at 18944, 14 at 3584), chosen by the planner
+# or forced (ZT_WOQ_WIDE: 5 splits of 43 phases -> 12, 12, 12, 7; 3 of 14
+# -> 8, 6)
+@pytest.mark.parametrize("M,K,N,splits,post,nbuf", [(17, 11008, 136, None, (), 0),
+                                                     (40, 18944, 200, None, ("add",), 1),
+                                                     (64, 11008, 264, "5", ("mul", "add"), 2),
+                                                     (33, 3584, 96, "3", (), 0)])
+def test_wide_kernel_uneven_splits(M, K, N, splits, post, nbuf, knobs):
+    if splits:
+        knobs.set("ZT_WOQ_WIDE", splits)
+    run_case(M, K, N, K // 128, kernel="wide", post=post, nbuf=nbuf, seed=M + K, bias=True)
+
+
+# 4608 x 3584 at 17..64 rows (Qwen2's QKV): more than one round of 16-row
+# tiles, so the library's own choice is the wide kernel (14 phases in 4
+# uneven splits), with post-ops
+@pytest.mark.parametrize("M", [17, 40, 64])
+def test_wide_kernel_default_past_one_round(M, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    run_case(M, 3584, 4608, 28, post=("add",), nbuf=1, seed=M, bias=True)
+    assert "woq wide" in capfd.readouterr().err
+
+
 def test_wide_kernel_strided_x():
     M, K, N, G = 48, 4096, 512, 32
     x, q, wp, s, z, b = make_case(M, K, N, G, seed=77)

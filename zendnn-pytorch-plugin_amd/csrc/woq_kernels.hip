@@ -2388,7 +2388,9 @@ __global__ __launch_bounds__(512) void woq_wide_kernel(WoqArgs a, int pps, int c
   const int ldx2 = (int)a.ldx * 2;
   const int n0 = blockIdx.x * kWideRows;
   const int ph0 = blockIdx.y * pps;  // first phase of this K split
-  const int pend = ph0 + pps;
+  // the last split may be shorter (uneven splits): its phases past K load
+  // zeros and add nothing
+  const int pend = min(ph0 + pps, (int)(a.K / kWideKP));
   // merged gate_up (gu = N/2, a multiple of 64): local rows [0, 64) are gate
   // rows j0.., local rows [64, 128) the up rows gu + j0..
   const int j0 = blockIdx.x * (kWideRows / 2);
@@ -2664,26 +2666,39 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   // M = 10, where x no longer fits twice)
   if (M * (K + 8) * 2 <= 76 * 1024 && !forced) return false;
   // (also up to 64 rows: the 4096 x 4096 O projection at M = 64 takes
-  // 12.3 us on the stream kernel against 15.8 us split 8 ways here)
-  if (M <= 64 && N * K <= (int64_t)4096 * 4096 && !forced) return false;
+  // 12.3 us on the stream kernel against 15.8 us split 8 ways here), while
+  // the stream kernel's 16-row tiles make one round (past 4096 rows its
+  // second round doubles the call: 4608 x 3584 at M = 32 / 64 took 15.2 /
+  // 24.6 us there against 11.8 / 14.4 here)
+  if (M <= 64 && N <= 4096 && N * K <= (int64_t)4096 * 4096 && !forced) return false;
   const int64_t gs = K / G, cpg = gs / 128;
   if (G != 1 && (gs % 128 || (cpg & (cpg - 1)))) return false;
   const int phases = (int)(K / kWideKP);
   const int64_t blocks = (N + kWideRows - 1) / kWideRows;
   // the most K splits (a divisor of the phase count) of whole rounds of
-  // phases that keep the grid within about 1.25 rounds of 256 CUs; without
-  // such a split the padded form with the most splits
-  int ks = 0;
+  // phases that keep the grid within about 1.25 rounds of 256 CUs.  Without
+  // such a divisor: splits of whole rounds with a shorter last split (its
+  // phases past K load zeros), as many as keep the grid within 1.25 rounds
+  // (a prime phase count left 4096 x 11008 at M = 17..64 unsplit on 32
+  // workgroups: 41-52 us)
+  int ks = 0, pps = 0;
   for (int d = 1; d <= phases; ++d)
     if (phases % d == 0 && (phases / d) % kWideRound == 0 && blocks * d <= 320) ks = d;
-  if (ks == 0) {
-    ks = 1;
-    for (int d = 1; d <= phases; ++d)
-      if (phases % d == 0 && blocks * d <= 320) ks = d;
+  if (ks > 0) {
+    pps = phases / ks;
+  } else {
+    const int target = (int)std::max<int64_t>(1, std::min<int64_t>(phases, 320 / blocks));
+    pps = ((phases + target - 1) / target + kWideRound - 1) / kWideRound * kWideRound;
+    ks = (phases + pps - 1) / pps;
   }
   if (e) {
     const int f = std::atoi(e);
-    if (f >= 1 && phases % f == 0) ks = f;
+    if (f >= 1 && f <= phases) {
+      ks = f;
+      pps = (phases + f - 1) / f;
+      if (phases % f) pps = (pps + kWideRound - 1) / kWideRound * kWideRound;
+      ks = (phases + pps - 1) / pps;
+    }
   }
   // up to 16 rows: only without a K split (measured: gate_up 28672 x 4096
   // at M = 12 / 16 takes 22.6 / 22.9 us here against 25.9 / 27.2 on the
@@ -2693,7 +2708,7 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   if (M < 17 && (ks > 1 || blocks < 128) && !forced) return false;
   p->mt = M <= 32 ? 1 : 2;
   p->splits = ks;
-  p->pps = phases / ks;
+  p->pps = pps;
   p->pad = p->pps % kWideRound != 0;
   return true;
 }
