@@ -97,10 +97,12 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                   int32_t y_dtype, int64_t ldy, void *workspace,
                   size_t workspace_bytes, zt_stream_t stream);
 
-/* Bytes of device workspace zt_woq_linear needs for these sizes.  Calls of
- * 17..64 rows that split K over several workgroups keep fp32 partials
- * [splits][M][N] there (no initial contents needed); other sizes need none
- * (0).  Calls that overlap in time must not share a workspace. */
+/* Bytes of device workspace zt_woq_linear needs for these sizes.  Calls that
+ * split K over several workgroups keep fp32 partials [splits][M][N] there
+ * (no initial contents needed): 17..64 rows on large matrices, and prefill
+ * calls whose row tiles make less than one round of the GPU (a smaller
+ * workspace runs those unsplit); other sizes need none (0).  Calls that
+ * overlap in time must not share a workspace. */
 size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
                                     int64_t G);
 

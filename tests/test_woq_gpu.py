@@ -151,6 +151,20 @@ def test_wide_kernel_default_past_one_round(M, knobs, capfd):
     assert "woq wide" in capfd.readouterr().err
 
 
+# prefill GEMM with a K split: when its 128 x 128 tiles make less than one
+# round (65..~500 rows on small matrices) the workgroups write fp32 partials
+# of whole 64-k step ranges into the workspace and the reduce kernel adds
+# them in split order and applies bias and post-ops
+@pytest.mark.parametrize("M,K,N,post,nbuf", [(65, 4096, 264, (), 0), (128, 11008, 256, ("add",), 1),
+                                             (300, 2048, 512, ("gelu_tanh",), 0),
+                                             (512, 8192, 136, ("mul", "add"), 2)])
+def test_gemm32_kernel_k_split(M, K, N, post, nbuf, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    run_case(M, K, N, K // 128, post=post, nbuf=nbuf, seed=M + N, bias=True)
+    assert "K splits" in capfd.readouterr().err
+
+
 def test_wide_kernel_strided_x():
     M, K, N, G = 48, 4096, 512, 32
     x, q, wp, s, z, b = make_case(M, K, N, G, seed=77)

@@ -278,9 +278,11 @@ size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
   // Assume aligned pointers: the workspace a call needs is never larger.
   a.x = reinterpret_cast<const void *>(256);
   a.w = reinterpret_cast<const uint32_t *>(256);
-  if (zt::woq_select_kernel(a) != zt::kWoqDecode) return wide;
+  // the prefill GEMM's K-split partials (few tiles)
+  const size_t gemm = zt::woq_gemm_workspace(M, N, K);
+  if (zt::woq_select_kernel(a) != zt::kWoqDecode) return std::max(wide, gemm);
   zt::DecodePlan p;
-  if (!zt::woq_decode_plan(M, N, K, &p)) return wide;
+  if (!zt::woq_decode_plan(M, N, K, &p)) return std::max(wide, gemm);
   return std::max(wide, zt::woq_decode_workspace(p, M, N));
 }
 
@@ -356,7 +358,8 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
     zt::DecodePlan p;
     if (!zt::woq_decode_plan(M, N, K, &p)) {
       const int64_t gs = K / G;
-      if (K % 64 == 0 && gs % 32 == 0) return hip_status(zt::launch_woq_gemm(a, s), op);
+      if (K % 64 == 0 && gs % 32 == 0)
+        return hip_status(zt::launch_woq_gemm(a, s, workspace, workspace_bytes), op);
       return hip_status(zt::launch_woq_generic(a, s), op);
     }
     const size_t need = zt::woq_decode_workspace(p, M, N);
@@ -366,7 +369,7 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
     return hip_status(zt::launch_woq_decode(a, p, workspace, s), op);
   }
   case zt::kWoqGemm:
-    return hip_status(zt::launch_woq_gemm(a, s), op);
+    return hip_status(zt::launch_woq_gemm(a, s, workspace, workspace_bytes), op);
   default:
     return hip_status(zt::launch_woq_generic(a, s), op);
   }

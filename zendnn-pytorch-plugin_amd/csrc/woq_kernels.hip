@@ -845,6 +845,22 @@ void woq_gemm_dma_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int c
   woq_tile_epilogue<BM, BN>(a, tile, m0, n0, tid);
 }
 
+// ROWS x BN fp32 tile staged in LDS (row pitch BN + 4) -> rows m0.. and
+// columns n0.. of a K split's fp32 partial [M][N] (N % 4 == 0: a column
+// quad lies wholly inside or past N), NT threads.
+template <int ROWS, int BN, int NT = 256>
+__device__ __forceinline__ void woq_tile_store_partial(const float *tile, float *pp, int m0,
+                                                       int n0, int M, int N, int tid) {
+  constexpr int TP = BN + 4, Q = BN / 4;
+  for (int idx = tid; idx < ROWS * Q; idx += NT) {
+    const int r = idx / Q, c = (idx - r * Q) * 4;
+    const int m = m0 + r, n = n0 + c;
+    if (m < M && n < N)
+      *reinterpret_cast<f32x4_t *>(pp + (size_t)m * N + n) =
+          *reinterpret_cast<const f32x4_t *>(tile + r * TP + c);
+  }
+}
+
 // Prefill int4 GEMM on v_mfma_f32_32x32x16_bf16 (signed int4, bf16 scales):
 // BM x BN tiles, 4 waves of (BM/2) x (BN/2), K in steps of 64, two stages
 // moved straight into LDS by the buffer unit: the x slab [BM][64] bf16 (128 B
@@ -866,6 +882,10 @@ void woq_gemm_dma_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int c
 // weight), B = x, so D is [n][m]: register r of lane l holds
 // n = 8*(r/4) + 4*(l/32) + r%4 and m = l%32.  The epilogue stages one half of
 // the tile (the rows of the waves with wm == h) as fp32 [m][n] at a time.
+// With a K split (partial set, grid.y splits of sps steps) a workgroup walks
+// its split's steps only and writes its fp32 tile to partial[split][M][N];
+// woq_splitk_reduce_kernel then adds the splits in order and applies the
+// epilogue.
 constexpr int kW32BK = 64;
 
 // s_waitcnt immediate that waits for at most n outstanding vector-memory
@@ -888,7 +908,7 @@ constexpr size_t woq_gemm32_lds() {
 template <int BM, int BN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void woq_gemm32_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg_shift,
-                       int gmask) {
+                       int gmask, float *partial, int sps) {
   constexpr int WTM = BM / 64, WTN = BN / 64;  // 32 x 32 tiles per wave
   constexpr int STAGE = (int)woq_gemm32_stage<BM, BN>();
   constexpr int XI = BM / 8;                    // 1 KB x loads (8 rows) per stage
@@ -918,9 +938,12 @@ void woq_gemm32_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg
 
   // the wave's loads: index li = wv * LPW + q; x loads first, then the
   // weight loads, then the scale row (lanes 0..BN/8-1, 16 bytes each)
+  const int nk = K / kW32BK;
+  const int kb = partial ? (int)blockIdx.y * sps : 0;   // this workgroup's steps [kb, ke)
+  const int ke = partial ? min(kb + sps, nk) : nk;
   auto dma = [&](int step) {
     const int k0 = step * kW32BK;
-    const bool in = k0 < K;
+    const bool in = step < ke;
     unsigned char *stage = smem + (step & 1) * STAGE;
 #pragma unroll
     for (int q = 0; q < LPW; ++q) {
@@ -959,9 +982,8 @@ void woq_gemm32_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = K / kW32BK;
-  dma(0);
-  for (int ks = 0; ks < nk; ++ks) {
+  dma(kb);
+  for (int ks = kb; ks < ke; ++ks) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of step ks
     asm volatile("s_barrier" ::: "memory");
     dma(ks + 1);  // past the last step: zeros into the buffer step ks - 1 used
@@ -1017,7 +1039,11 @@ void woq_gemm32_kernel(WoqArgs a, int tiles_m, int tiles_n, int group_m, int cpg
                         acc[i][j][4 * q + 3]};
     }
     __syncthreads();
-    woq_tile_epilogue<BM / 2, BN>(a, tile, m0 + h * (BM / 2), n0, tid);
+    if (partial)
+      woq_tile_store_partial<BM / 2, BN>(tile, partial + (size_t)blockIdx.y * M * N,
+                                         m0 + h * (BM / 2), n0, M, N, tid);
+    else
+      woq_tile_epilogue<BM / 2, BN>(a, tile, m0 + h * (BM / 2), n0, tid);
     __syncthreads();
   }
 }
@@ -1191,12 +1217,18 @@ static hipError_t launch_woq_gemm_ws_t(const WoqArgs &a, hipStream_t s, int shif
   return hipGetLastError();
 }
 
+// splits > 1: K split into splits ranges of whole steps, fp32 partials to
+// `partial` ([splits][M][N]); the caller adds them
 template <int BM, int BN>
-static hipError_t launch_woq_gemm32_t(const WoqArgs &a, hipStream_t s, int shift, int gmask) {
+static hipError_t launch_woq_gemm32_t(const WoqArgs &a, hipStream_t s, int shift, int gmask,
+                                      float *partial = nullptr, int splits = 1) {
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
   const int group_m = tiles_m < 4 ? tiles_m : 4;
-  woq_gemm32_kernel<BM, BN><<<dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
-                              woq_gemm32_lds<BM, BN>(), s>>>(a, tiles_m, tiles_n, group_m, shift, gmask);
+  const int nk = (int)(a.K / kW32BK);
+  const int sps = splits > 1 ? (nk + splits - 1) / splits : nk;
+  woq_gemm32_kernel<BM, BN><<<dim3((unsigned)(tiles_m * tiles_n), (unsigned)(splits > 1 ? splits : 1)),
+                              dim3(256), woq_gemm32_lds<BM, BN>(), s>>>(
+      a, tiles_m, tiles_n, group_m, shift, gmask, splits > 1 ? partial : nullptr, sps);
   return hipGetLastError();
 }
 
@@ -2639,6 +2671,22 @@ __global__ __launch_bounds__(256) void woq_splitk_reduce_kernel(WoqArgs a, const
   }
 }
 
+// y = epilogue(sum of the `splits` fp32 partials [splits][M][N]), in split order
+static hipError_t launch_splitk_reduce(const WoqArgs &a, const float *partial, int splits,
+                                       hipStream_t s) {
+  const int64_t n4 = a.M * (a.N / 4);
+  const dim3 rgrid((unsigned)((n4 + 255) / 256)), rblock(256);
+  switch (splits) {
+#define ZT_REDUCE_CASE(S_) \
+  case S_: woq_splitk_reduce_kernel<S_><<<rgrid, rblock, 0, s>>>(a, partial, splits); break;
+    ZT_REDUCE_CASE(2) ZT_REDUCE_CASE(3) ZT_REDUCE_CASE(4) ZT_REDUCE_CASE(5)
+    ZT_REDUCE_CASE(6) ZT_REDUCE_CASE(7) ZT_REDUCE_CASE(8)
+#undef ZT_REDUCE_CASE
+    default: woq_splitk_reduce_kernel<0><<<rgrid, rblock, 0, s>>>(a, partial, splits); break;
+  }
+  return hipGetLastError();
+}
+
 static void launch_wide_t(const WoqArgs &a, const WidePlan &p, dim3 grid, int shift, int gmask,
                           float *partial, int gu, hipStream_t s) {
   if (p.mt == 1 && !p.pad)
@@ -2743,17 +2791,7 @@ hipError_t launch_woq_wide(const WoqArgs &a, const WidePlan &p, void *workspace,
   launch_wide_t(a, p, grid, shift, gmask, partial, 0, s);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
-  const int64_t n4 = a.M * (a.N / 4);
-  const dim3 rgrid((unsigned)((n4 + 255) / 256)), rblock(256);
-  switch (p.splits) {
-#define ZT_REDUCE_CASE(S_) \
-  case S_: woq_splitk_reduce_kernel<S_><<<rgrid, rblock, 0, s>>>(a, partial, p.splits); break;
-    ZT_REDUCE_CASE(2) ZT_REDUCE_CASE(3) ZT_REDUCE_CASE(4) ZT_REDUCE_CASE(5)
-    ZT_REDUCE_CASE(6) ZT_REDUCE_CASE(7) ZT_REDUCE_CASE(8)
-#undef ZT_REDUCE_CASE
-    default: woq_splitk_reduce_kernel<0><<<rgrid, rblock, 0, s>>>(a, partial, p.splits); break;
-  }
-  return hipGetLastError();
+  return launch_splitk_reduce(a, partial, p.splits, s);
 }
 
 // Merged gate_up on the wide kernel: one launch writes silu(gate) * up,
@@ -2898,7 +2936,28 @@ hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *worksp
   return hipErrorInvalidValue;
 }
 
+// K splits of the prefill GEMM when its 128 x 128 tiles (the tile it takes
+// below half a round of 256 x 128 tiles) make less than one round: up to 8,
+// about two workgroups per CU, at least 16 steps of 64 each (1 = no split)
+int woq_gemm_splits(int64_t M, int64_t N, int64_t K) {
+  if (knob(kKnobWoqGemm)) return 1;
+  const int64_t t256 = ((M + 255) / 256) * ((N + 127) / 128);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (t256 >= 128 || t128 >= 256) return 1;
+  const int64_t sp = std::min<int64_t>(std::min<int64_t>(8, 512 / t128), (K / kW32BK) / 16);
+  return sp >= 2 ? (int)sp : 1;
+}
+
+size_t woq_gemm_workspace(int64_t M, int64_t N, int64_t K) {
+  const int sp = woq_gemm_splits(M, N, K);
+  return sp > 1 ? (size_t)sp * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
 hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
+  return launch_woq_gemm(a, s, nullptr, 0);
+}
+
+hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s, void *workspace, size_t workspace_bytes) {
   {
     // the DMA kernel: bf16 x, K % 128 == 0, one scale per 128-chunk, 32-bit
     // byte offsets for x and the weights
@@ -2933,8 +2992,24 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s) {
         if (ws)
           return e && e[0] == 'w' ? launch_woq_gemm_ws_t<256, 128, 4>(a, s, shift, gmask)
                                   : launch_woq_gemm_ws_t<256, 128, 3>(a, s, shift, gmask);
-        return big32 ? launch_woq_gemm32_t<256, 128>(a, s, shift, gmask)
-                     : launch_woq_gemm32_t<128, 128>(a, s, shift, gmask);
+        if (big32) return launch_woq_gemm32_t<256, 128>(a, s, shift, gmask);
+        // few tiles: K split over fp32 partials in the workspace when it has
+        // room (graph replays over rotating weights, one box, M = 512:
+        // 4096 x 11008 148.5 us and 3072 x 8192 113.9 us unsplit, as long as
+        // at M = 2048 on twice the tile area)
+        const int sp = woq_gemm_splits(a.M, a.N, a.K);
+        const size_t need = woq_gemm_workspace(a.M, a.N, a.K);
+        if (sp > 1 && workspace && workspace_bytes >= need &&
+            (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
+          if (knob(kKnobWoqDebug))
+            std::fprintf(stderr, "[zt] woq gemm32 M=%lld N=%lld K=%lld: 128x128 tiles, %d K splits\n",
+                         (long long)a.M, (long long)a.N, (long long)a.K, sp);
+          float *partial = static_cast<float *>(workspace);
+          hipError_t err = launch_woq_gemm32_t<128, 128>(a, s, shift, gmask, partial, sp);
+          if (err != hipSuccess) return err;
+          return launch_splitk_reduce(a, partial, sp, s);
+        }
+        return launch_woq_gemm32_t<128, 128>(a, s, shift, gmask);
       }
       // 256 x 128 only for the fast mode: the general dequant spills there
       const bool big = mode == kDecFast && (e ? e[0] == '2' : t256 >= 128);

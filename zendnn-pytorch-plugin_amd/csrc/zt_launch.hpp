@@ -51,6 +51,13 @@ hipError_t launch_woq_generic(const WoqArgs &a, hipStream_t s);
 hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p,
                              void *workspace, hipStream_t s);
 hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s);
+// With a workspace of woq_gemm_workspace(M, N, K) bytes the prefill GEMM
+// splits K when its tiles make less than a round (woq_gemm_splits > 1);
+// with less it runs unsplit.
+hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s, void *workspace,
+                           size_t workspace_bytes);
+int woq_gemm_splits(int64_t M, int64_t N, int64_t K);
+size_t woq_gemm_workspace(int64_t M, int64_t N, int64_t K);
 // The weight-streaming decode kernel for up to 64 rows, when it applies
 // (returns false otherwise; *err holds the launch status when it does).
 bool woq_try_stream(const WoqArgs &a, hipStream_t s, hipError_t *err);
