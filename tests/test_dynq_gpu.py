@@ -75,7 +75,11 @@ def test_quantize_ties_bit_exact(x_dtype):
                                    (33, 100, 4112), (100, 4100, 272), (17, 50, 80),
                                    # more tiles than CUs (workgroups loop over tiles),
                                    # ragged M and N, K % 64 != 0
-                                   (2100, 4100, 144), (4096, 2080, 208)])
+                                   (2100, 4100, 144), (4096, 2080, 208),
+                                   # 129..255 rows on the tiled kernels, and at most
+                                   # half a round of 256 x 128 tiles (128 x 128)
+                                   (129, 300, 1024), (200, 4096, 2048), (255, 136, 4112),
+                                   (512, 4096, 1024)])
 def test_s8_gemm_accumulators_bit_exact(M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
@@ -86,7 +90,8 @@ def test_s8_gemm_accumulators_bit_exact(M, N, K):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4, 8), (4, 12, 16), (16, 16, 32), (24, 128, 48),
-                                   (128, 4096, 11008), (33, 4096, 4096), (256, 1024, 640)])
+                                   (128, 4096, 11008), (33, 4096, 4096), (256, 1024, 640),
+                                   (160, 2048, 4096), (512, 1024, 3584)])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
 def test_dynamic_qlinear_vs_oracle(M, K, N, x_dtype):
     x, w, sw, b = make(M, K, N, seed=M + K + N, x_dtype=x_dtype)

@@ -2120,7 +2120,10 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
   // the fast kernels address qx and W with 32-bit byte offsets
   const bool fits32 = a.M * a.K < (int64_t)kOobOffset && a.N * a.K < (int64_t)kOobOffset;
   const char *force = knob(kKnobS8Force);  // t: tiled, s: skinny, o: old
-  const bool tiled = force ? force[0] == 't' : a.M >= 256;
+  // past the skinny kernels' 128 tokens the tiled kernels (129..255 had
+  // fallen to the 16x16 kernel below: O 4096 x 4096 at M = 192 took 176 us
+  // against 40 at M = 256)
+  const bool tiled = force ? force[0] == 't' : a.M > 128;
   const bool skinny = force ? force[0] == 's' : a.M <= 128;
   if (skinny && fits32 && a.K % 64 == 0) return launch_s8_skinny(a, s);
   if (tiled && fits32) {
@@ -2135,6 +2138,13 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
       // stages (two workgroups per CU)
       if (tile && tile[0] == '1') return launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s);
       if (tile && tile[0] == '0') return launch_s8_ws<128, 128, 2, 2, 4, 2>(a, s);
+      // at most half a round of 256 x 128 tiles: 128 x 128 tiles, twice as
+      // many workgroups (graph replays, one box: 4096 x 14336 at M = 256 /
+      // 512 / 1024 90.1 / 92.4 / 96.9 -> 57.8 / 59.7 / 77.5 us, 4096 x 4096
+      // 40.3 / 38.1 / 39.9 -> 38.6 / 27.0 / 32.7, 6144 x 4096 at M = 256 /
+      // 512 36.9 / 38.0 -> 26.0 / 28.4; more tiles keep 256 x 128: 11008 x
+      // 4096 at M = 512 39.0 against 47.1)
+      if (!tile && t256 <= 128) return launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s);
       // 256 x 192 tiles (six compute waves of 128 x 64, two load waves, two
       // stages) where they make one round and 256 x 128 tiles do not: QKV at
       // M = 2048, 256 against 384 tiles, 69 -> 58.5 us
