@@ -94,6 +94,17 @@ def test_c_abi_validates_without_gpu():
     # the WOQ kernels reduce K inside a workgroup: no device workspace
     assert L.zt_woq_linear_workspace_size(16, 14336, 4096, 112) == 0
     assert L.zt_woq_linear_workspace_size(2048, 4096, 4096, 32) == 0
+    # prefill GEMMs whose tiles make less than one round split K: fp32 (int4)
+    # or int32 (int8) partials [splits][M][N] follow the base workspace
+    assert L.zt_woq_linear_workspace_size(512, 4096, 4096, 32) == 4 * 512 * 4096 * 4
+    assert L.zt_woq_linear_workspace_size(128, 11008, 4096, 86) == 8 * 128 * 4096 * 4
+    assert L.zt_dynamic_qlinear_workspace_size(512, 4096, 4096) >= \
+        L.zt_dynamic_qlinear_workspace_size(512, 4096, 0) + 2 * 512 * 4096 * 4
+    # empty sizes (N = 0 asks for the least workspace) plan no split
+    assert L.zt_dynamic_qlinear_workspace_size(512, 4096, 0) >= 512 * 4096 + 512 * 4
+    assert L.zt_dynamic_qlinear_asym_workspace_size(512, 4096, 0) >= 512 * 4096 + 512 * 8
+    assert L.zt_woq_linear_workspace_size(512, 4096, 0, 32) == 0
+    assert L.zt_dynamic_qlinear_workspace_size(0, 4096, 4096) == 0
 
 
 # Schemas as the reference registers them (src/cpu/cpp/WOQ_Linear.cpp:435-480,

@@ -296,6 +296,37 @@ def test_dynamic_qlinear_fragment_kernel_post_ops(post):
     torch.testing.assert_close(y.float(), y_ref.float(), rtol=1e-2, atol=1e-2)
 
 
+# past 128 tokens with at most half a round of 256 x 128 tiles, the tiled
+# kernel's K split (128 x 128 tiles, int32 partials in the workspace, then
+# the sum kernel's epilogue): bit-identical to the unsplit kernel (the least
+# workspace), including a last step past K and post-ops; the asymmetric op
+# takes it too
+@pytest.mark.parametrize("M,K,N,post", [(129, 4096, 4096, ()), (300, 5008, 520, ("add",)),
+                                        (512, 14336, 1024, ("mul", "add")),
+                                        (200, 2048, 136, ("gelu_tanh",))])
+def test_dynamic_qlinear_tiled_k_split(M, K, N, post, knobs, capfd):
+    x, w, sw, b = make(M, K, N, seed=M + K)
+    g = torch.Generator().manual_seed(3)
+    bufs = [torch.randn(M, N, generator=g).bfloat16() for p in post if p in ("add", "mul")]
+    args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV))
+    kw = dict(post_ops=post, post_bufs=[t.to(DEV) for t in bufs])
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    y = C.dynamic_qlinear(*args, **kw).cpu()
+    assert "K splits" in capfd.readouterr().err
+    assert torch.equal(y, C.dynamic_qlinear(*args, split=False, **kw).cpu())
+    torch.testing.assert_close(y.float(), O.dynamic_qlinear(x, w, sw, b, post_ops=post,
+                                                            post_bufs=bufs).float(),
+                               rtol=1e-2, atol=1e-2)
+    if not post:
+        import zentorch  # noqa: F401  (registers the column-sum op)
+        cs = torch.ops.zentorch.zentorch_s8_weight_colsum(w.to(DEV))
+        ya = C.dynamic_qlinear_asym(x.to(DEV), w.to(DEV), sw.to(DEV), cs, b.to(DEV)).cpu()
+        yb = C.dynamic_qlinear_asym(x.to(DEV), w.to(DEV), sw.to(DEV), cs, b.to(DEV),
+                                    split=False).cpu()
+        assert torch.equal(ya, yb)
+
+
 # post-ops in the large-M load-wave kernel's epilogue (the general path of
 # its tile epilogue), with 256 x 128 and 256 x 192 tiles
 @pytest.mark.parametrize("tile", ["2", "9"])

@@ -444,9 +444,16 @@ size_t zt_dynamic_qlinear_workspace_size(int64_t M, int64_t K, int64_t N) {
 
 // Points a at the split-K exchange when the workspace holds it; returns the
 // tile-counter count the quantise kernel must clear (0: no split).
+// Past 128 tokens the same room holds the tiled GEMM's K-split partials
+// (gemm_splits > 1, no counters).
 static int attach_split(zt::DynArgs &a, char *ws, size_t ws_bytes, size_t base) {
   const size_t sb = zt::s8_split_bytes(a.M, a.K, a.N);
   if (!sb || ws_bytes < base + sb) return 0;
+  if (a.M > 128) {
+    a.split_part = reinterpret_cast<int32_t *>(ws + base);
+    a.gemm_splits = zt::s8_ws_splits(a.M, a.N, a.K);
+    return 0;
+  }
   const int nc = zt::s8_split_counters(a.N);
   a.split_part = reinterpret_cast<int32_t *>(ws + base);
   a.split_cnt = reinterpret_cast<int32_t *>(ws + base + sb - (((size_t)nc * 4 + 255) & ~(size_t)255));
@@ -519,7 +526,7 @@ static int dynamic_qlinear_common(const char *op, const void *x, int32_t x_dtype
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // few tokens: one launch that quantises x in the GEMM's prologue
   if (zt::s8_fused_ok(a)) return hip_status(zt::launch_s8_skinny_fused(a, s), op);
-  const int nc = a.qx_frag ? attach_split(a, ws, workspace_bytes, need) : 0;
+  const int nc = a.qx_frag || a.M > 128 ? attach_split(a, ws, workspace_bytes, need) : 0;
   rc = hip_status(zt::launch_dyn_quantize(x, x_dtype, M, K, qx, sx, a.qx_frag != 0, s, azp,
                                           a.split_cnt, nc),
                   op);
@@ -592,7 +599,7 @@ int zt_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K, const float
   int32_t *azp = offset ? reinterpret_cast<int32_t *>(ws + dyn_qx_bytes(M, K) + M * 4) : nullptr;
   a.qx = qx, a.sx = sx, a.azp = azp, a.colsum = offset ? w_colsum : nullptr;
   a.qx_frag = zt::s8_frag_ok(a) ? 1 : 0;
-  const int nc = a.qx_frag ? attach_split(a, ws, workspace_bytes, need) : 0;
+  const int nc = a.qx_frag || a.M > 128 ? attach_split(a, ws, workspace_bytes, need) : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   rc = hip_status(zt::launch_static_quantize(x, x_dtype, M, K, qx, a.qx_frag != 0, x_scale,
                                              x_zero_point, sx, azp, s, a.split_cnt, nc),

@@ -961,9 +961,14 @@ constexpr size_t s8_ws_lds() {
   return stages > tile ? stages : tile;
 }
 
+// With a K split (partial set, grid.y splits of sps steps) a workgroup
+// walks its split's steps only and writes its int32 tile to
+// partial[split][M][N] (N % 4 == 0); s8_splitk_sum_kernel adds the splits
+// and applies the epilogue.
 template <int BM, int BN, int WM, int WN, int ND, int S>
 __global__ __launch_bounds__(64 * (WM * WN + ND)) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
+void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m, int32_t *partial,
+                       int sps) {
   constexpr int NC = WM * WN, NT = 64 * (NC + ND);
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32 x 32 tiles per compute wave
   constexpr int STAGE = (BM + BN) * kWsBK;
@@ -981,6 +986,8 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
   const int M = (int)a.M, N = (int)a.N, K = (int)a.K;
   const int m0 = tm * BM, n0 = tn * BN;
   const int nk = (K + kWsBK - 1) / kWsBK;
+  const int kb = partial ? (int)blockIdx.y * sps : 0;  // this workgroup's steps [kb, ke)
+  const int ke = partial ? min(kb + sps, nk) : nk;
   // the accumulators are set (zeroed) only on the compute waves' path, so
   // the load waves' loop does not hold their registers
   i32x16_t acc[TM][TN];
@@ -1008,7 +1015,7 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
 #pragma unroll
       for (int q = 0; q < LPW; ++q) {
         // K % 16 == 0: a 16-byte chunk lies wholly inside or past its row
-        const uint32_t off = (src[q] == kOobOffset || step >= nk || k0 + chunk(q) >= K)
+        const uint32_t off = (src[q] == kOobOffset || step >= ke || k0 + chunk(q) >= K)
                                  ? kOobOffset : src[q] + (uint32_t)k0;
         lds_ptr_t dst = (lds_ptr_t)(stage + (dw * LPW + q) * 1024);
         if ((dw * LPW + q) * 8 < BM)  // whole loads lie in A or in B
@@ -1018,8 +1025,8 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
       }
     };
 #pragma unroll
-    for (int p = 0; p < S - 1; ++p) dma(p);
-    for (int ks = 0; ks < nk; ++ks) {
+    for (int p = 0; p < S - 1; ++p) dma(kb + p);
+    for (int ks = kb; ks < ke; ++ks) {
       __builtin_amdgcn_s_waitcnt(vmcnt_wait_imm((S - 2) * LPW));
       asm volatile("s_barrier" ::: "memory");
       dma(ks + S - 1);
@@ -1048,7 +1055,7 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
       for (int j = 0; j < TN; ++j)
         Fb[buf][j] = *reinterpret_cast<const i32x4_t *>(stage + b_base + j * 32 * kWsBK + pos);
     };
-    for (int ks = 0; ks < nk; ++ks) {
+    for (int ks = kb; ks < ke; ++ks) {
       asm volatile("s_barrier" ::: "memory");
       read(ks, 0, 0);
 #pragma unroll
@@ -1089,19 +1096,63 @@ void s8_gemm_ws_kernel(DynArgs a, int tiles_m, int tiles_n, int group_m) {
                 i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                         acc[i][j][4 * q + 3]};
     }
+    if (partial) {
+      // the split's int32 tile, four columns at a time (N % 4 == 0)
+      __syncthreads();
+      int32_t *pp = partial + (size_t)blockIdx.y * M * N;
+      for (int idx = tid; idx < R * (BN / 4); idx += NT) {
+        const int r = idx / (BN / 4), c = (idx - r * (BN / 4)) * 4;
+        const int m = m0 + h * R + r, n = n0 + c;
+        if (m < M && n < N)
+          *reinterpret_cast<i32x4_t *>(pp + (size_t)m * N + n) =
+              *reinterpret_cast<const i32x4_t *>(tile + r * AP + c);
+      }
+      continue;
+    }
     s8_stage_row_scales<R, NT>(a, sx_l, m0 + h * R, tid);
     __syncthreads();
     s8_tile_epilogue<R, BN, NT>(a, tile, sx_l, m0 + h * R, n0, tid);
   }
 }
 
+// y = epilogue(the sum of the K splits' int32 partials [splits][M][N]),
+// four columns per thread (N % 4 == 0); the sums are exact, so the result
+// is the unsplit kernel's bit for bit
+__global__ __launch_bounds__(256) void s8_splitk_sum_kernel(DynArgs a, const int32_t *partial,
+                                                            int splits) {
+  const int M = (int)a.M, N = (int)a.N;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * (N / 4)) return;
+  const int m = (int)(idx / (N / 4)), n = (int)(idx % (N / 4)) * 4;
+  const size_t stride = (size_t)M * N;
+  const int32_t *p = partial + (size_t)m * N + n;
+  i32x4_t q[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    q[s] = s < splits ? *reinterpret_cast<const i32x4_t *>(p + s * stride) : i32x4_t{0, 0, 0, 0};
+  i32x4_t v = q[0];
+#pragma unroll
+  for (int s = 1; s < 8; ++s) v += q[s];
+  dyn_epilogue4(a, m, n, v);
+}
+
+// splits > 1: K split over a.split_part (int32 partials), then the sum
 template <int BM, int BN, int WM, int WN, int ND, int S>
-hipError_t launch_s8_ws(const DynArgs &a, hipStream_t s) {
+hipError_t launch_s8_ws(const DynArgs &a, hipStream_t s, int splits = 1) {
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
   const int group_m = tiles_m < 4 ? tiles_m : 4;
+  const int nk = (int)((a.K + kWsBK - 1) / kWsBK);
+  const bool split = splits > 1 && a.split_part;
+  const int sps = split ? (nk + splits - 1) / splits : nk;
+  const int gy = split ? (nk + sps - 1) / sps : 1;
   s8_gemm_ws_kernel<BM, BN, WM, WN, ND, S>
-      <<<dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * (WM * WN + ND)), s8_ws_lds<BM, BN, S>(),
-         s>>>(a, tiles_m, tiles_n, group_m);
+      <<<dim3((unsigned)(tiles_m * tiles_n), (unsigned)gy), dim3(64 * (WM * WN + ND)),
+         s8_ws_lds<BM, BN, S>(), s>>>(a, tiles_m, tiles_n, group_m,
+                                      split ? a.split_part : nullptr, sps);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || !split) return err;
+  const int64_t n4 = a.M * (a.N / 4);
+  s8_splitk_sum_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(a, a.split_part, gy);
   return hipGetLastError();
 }
 
@@ -2087,7 +2138,24 @@ hipError_t launch_s8_colsum(const int8_t *w, int64_t N, int64_t K, int32_t *cols
 
 int s8_split_counters(int64_t N) { return (int)((N + kSpBN - 1) / kSpBN); }
 
+int s8_ws_splits(int64_t M, int64_t N, int64_t K) {
+  if (M <= 128 || N < 4 || K < 1 || N % 4 || knob(kKnobS8Tile) || knob(kKnobS8Kind) ||
+      knob(kKnobS8Force))
+    return 1;
+  if (M * K >= (int64_t)kOobOffset || N * K >= (int64_t)kOobOffset) return 1;
+  const int64_t t256 = ((M + 255) / 256) * ((N + 127) / 128);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (t256 > 128 || t128 >= 256) return 1;
+  const int64_t nk = (K + kWsBK - 1) / kWsBK;
+  const int64_t sp = std::min<int64_t>(std::min<int64_t>(8, 256 / t128), nk / 8);
+  return sp >= 2 ? (int)sp : 1;
+}
+
 size_t s8_split_bytes(int64_t M, int64_t K, int64_t N) {
+  if (M > 128) {
+    const int sp = s8_ws_splits(M, N, K);
+    return sp > 1 ? ((size_t)sp * (size_t)M * (size_t)N * 4 + 255) & ~(size_t)255 : 0;
+  }
   if (!s8_split_shape(M, K, N)) return 0;
   const size_t tiles = (size_t)s8_split_counters(N);
   return tiles * 2 * kSpPart * 4 + ((tiles * 4 + 255) & ~(size_t)255);
@@ -2144,7 +2212,15 @@ hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s) {
       // 40.3 / 38.1 / 39.9 -> 38.6 / 27.0 / 32.7, 6144 x 4096 at M = 256 /
       // 512 36.9 / 38.0 -> 26.0 / 28.4; more tiles keep 256 x 128: 11008 x
       // 4096 at M = 512 39.0 against 47.1)
-      if (!tile && t256 <= 128) return launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s);
+      if (!tile && t256 <= 128) {
+        // and, when the workspace holds the partials, a K split
+        if (a.gemm_splits > 1 && a.split_part && !a.split_cnt && knob(kKnobWoqDebug))
+          std::fprintf(stderr, "[zt] s8 ws M=%lld N=%lld K=%lld: 128x128 tiles, %d K splits\n",
+                       (long long)a.M, (long long)a.N, (long long)a.K, a.gemm_splits);
+        return a.gemm_splits > 1 && !a.split_cnt
+                   ? launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s, a.gemm_splits)
+                   : launch_s8_ws<128, 128, 2, 2, 4, 3>(a, s);
+      }
       // 256 x 192 tiles (six compute waves of 128 x 64, two load waves, two
       // stages) where they make one round and 256 x 128 tiles do not: QKV at
       // M = 2048, 256 against 384 tiles, 69 -> 58.5 us

@@ -2940,7 +2940,7 @@ hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *worksp
 // below half a round of 256 x 128 tiles) make less than one round: up to 8,
 // about two workgroups per CU, at least 16 steps of 64 each (1 = no split)
 int woq_gemm_splits(int64_t M, int64_t N, int64_t K) {
-  if (knob(kKnobWoqGemm)) return 1;
+  if (M < 1 || N < 1 || K < 1 || knob(kKnobWoqGemm)) return 1;
   const int64_t t256 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   if (t256 >= 128 || t128 >= 256) return 1;

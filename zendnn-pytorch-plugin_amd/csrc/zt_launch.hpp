@@ -114,9 +114,12 @@ struct DynArgs {
   const int32_t *out_zp;
   // split-K exchange of s8_splitk_kernel (both null: not used): int32
   // partials of both K halves of every tile, then one counter per tile that
-  // the quantise kernel of the same call clears
+  // the quantise kernel of the same call clears.  Past 128 tokens,
+  // split_part with gemm_splits > 1 holds the tiled GEMM's int32 partials
+  // [gemm_splits][M][N] instead (no counters).
   int32_t *split_part;
   int32_t *split_cnt;
+  int gemm_splits;
 };
 
 // frag: write qx in the fragment order (K % 64 == 0; the buffer holds
@@ -142,6 +145,9 @@ bool s8_frag_ok(const DynArgs &a);
 // shape s8_splitk_kernel takes (0 otherwise), and its tile-counter count;
 // the counters follow split_bytes - 4 * counters bytes of partials.
 size_t s8_split_bytes(int64_t M, int64_t K, int64_t N);
+// K splits of the tiled int8 GEMM past 128 tokens when its 128 x 128 tiles
+// make less than one round (1 = none)
+int s8_ws_splits(int64_t M, int64_t N, int64_t K);
 int s8_split_counters(int64_t N);
 hipError_t launch_s8_gemm(const DynArgs &a, hipStream_t s);
 // The 16-token skinny GEMM with the per-token quantisation in its prologue
