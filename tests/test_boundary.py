@@ -94,6 +94,11 @@ def test_c_abi_validates_without_gpu():
     # the WOQ kernels reduce K inside a workgroup: no device workspace
     assert L.zt_woq_linear_workspace_size(16, 14336, 4096, 112) == 0
     assert L.zt_woq_linear_workspace_size(2048, 4096, 4096, 32) == 0
+    # up to 16 rows a shape without a stream-kernel x layout takes the wide
+    # kernel, whose K splits keep fp32 partials [splits][M][N] (4096 x 11008
+    # at M = 16: 43 phases in 6 splits of 8); with a layout it needs none
+    assert L.zt_woq_linear_workspace_size(16, 11008, 4096, 86) == 6 * 16 * 4096 * 4
+    assert L.zt_woq_linear_workspace_size(14, 11008, 4096, 86) == 0
     # prefill GEMMs whose tiles make less than one round split K: fp32 (int4)
     # or int32 (int8) partials [splits][M][N] follow the base workspace
     assert L.zt_woq_linear_workspace_size(512, 4096, 4096, 32) == 4 * 512 * 4096 * 4

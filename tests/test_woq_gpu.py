@@ -151,6 +151,35 @@ def test_wide_kernel_default_past_one_round(M, knobs, capfd):
     assert "woq wide" in capfd.readouterr().err
 
 
+# Up to 16 rows the wide kernel takes the calls for which the stream kernel
+# has no x layout (K = 11008 at 15-16 rows: two phases do not fit the LDS and
+# 86 chunks do not split in four; K = 28672 at 11-16 rows: four phases do not
+# fit, eight have no compiled case) or whose phased grid of one workgroup per
+# CU makes more than one round (5120 rows at K = 13824 from 12 rows, 4160 at
+# K = 28672 from 4 rows)
+@pytest.mark.parametrize("M,K,N", [(15, 11008, 2048), (16, 11008, 1544), (8, 28672, 4160),
+                                   (16, 28672, 1032), (12, 13824, 5120), (6, 28672, 4160)])
+def test_wide_kernel_below_17_rows_without_stream_layout(M, K, N, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    run_case(M, K, N, K // 128, post=("add",), nbuf=1, seed=M + K, bias=True)
+    assert "woq wide" in capfd.readouterr().err
+
+
+# K = 28672 (224 chunks, 28 per wave): the lean kernel at 1-2 rows, the
+# stream kernel with x whole at 1-2 rows (lean kernel off) and in two K
+# phases at 3 rows
+@pytest.mark.parametrize("M,N,lean", [(1, 256, None), (2, 264, None), (1, 264, "0"),
+                                      (2, 256, "0"), (3, 136, None)])
+def test_28_chunks_per_wave(M, N, lean, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    if lean:
+        knobs.set("ZT_WOQ_LEAN", lean)
+    capfd.readouterr()
+    run_case(M, 28672, N, 224, post=("add",), nbuf=1, seed=M + N, bias=True)
+    assert ("woq lean" if M <= 2 and not lean else "woq stream") in capfd.readouterr().err
+
+
 # prefill GEMM with a K split: when its 128 x 128 tiles make less than one
 # round (65..~500 rows on small matrices) the workgroups write fp32 partials
 # of whole 64-k step ranges into the workspace and the reduce kernel adds

@@ -2222,7 +2222,7 @@ static bool lean_preferred(const WoqArgs &a, int gu) {
 }
 
 // The lean kernel where it applies: fast mode, bf16 x with 16-byte rows,
-// M <= 16, K = 8 waves x CPW chunks (CPW 2, 4, 8 or 14), x within the LDS,
+// M <= 16, K = 8 waves x CPW chunks (CPW 2, 4, 8, 14 or 28), x within the LDS,
 // the index ranges within 32-bit buffer offsets; gu > 0 is the merged
 // gate_up (I = gu, a multiple of 16).
 static bool try_launch_lean(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
@@ -2250,7 +2250,7 @@ static bool try_launch_lean(const WoqArgs &a, hipStream_t s, int shift, int gmas
                    : launch_lean_t<8, CPW_, 1>(a, s, shift, gmask, gu);            \
     return true;                                                                   \
   }
-  ZT_LEAN_CASE(2) ZT_LEAN_CASE(4) ZT_LEAN_CASE(8) ZT_LEAN_CASE(14)
+  ZT_LEAN_CASE(2) ZT_LEAN_CASE(4) ZT_LEAN_CASE(8) ZT_LEAN_CASE(14) ZT_LEAN_CASE(28)
 #undef ZT_LEAN_CASE
   return false;
 }
@@ -2259,17 +2259,21 @@ static bool try_launch_lean(const WoqArgs &a, hipStream_t s, int shift, int gmas
 // in the fast mode, a 2-, 4- or 8-phase range of it) in at most
 // kStreamLdsMax of LDS.  Returns false when the caller should use another
 // kernel.
+// With plan_p set nothing is launched: the function returns whether the
+// stream kernel itself has a layout for the call and sets *plan_p to its
+// K phase count (1: x whole in LDS).
 static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gmask, int mode,
-                              hipError_t *err) {
+                              hipError_t *err, int *plan_p = nullptr) {
   const int C = (int)(a.K / 128);
   const int tiles = (int)((a.N + 15) / 16);
   if (a.M > 64) return false;
   // the fast mode moves the scales by 4-byte DMA, aligned for even N; odd
   // N take the general bf16-scale mode (same weights, same results)
   if (mode == kDecFast && a.N % 2 != 0) mode = kDecGenBf16;
-  if (!knob(kKnobWoqStream) && try_launch_lean(a, s, shift, gmask, mode, 0, err)) return true;
-  if (!knob(kKnobWoqStream) && try_launch_persist(a, s, shift, gmask, mode, 0, err)) return true;
-  if (!knob(kKnobWoqStream) && try_launch_wave(a, s, shift, gmask, mode, 0, err)) return true;
+  const bool others = !plan_p && !knob(kKnobWoqStream);
+  if (others && try_launch_lean(a, s, shift, gmask, mode, 0, err)) return true;
+  if (others && try_launch_persist(a, s, shift, gmask, mode, 0, err)) return true;
+  if (others && try_launch_wave(a, s, shift, gmask, mode, 0, err)) return true;
   // measured on MI355X (graph-replayed Llama shapes): 8 waves of few chunks
   // each, two tiles per wave once there are two rounds of tiles, or more
   // tiles than CUs when x takes most of the LDS (one workgroup per CU)
@@ -2295,17 +2299,19 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
       const int cp = C / p;
       if (C % p || (p > 1 && !stream_x_dma(a, p)) || !fits(p)) continue;
       const int cpw_need = p * ((cp + 7) / 8);  // chunks per wave over all phases
-      if (knob(kKnobWoqDebug))
+      if (knob(kKnobWoqDebug) && !plan_p)
         std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: MT=%d P=%d CPW>=%d\n",
                      (long long)a.M, (long long)a.N, (long long)a.K, mt, p, cpw_need);
 #define ZT_STREAM_PCASE(CPW_, P_, MT_)                                          \
   if (mt == MT_ && p == P_ && cpw_need <= CPW_ && CPW_ % P_ == 0) {            \
+    if (plan_p) return *plan_p = P_, true;                                      \
     *err = launch_stream_t<8, CPW_, 1, P_, MT_>(a, s, shift, gmask, mode);      \
     return true;                                                                \
   }
       // smallest CPW first, so that every wave has chunks in each phase
       ZT_STREAM_PCASE(8, 2, 1) ZT_STREAM_PCASE(14, 2, 1) ZT_STREAM_PCASE(16, 2, 1)
       ZT_STREAM_PCASE(16, 4, 1) ZT_STREAM_PCASE(20, 2, 1) ZT_STREAM_PCASE(20, 4, 1)
+      ZT_STREAM_PCASE(28, 2, 1) ZT_STREAM_PCASE(28, 4, 1)
       ZT_STREAM_PCASE(4, 1, 2) ZT_STREAM_PCASE(4, 2, 2) ZT_STREAM_PCASE(16, 4, 2)
       ZT_STREAM_PCASE(4, 1, 4) ZT_STREAM_PCASE(4, 4, 4) ZT_STREAM_PCASE(8, 8, 4)
 #undef ZT_STREAM_PCASE
@@ -2325,19 +2331,21 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     tpw = 4;
   const int need = (C + nw - 1) / nw;
   if (cpw == 0)
-    for (int c : {2, 4, 8, 12, 14, 16})
-      if (c >= need && (c != 14 || nw == 8)) { cpw = c; break; }
+    for (int c : {2, 4, 8, 12, 14, 16, 28})
+      if (c >= need && ((c != 14 && c != 28) || nw == 8)) { cpw = c; break; }
   if (cpw < need) return false;
-  if (knob(kKnobWoqDebug))
+  if (knob(kKnobWoqDebug) && !plan_p)
     std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: NW=%d CPW=%d TPW=%d\n",
                  (long long)a.M, (long long)a.N, (long long)a.K, nw, cpw, tpw);
 #define ZT_STREAM_CASE(NW_, CPW_, TPW_) \
-  if (nw == NW_ && cpw == CPW_ && tpw == TPW_) { *err = launch_stream_t<NW_, CPW_, TPW_>(a, s, shift, gmask, mode); return true; }
+  if (nw == NW_ && cpw == CPW_ && tpw == TPW_) { \
+    if (plan_p) return *plan_p = 1, true; \
+    *err = launch_stream_t<NW_, CPW_, TPW_>(a, s, shift, gmask, mode); return true; }
   ZT_STREAM_CASE(4, 2, 1) ZT_STREAM_CASE(4, 4, 1) ZT_STREAM_CASE(4, 8, 1) ZT_STREAM_CASE(4, 12, 1)
   ZT_STREAM_CASE(4, 16, 1) ZT_STREAM_CASE(4, 8, 2) ZT_STREAM_CASE(4, 4, 2) ZT_STREAM_CASE(4, 16, 2)
   ZT_STREAM_CASE(8, 4, 1) ZT_STREAM_CASE(8, 8, 1) ZT_STREAM_CASE(8, 12, 1) ZT_STREAM_CASE(8, 14, 1)
   ZT_STREAM_CASE(8, 16, 1) ZT_STREAM_CASE(8, 14, 2) ZT_STREAM_CASE(8, 2, 4) ZT_STREAM_CASE(8, 4, 4)
-  ZT_STREAM_CASE(8, 8, 4)
+  ZT_STREAM_CASE(8, 8, 4) ZT_STREAM_CASE(8, 28, 1)
   ZT_STREAM_CASE(8, 4, 2) ZT_STREAM_CASE(8, 8, 2) ZT_STREAM_CASE(8, 16, 2) ZT_STREAM_CASE(2, 16, 1)
   ZT_STREAM_CASE(16, 2, 1) ZT_STREAM_CASE(16, 2, 2) ZT_STREAM_CASE(16, 4, 1) ZT_STREAM_CASE(16, 8, 1)
 #undef ZT_STREAM_CASE
@@ -2699,6 +2707,31 @@ static void launch_wide_t(const WoqArgs &a, const WidePlan &p, dim3 grid, int sh
     woq_wide_kernel<2, true><<<grid, dim3(512), woq_wide_lds<2>(), s>>>(a, p.pps, shift, gmask, partial, gu);
 }
 
+// Whether the stream kernel takes a call of up to 16 rows of this shape
+// well (bf16 x and scales, aligned): it has a layout for x (whole in LDS, or
+// K phases with a compiled case), and in K phases its grid of one 16-row
+// tile per workgroup makes one round while x leaves room for one workgroup
+// per CU.  Measured (HIP-graph replays, one box; stream or decode kernel
+// against the wide kernel): without a layout 4096 x 11008 at M = 15 / 16
+// took 22.8 / 23.6 us against 17.2 / 17.4, 3584 x 18944 at M = 16 32.5
+// against 25.7, 8192 x 28672 at M = 9..16 57-81 against 37-39; with a
+// layout but 320 tiles on one workgroup per CU, 5120 x 13824 at M = 12 / 16
+// 27.9 / 30.8 against 25.6 / 26.2.  With a layout and one round the stream
+// kernel was faster (3584 x 18944 at M = 9..15: 17.6-20.7 against 24.9-25.6).
+static bool stream_takes_well(int64_t M, int64_t N, int64_t K, int64_t G) {
+  WoqArgs a{};
+  a.x = reinterpret_cast<const void *>(256);
+  a.w = reinterpret_cast<const uint32_t *>(256);
+  a.x_dt = ZT_DT_BF16, a.s_dt = ZT_DT_BF16, a.y_dt = ZT_DT_BF16;
+  a.M = M, a.N = N, a.K = K, a.G = G, a.ldx = K, a.ldy = N;
+  int p = 0;
+  hipError_t err = hipSuccess;
+  if (!try_launch_stream(a, nullptr, 0, 0, kDecFast, &err, &p)) return false;
+  if (p == 1) return true;
+  const bool one_per_cu = (size_t)M * stream_phase_pitch((int)(K / p)) * 2 > kStreamLdsMax / 2;
+  return !(one_per_cu && (N + 15) / 16 > 256);
+}
+
 bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   const char *e = knob(kKnobWoqWide);  // "0" disables; "KS" forces the split count
   if (e && e[0] == '0') return false;
@@ -2707,7 +2740,11 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   // faster (measured: the split-K reduce launch outweighs the x savings)
   const char *f = knob(kKnobWoqForceKernel);
   const bool forced = e || (f && !std::strcmp(f, "wide"));
-  if (M < 8 && !forced) return false;
+  // below 8 rows only from 4 rows, where the stream kernel has no good
+  // layout (measured: 8192 x 28672 at M = 4 / 6 took 35.9 / 40.8 us on the
+  // stream kernel in K phases against 35.2 / 35.2 here; at M = 1 / 2 29.0 /
+  // 32.1 against 35.2 / 34.8)
+  if (M < 8 && !forced && (M < 4 || stream_takes_well(M, N, K, G))) return false;
   // while x [M, K] leaves room for two stream-kernel workgroups per CU the
   // stream kernel is faster (measured: gate_up 28672 x 4096 at M = 8 / 9
   // takes 18.5 / 18.8 us there against 22.2 / 22.8 us here; 25.1 / 22.9 at
@@ -2752,8 +2789,10 @@ bool woq_wide_plan(int64_t M, int64_t N, int64_t K, int64_t G, WidePlan *p) {
   // at M = 12 / 16 takes 22.6 / 22.9 us here against 25.9 / 27.2 on the
   // stream kernel, while the split shapes lose the reduce launch), and only
   // with at least half a round of workgroups (a prime phase count leaves no
-  // split: 4096 x 11008 at M = 8 took 40.9 us on 32 workgroups)
-  if (M < 17 && (ks > 1 || blocks < 128) && !forced) return false;
+  // split: 4096 x 11008 at M = 8 took 40.9 us on 32 workgroups) -- unless
+  // the stream kernel has no good layout for the call (stream_takes_well)
+  if (M < 17 && (ks > 1 || blocks < 128) && !forced && stream_takes_well(M, N, K, G))
+    return false;
   p->mt = M <= 32 ? 1 : 2;
   p->splits = ks;
   p->pps = pps;
