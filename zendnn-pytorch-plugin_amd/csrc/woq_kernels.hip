@@ -2290,7 +2290,15 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
                (mode == kDecFast ? stream_scale_bytes((int)a.G, tpw) : 0) <=
            kStreamLdsMax;
   };
-  if (mt > 1 || !fits(1)) {
+  // x whole would leave room for one workgroup per CU while the grid makes
+  // more than one round: K phases first, whose smaller x range fits two or
+  // more workgroups per CU (measured: 10240 x 8192 at M = 6 / 8 took
+  // 20.4 / 21.3 us with x whole on 320 workgroups of two tiles)
+  const int tpw0 = tpw;
+  const bool prefer_phases =
+      !e && mt == 1 && mode == kDecFast && a.x_dt == ZT_DT_BF16 && fits(1) &&
+      (size_t)a.M * stream_x_pitch((int)a.K) * 2 > kStreamLdsMax / 2 && (tiles + tpw - 1) / tpw > 256;
+  if (mt > 1 || !fits(1) || prefer_phases) {
     // several token tiles or K phases: 8 waves, one tile each, fast mode,
     // the fewest phases whose x range fits
     if (e || mode != kDecFast || a.x_dt != ZT_DT_BF16) return false;
@@ -2298,6 +2306,9 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
     for (int p : {1, 2, 4, 8}) {
       const int cp = C / p;
       if (C % p || (p > 1 && !stream_x_dma(a, p)) || !fits(p)) continue;
+      if (prefer_phases &&
+          (p == 1 || (size_t)a.M * stream_phase_pitch((int)(a.K / p)) * 2 > kStreamLdsMax / 2))
+        continue;
       const int cpw_need = p * ((cp + 7) / 8);  // chunks per wave over all phases
       if (knob(kKnobWoqDebug) && !plan_p)
         std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: MT=%d P=%d CPW>=%d\n",
@@ -2316,7 +2327,8 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
       ZT_STREAM_PCASE(4, 1, 4) ZT_STREAM_PCASE(4, 4, 4) ZT_STREAM_PCASE(8, 8, 4)
 #undef ZT_STREAM_PCASE
     }
-    return false;
+    if (!prefer_phases) return false;
+    nw = 8, tpw = tpw0;  // no phase case: x whole after all
   }
   // at M <= 4 one tile per wave at any tile count (measured in HIP-graph
   // replays of the Llama-3 8B shapes: gate_up 28672 x 4096 at M = 1 takes
