@@ -31,10 +31,11 @@ def make(M, K, N, seed, x_dtype=torch.bfloat16, sw_dtype=torch.float32, bias=Tru
     return x, w, sw, b
 
 
-# long rows (7 vectors per thread), a partial last 16-byte vector per
-# thread, odd row counts
+# long rows (7, 14 and 16 vectors per thread, and past 16 the element-wise
+# kernel), a partial last 16-byte vector per thread, odd row counts
 @pytest.mark.parametrize("M,K", [(1, 4), (3, 12), (16, 16), (128, 4096), (7, 11008),
-                                 (2048, 4096), (5, 1), (1025, 14336), (3001, 2056), (1024, 8)])
+                                 (2048, 4096), (5, 1), (1025, 14336), (3001, 2056), (1024, 8),
+                                 (5, 28672), (3, 32768), (2, 32776), (9, 24584)])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
 def test_quantize_bit_exact(M, K, x_dtype):
     g = torch.Generator().manual_seed(M * 31 + K)
@@ -209,7 +210,8 @@ def test_dynamic_qlinear_fused_quantise(M, K, N, bias, knobs, capfd):
 # quantisation in the GEMM's prologue and as its own launch: all
 # bit-identical to one another and within tolerance of the oracle
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (7, 1024, 300), (16, 2048, 11008),
-                                   (2, 14336, 520), (8, 192, 36)])
+                                   (2, 14336, 520), (8, 192, 36), (4, 28672, 264),
+                                   (9, 24576, 72)])
 def test_dynamic_qlinear_skinny_tile_shapes(M, K, N, knobs):
     x, w, sw, b = make(M, K, N, seed=M * 13 + K + N)
     args = (x.to(DEV), w.to(DEV), sw.to(DEV), b.to(DEV))

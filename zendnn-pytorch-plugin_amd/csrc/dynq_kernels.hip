@@ -2069,7 +2069,10 @@ hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(qx)) & 15u) == 0;
   const int64_t per = (K / 8 + 255) / 256;  // 8-element vectors per thread
   const dim3 grid((unsigned)M), block(256);
-  if (vec && per <= 8) {
+  // up to 16 vectors per thread (K <= 32768); longer rows take the
+  // element-wise kernel (measured: at K = 28672 the element-wise kernel made
+  // the op at M = 3..5, N = 8192 take 113-114 us)
+  if (vec && per <= 16) {
     const uint16_t *xb = static_cast<const uint16_t *>(x);
 #define ZT_QB(V_)                                                                          \
   if (per <= V_) {                                                                         \
@@ -2081,7 +2084,7 @@ hipError_t launch_dyn_quantize(const void *x, int x_dt, int64_t M, int64_t K,
            : dyn_quantize_bf16_kernel<V_, false, false><<<grid, block, 0, s>>>(xb, K, qx, sx, azp, zero, nzero); \
     return hipGetLastError();                                                              \
   }
-    ZT_QB(2) ZT_QB(4) ZT_QB(8)
+    ZT_QB(2) ZT_QB(4) ZT_QB(8) ZT_QB(16)
 #undef ZT_QB
   }
   if (azp)
