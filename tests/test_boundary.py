@@ -103,6 +103,8 @@ def test_c_abi_validates_without_gpu():
     # or int32 (int8) partials [splits][M][N] follow the base workspace
     assert L.zt_woq_linear_workspace_size(512, 4096, 4096, 32) == 4 * 512 * 4096 * 4
     assert L.zt_woq_linear_workspace_size(128, 11008, 4096, 86) == 8 * 128 * 4096 * 4
+    # exactly half a round of 256 x 128 tiles (128) splits too: 2 ways
+    assert L.zt_woq_linear_workspace_size(512, 8192, 8192, 64) == 2 * 512 * 8192 * 4
     assert L.zt_dynamic_qlinear_workspace_size(512, 4096, 4096) >= \
         L.zt_dynamic_qlinear_workspace_size(512, 4096, 0) + 2 * 512 * 4096 * 4
     # empty sizes (N = 0 asks for the least workspace) plan no split

@@ -186,7 +186,8 @@ def test_28_chunks_per_wave(M, N, lean, knobs, capfd):
 # them in split order and applies bias and post-ops
 @pytest.mark.parametrize("M,K,N,post,nbuf", [(65, 4096, 264, (), 0), (128, 11008, 256, ("add",), 1),
                                              (300, 2048, 512, ("gelu_tanh",), 0),
-                                             (512, 8192, 136, ("mul", "add"), 2)])
+                                             (512, 8192, 136, ("mul", "add"), 2),
+                                             (256, 2048, 16384, (), 0)])
 def test_gemm32_kernel_k_split(M, K, N, post, nbuf, knobs, capfd):
     knobs.set("ZT_WOQ_DEBUG", "1")
     capfd.readouterr()

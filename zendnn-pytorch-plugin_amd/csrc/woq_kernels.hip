@@ -2988,13 +2988,13 @@ hipError_t launch_woq_decode(const WoqArgs &a, const DecodePlan &p, void *worksp
 }
 
 // K splits of the prefill GEMM when its 128 x 128 tiles (the tile it takes
-// below half a round of 256 x 128 tiles) make less than one round: up to 8,
-// about two workgroups per CU, at least 16 steps of 64 each (1 = no split)
+// at half a round of 256 x 128 tiles or less) make at most one round: up to
+// 8, about two workgroups per CU, at least 16 steps of 64 each (1 = no split)
 int woq_gemm_splits(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || K < 1 || knob(kKnobWoqGemm)) return 1;
   const int64_t t256 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (t256 >= 128 || t128 >= 256) return 1;
+  if (t256 > 128 || t128 > 256) return 1;
   const int64_t sp = std::min<int64_t>(std::min<int64_t>(8, 512 / t128), (K / kW32BK) / 16);
   return sp >= 2 ? (int)sp : 1;
 }
@@ -3029,14 +3029,17 @@ hipError_t launch_woq_gemm(const WoqArgs &a, hipStream_t s, void *workspace, siz
       // 16-byte pieces
       if (mode == kDecFast && a.N % 8 == 0 && !(e && e[0] == 'd') &&
           (int64_t)a.G * a.N * 2 < (int64_t)kOobOffset) {
-        // one round of 256 x 128 tiles (at most one per CU): the load-wave
-        // kernel, whose deeper prefetch is then not paid for by an epilogue
-        // that a second workgroup per CU would hide (O and down at M = 2048:
-        // 104 -> 81 and 327 -> 255 us); when 256 x 192 tiles make one round
-        // where 256 x 128 do not, those (QKV: 152 -> 112 us); more rounds:
-        // two workgroups per CU (gate_up 508 against 549 us with 256 x 128)
-        const bool big32 = e ? e[0] != '1' : t256 >= 128;
-        const bool ws = e ? e[0] == 'w' || e[0] == 'v' : t256 >= 128 && t256 <= 256;
+        // one round of 256 x 128 tiles (at most one per CU, more than half
+        // of them): the load-wave kernel, whose deeper prefetch is then not
+        // paid for by an epilogue that a second workgroup per CU would hide
+        // (O and down at M = 2048: 104 -> 81 and 327 -> 255 us); when 256 x
+        // 192 tiles make one round where 256 x 128 do not, those (QKV: 152 ->
+        // 112 us); more rounds: two workgroups per CU (gate_up 508 against 549
+        // us with 256 x 128).  At half a round or less the split path below
+        // (8192 x 8192 / 8192 x 28672 at M = 384: 106.8 / 338 us on 128
+        // load-wave tiles, 87.0 / 265 split in two)
+        const bool big32 = e ? e[0] != '1' : t256 > 128;
+        const bool ws = e ? e[0] == 'w' || e[0] == 'v' : t256 > 128 && t256 <= 256;
         const int64_t t192 = ((a.M + 255) / 256) * ((a.N + 191) / 192);
         const bool ws192 = e ? e[0] == 'x' : t256 > 256 && t192 <= 256;
         if (ws192) return launch_woq_gemm_ws_t<256, 192, 3>(a, s, shift, gmask);
