@@ -2309,6 +2309,15 @@ static bool try_launch_stream(const WoqArgs &a, hipStream_t s, int shift, int gm
       if (prefer_phases &&
           (p == 1 || (size_t)a.M * stream_phase_pitch((int)(a.K / p)) * 2 > kStreamLdsMax / 2))
         continue;
+      // two phases that leave room for one workgroup per CU under more than
+      // a round of tiles: four when they fit two per CU and have a case
+      // (cpw_need <= 28 below)
+      auto half_x = [&](int q) {
+        return (size_t)a.M * stream_phase_pitch((int)(a.K / q)) * 2 <= kStreamLdsMax / 2;
+      };
+      if (p == 2 && mt == 1 && tiles > 256 && !half_x(2) && C % 4 == 0 && stream_x_dma(a, 4) &&
+          fits(4) && half_x(4) && 4 * ((C / 4 + 7) / 8) <= 28)
+        continue;
       const int cpw_need = p * ((cp + 7) / 8);  // chunks per wave over all phases
       if (knob(kKnobWoqDebug) && !plan_p)
         std::fprintf(stderr, "[zt] woq stream M=%lld N=%lld K=%lld: MT=%d P=%d CPW>=%d\n",
