@@ -166,6 +166,17 @@ def test_wide_kernel_below_17_rows_without_stream_layout(M, K, N, knobs, capfd):
     assert "woq wide" in capfd.readouterr().err
 
 
+# past a round of workgroups the stream kernel takes K phases that fit two
+# workgroups per CU: two phases instead of x whole (6 rows, 520 tiles two
+# per workgroup), four instead of two (10 rows, 260 tiles)
+@pytest.mark.parametrize("M,N,P", [(6, 8320, 2), (10, 4160, 4)])
+def test_stream_kernel_phase_preference(M, N, P, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    run_case(M, 8192, N, 64, post=("add",), nbuf=1, seed=M + N, bias=True)
+    assert f"P={P} " in capfd.readouterr().err
+
+
 # K = 28672 (224 chunks, 28 per wave): the lean kernel at 1-2 rows, the
 # stream kernel with x whole at 1-2 rows (lean kernel off) and in two K
 # phases at 3 rows
