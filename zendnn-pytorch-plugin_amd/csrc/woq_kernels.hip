@@ -2215,7 +2215,10 @@ static hipError_t launch_lean_t(const WoqArgs &a, hipStream_t s, int shift, int 
 // faster (M = 3 / 4: 16.6 / 16.4 against 17.3 / 18.2 here).  QKV and most
 // shapes at M = 8 stay where they are (2-43 % slower on the lean kernel).
 static bool lean_preferred(const WoqArgs &a, int gu) {
-  if (gu) return a.M <= 2;
+  // the merged gate_up: 1-2 rows; at K = 8192, where the persistent kernel
+  // has no register budget, up to 4 (57344 x 8192 at M = 4: 60.2 us against
+  // 65.0 on the wave kernel)
+  if (gu) return a.M <= 2 || (a.M <= 4 && a.K >= 8192);
   if (a.K >= 8192) return a.M <= 4;
   if (a.N > 8192) return a.M <= 2 || (a.N >= 28672 && a.M >= 12);
   return false;
