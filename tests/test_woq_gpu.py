@@ -354,6 +354,17 @@ def test_gate_up_wide_llama(M):
     run_gate_up(M, 4096, 14336, 32, seed=M)
 
 
+# 8-16 rows whose x leaves the stream kernel one workgroup per CU (K = 5120,
+# where the persistent kernel has no case): the wide kernel's merged form
+# when it takes the call in one launch
+@pytest.mark.parametrize("M", [8, 14])
+def test_gate_up_wide_below_17_rows(M, knobs, capfd):
+    knobs.set("ZT_WOQ_DEBUG", "1")
+    capfd.readouterr()
+    run_gate_up(M, 5120, 8192, 40, seed=M)
+    assert "woq wide gate_up" in capfd.readouterr().err
+
+
 def test_gate_up_torch_op():
     import zentorch  # noqa: F401
     M, K, I, G = 4, 1024, 128, 8

@@ -2911,6 +2911,12 @@ bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
     return true;
   const int C = (int)(a.K / 128), tiles = (int)(a.N / 16);
   const size_t x_bytes = (size_t)a.M * stream_x_pitch((int)a.K) * 2;
+  // x leaving room for one workgroup per CU: the wide kernel's merged form
+  // when it takes the call in one launch (woq_try_wide_gate_up)
+  if (!knob(kKnobWoqStream) && x_bytes > 76 * 1024 && a.post.count == 0 && a.N % 128 == 0) {
+    WidePlan wp;
+    if (woq_wide_ok(a, &wp) && wp.splits == 1) return false;
+  }
   // as the plain stream kernel: four tiles (two pairs) per wave once x
   // takes a CU's LDS and there are enough tiles, else one pair
   const int tpw = x_bytes > 76 * 1024 && tiles >= 800 ? 4 : 2;
