@@ -99,8 +99,10 @@ int zt_woq_linear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
 
 /* Bytes of device workspace zt_woq_linear needs for these sizes.  Calls that
  * split K over several workgroups keep fp32 partials [splits][M][N] there
- * (no initial contents needed): 17..64 rows on large matrices, and prefill
- * calls whose row tiles make less than one round of the GPU (a smaller
+ * (no initial contents needed): 17..64 rows on large matrices (and from 4
+ * rows where the decode kernels have no good layout for x, e.g. K = 11008
+ * at 15-16 rows; a smaller workspace is refused for these), and prefill
+ * calls whose row tiles make at most one round of the GPU (a smaller
  * workspace runs those unsplit); other sizes need none (0).  Calls that
  * overlap in time must not share a workspace. */
 size_t zt_woq_linear_workspace_size(int64_t M, int64_t K, int64_t N,
@@ -150,10 +152,12 @@ size_t zt_woq_linear_gate_up_workspace_size(int64_t M, int64_t K, int64_t N,
  *  y        [M, N] in y_dtype
  *  workspace: zt_dynamic_qlinear_workspace_size(M, K, N) bytes.  Its first
  *           part holds the quantised activations and row scales; the rest
- *           (for 64 < M <= 128, K % 256 == 0) holds the exchange of the
- *           split-K GEMM.  A workspace holding only the first part
- *           (zt_dynamic_qlinear_workspace_size(M, K, 0)) is accepted and runs
- *           the unsplit kernel, with the same results.
+ *           holds the exchange of the split-K GEMM (64 < M <= 128,
+ *           K % 256 == 0) or, past 128 rows when the tiled GEMM's tiles make
+ *           less than one round, its int32 K-split partials.  A workspace
+ *           holding only the first part (zt_dynamic_qlinear_workspace_size(M,
+ *           K, 0)) is accepted and runs the unsplit kernels, with the same
+ *           results.
  */
 int zt_dynamic_qlinear(const void *x, int32_t x_dtype, int64_t M, int64_t K,
                        const int8_t *w, int64_t N, const void *w_scales,
