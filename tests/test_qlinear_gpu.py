@@ -123,7 +123,10 @@ def test_qlinear_out_forms(variant):
                                    (5, 33, 12),
                                    # 216 tiles of 256 x 192: requantised outputs
                                    # through the half-tile epilogue
-                                   (2100, 4608, 272)])
+                                   (2100, 4608, 272),
+                                   # 16 tiles of 128 x 128: K split in four over
+                                   # int32 partials, outputs from the sum kernel
+                                   (200, 1024, 4096)])
 @pytest.mark.parametrize("kind", ["u8_in_u8_out", "f32_zp_s8_out", "bf16_sym_bf16_out"])
 def test_qlinear_kernels(M, N, K, kind):
     in_dtype = {"u8_in_u8_out": torch.uint8, "f32_zp_s8_out": torch.float32,
