@@ -354,15 +354,18 @@ def test_gate_up_wide_llama(M):
     run_gate_up(M, 4096, 14336, 32, seed=M)
 
 
-# 8-16 rows whose x leaves the stream kernel one workgroup per CU (K = 5120,
-# where the persistent kernel has no case): the wide kernel's merged form
-# when it takes the call in one launch
-@pytest.mark.parametrize("M", [8, 14])
-def test_gate_up_wide_below_17_rows(M, knobs, capfd):
+# 8-16 rows whose x leaves the stream kernel one workgroup per CU over more
+# than a round of workgroups (K = 5120, where the persistent kernel has no
+# case; 258 workgroups of two gate/up tile pairs): the wide kernel's merged
+# form when it takes the call in one launch.  With one round (I = 8192) the
+# stream kernel keeps it.
+@pytest.mark.parametrize("M,I,kernel", [(8, 8256, "woq wide gate_up"), (14, 8256, "woq wide gate_up"),
+                                        (14, 8192, "woq gate_up stream")])
+def test_gate_up_wide_below_17_rows(M, I, kernel, knobs, capfd):
     knobs.set("ZT_WOQ_DEBUG", "1")
     capfd.readouterr()
-    run_gate_up(M, 5120, 8192, 40, seed=M)
-    assert "woq wide gate_up" in capfd.readouterr().err
+    run_gate_up(M, 5120, I, 40, seed=M)
+    assert kernel in capfd.readouterr().err
 
 
 def test_gate_up_torch_op():

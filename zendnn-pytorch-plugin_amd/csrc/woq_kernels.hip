@@ -2911,15 +2911,19 @@ bool woq_try_stream_gate_up(const WoqArgs &a, hipStream_t s, hipError_t *err) {
     return true;
   const int C = (int)(a.K / 128), tiles = (int)(a.N / 16);
   const size_t x_bytes = (size_t)a.M * stream_x_pitch((int)a.K) * 2;
-  // x leaving room for one workgroup per CU: the wide kernel's merged form
-  // when it takes the call in one launch (woq_try_wide_gate_up)
-  if (!knob(kKnobWoqStream) && x_bytes > 76 * 1024 && a.post.count == 0 && a.N % 128 == 0) {
-    WidePlan wp;
-    if (woq_wide_ok(a, &wp) && wp.splits == 1) return false;
-  }
   // as the plain stream kernel: four tiles (two pairs) per wave once x
   // takes a CU's LDS and there are enough tiles, else one pair
   const int tpw = x_bytes > 76 * 1024 && tiles >= 800 ? 4 : 2;
+  // x leaving room for one workgroup per CU over more than a round of
+  // workgroups: the wide kernel's merged form when it takes the call in one
+  // launch (woq_try_wide_gate_up).  Measured: 27648 x 5120 at M = 10 / 12
+  // took 29.3 / 30.2 us here against 25.2 / 24.9 there; 16384 x 3072 at
+  // M = 16 (one round here, half a round there) 12.2 against 16.2
+  if (!knob(kKnobWoqStream) && x_bytes > 76 * 1024 && a.post.count == 0 && a.N % 128 == 0 &&
+      (I / 16 + tpw / 2 - 1) / (tpw / 2) > 256) {
+    WidePlan wp;
+    if (woq_wide_ok(a, &wp) && wp.splits == 1) return false;
+  }
   const size_t lds = stream_scale_offset(stream_slab_bytes(8, tpw, 1), x_bytes) +
                      stream_scale_bytes((int)a.G, tpw);
   if (lds > kStreamLdsMax) return false;
