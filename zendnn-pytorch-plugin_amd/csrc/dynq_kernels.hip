@@ -1959,12 +1959,14 @@ hipError_t launch_s8_skinny(const DynArgs &a, hipStream_t s) {
   } else if (mt == 1) {
     // one token tile: 16-row weight tiles, as many workgroups as CUs or
     // more, except 32-row tiles from 4097 to 8192 rows and 64-row tiles
-    // past 16384 (graph replays over rotating weights, M = 1..16, one box:
+    // past 12288 (graph replays over rotating weights, M = 1..16, one box:
     // at M = 1 O 4096 x 4096 18.1 -> 11.0 us, down 4096 x 14336 44.9 ->
     // 20.3, QKV 6144 x 4096 18.7 -> 13.8, 11008 x 4096 20.4 -> 17.8, all
     // against 64-row tiles; gate_up 28672 x 4096 keeps them, 37.4 against
-    // 40.2 with 16-row tiles at M = 8)
-    tpw = a.N > 16384 ? 4 : (a.N > 4096 && a.N <= 8192) ? 2 : 1;
+    // 40.2 with 16-row tiles at M = 8; at M = 9 / 16 14336 x 4096 22.3 /
+    // 23.2 against 23.5 / 26.3 with 16-row tiles, 16384 x 3072 19.2 / 19.8
+    // against 20.2 / 22.5)
+    tpw = a.N > 12288 ? 4 : (a.N > 4096 && a.N <= 8192) ? 2 : 1;
     pf = 4, nw = 8;
   }
 #define ZT_SK(MT_, TPW_, PF_, NW_)                                            \
