@@ -182,13 +182,14 @@ def test_dynamic_qlinear_fragment_kernel_default_tiles(M, N, K, knobs):
 # The skinny GEMM with the per-token quantisation in its prologue (one
 # launch for at most 16 tokens of bf16 x): bit-identical to the quantise
 # launch + skinny GEMM (the same qx, sx and int32 sums) for every register
-# layout it has (1, 2, 4 and 8 vectors per thread and row), ragged N and K,
+# layout it has (1, 2, 4 and 8 vectors per thread and row, 2 to 16 rows), ragged N and K,
 # with and without bias.  ZT_WOQ_DEBUG names the kernel that ran.
 @pytest.mark.parametrize("M,K,N", [(1, 64, 8), (2, 4096, 11008), (3, 192, 70), (5, 4096, 6144),
                                    (8, 4096, 4096), (9, 4096, 200), (16, 4096, 136),
                                    (4, 8192, 300), (3, 5120, 77), (2, 14336, 4096),
                                    (1, 16384, 64), (4, 4096, 28672), (1, 28672, 8192),
-                                   (2, 24640, 130), (2, 32768, 72)])
+                                   (2, 24640, 130), (2, 32768, 72), (3, 14336, 4096),
+                                   (3, 11008, 136)])
 @pytest.mark.parametrize("bias", [True, False])
 def test_dynamic_qlinear_fused_quantise(M, K, N, bias, knobs, capfd):
     x, w, sw, b = make(M, K, N, seed=M * 31 + K + N, bias=bias)

@@ -2026,7 +2026,10 @@ bool s8_fused_ok(const DynArgs &a) {
     return false;
   if (a.N * a.K >= (int64_t)kOobOffset || a.M * a.K * 2 >= (int64_t)kOobOffset) return false;
   const int vr = s8_fused_vr(a.K);
-  const int64_t rm = vr == 1 ? 16 : vr == 2 ? 4 : vr <= 8 ? 2 : 0;
+  // rows the fused form takes per register layout; at 3-4 vectors per row
+  // three (four rows held as 4 x 4 vectors measured 1-4 % slower than two
+  // launches at M = 4 on 8192 x 16384, 6-10 % faster at M = 3)
+  const int64_t rm = vr <= 1 ? 16 : vr <= 2 ? 4 : vr <= 4 ? 3 : vr <= 8 ? 2 : 0;
   if (a.M > rm || s8_fused_lds(a.M, a.K, 4) > 160 * 1024) return false;
   return (e && e[0] == '1') || a.M <= kS8FusedRows;
 }
@@ -2037,7 +2040,8 @@ hipError_t launch_s8_skinny_fused_tp(const DynArgs &a, hipStream_t s) {
   if (vr == 1) return a.M <= 8 ? launch_s8_skinny_fused_t<TPW, PF, 8, 1>(a, s)
                                : launch_s8_skinny_fused_t<TPW, PF, 16, 1>(a, s);
   if (vr == 2) return launch_s8_skinny_fused_t<TPW, PF, 4, 2>(a, s);
-  if (vr <= 4) return launch_s8_skinny_fused_t<TPW, PF, 2, 4>(a, s);
+  if (vr <= 4) return a.M <= 2 ? launch_s8_skinny_fused_t<TPW, PF, 2, 4>(a, s)
+                               : launch_s8_skinny_fused_t<TPW, PF, 4, 4>(a, s);
   return launch_s8_skinny_fused_t<TPW, PF, 2, 8>(a, s);
 }
 
